@@ -1,0 +1,161 @@
+/*
+ * pyodide_llm_hip.h — the C ABI of the MI355X forward engine for pyodide-llm's quantized matmul path.
+ *
+ * The engine replaces the object public/forward.js:createForward returns (public/forward.js:1676-1955) for the
+ * int8 / int6 Llama and Qwen2 forms. Every entry point takes plain pointers and sizes; device pointers are `void *`
+ * and streams are `void *` (a hipStream_t, NULL = the engine's own stream). Every function returns 0 on success or a
+ * negative HE_E* code; he_last_error() then names what failed (a thread-local string).
+ *
+ * Weights are the checkpoint's own bytes as quantize.py writes them (quantize.py:22-40, the tensor order of
+ * public/llama2_convert.py:32-83): an int8 matrix is its int8 values [rows][K] followed by one float32 scale per group
+ * of 32 [rows][K/32]; an int6 matrix packs every group into 24 bytes (public/llama2_numpy.py:678-692). The engine
+ * uploads those bytes unchanged and addresses every tensor by the offsets the caller's plan gives
+ * (public/llama2_numpy.py:751-795, Tensor.plan()).
+ *
+ * Arithmetic is the reference's CPU path to the bit: activations quantized per group of 32 (kernels/kernel.ts:129-156),
+ * exact int32 group sums, and the float32 order of kernels/kernel_relaxed.ts:34-67 (bias 64) or kernels/kernel.ts:
+ * 231-258 (bias 0), rmsnorm/rope/attention/swiglu in the order of kernels/kernel.ts.
+ */
+#ifndef PYODIDE_LLM_HIP_H
+#define PYODIDE_LLM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ---- */
+#define HE_OK 0
+#define HE_E_ARG -1      /* an argument is outside what the engine or the kernel takes */
+#define HE_E_HIP -2      /* a HIP call failed (no device, out of memory, a launch failure) */
+#define HE_E_STATE -3    /* the call does not fit the engine's state (a position past the context, ...) */
+#define HE_E_NOTFINITE -4 /* greedy decoding met logits whose largest value is not finite (llama2_numpy.NOT_FINITE) */
+
+/* The model: the fields of `plan` (public/llama2_numpy.py:1261-1270) the Llama/Qwen2 forward reads. */
+typedef struct he_config {
+  int32_t dim;               /* plan.dim */
+  int32_t hidden_dim;        /* plan.hidden_dim */
+  int32_t n_layers;          /* plan.n_layers */
+  int32_t n_heads;           /* plan.n_heads */
+  int32_t n_kv_heads;        /* plan.n_kv_heads */
+  int32_t head_size;         /* plan.head_size */
+  int32_t vocab_size;        /* plan.vocab_size (positive) */
+  int32_t seq_len;           /* plan.seq_len: the context, and the rows of the RoPE tables */
+  int32_t shared_classifier; /* plan.shared_classifier: wcls is token_embedding_table */
+  int32_t six;               /* the matrices are int6 (Tensor kind "int6"), else int8 */
+  int32_t qkv_bias;          /* Qwen2: bq, bk, bv are added after the q, k, v matmuls (public/forward.js:1038-1042) */
+  int32_t relaxed;           /* 1: activations with bias 64, matmul_q8r order; 0: bias 0, matmul_q8 lane order */
+  int32_t half_kv;           /* keys and values kept in float16 (public/forward.js:762, kernels/kernel.ts:570-608) */
+  float rms_norm_eps;        /* plan.rms_norm_eps */
+} he_config;
+
+/* Where a tensor is: byte offsets from the start of the checkpoint (Tensor.offset, Tensor.scales). */
+typedef struct he_tensor {
+  int64_t offset;
+  int64_t scales; /* matrices only; 0 for float32 vectors */
+} he_tensor;
+
+/* The order of he_tensor arrays: the names of public/llama2_numpy.py TENSOR_NAMES the forward reads. */
+enum {
+  HE_T_EMBEDDING = 0, /* token_embedding_table [vocab][dim], int8 or int6 */
+  HE_T_RMS_ATT,       /* rms_att_weight [layers][dim] f32 */
+  HE_T_WQ,            /* wq [layers][n_heads*head_size][dim] */
+  HE_T_WK,            /* wk [layers][kv_dim][dim] */
+  HE_T_WV,            /* wv [layers][kv_dim][dim] */
+  HE_T_WO,            /* wo [layers][dim][n_heads*head_size] */
+  HE_T_RMS_FFN,       /* rms_ffn_weight [layers][dim] f32 */
+  HE_T_W1,            /* w1 [layers][hidden][dim] */
+  HE_T_W2,            /* w2 [layers][dim][hidden] */
+  HE_T_W3,            /* w3 [layers][hidden][dim] */
+  HE_T_RMS_FINAL,     /* rms_final_weight [dim] f32 */
+  HE_T_WCLS,          /* wcls [vocab][dim] (the embedding's offsets when shared) */
+  HE_T_BQ,            /* bq [layers][q_dim] f32 (qkv_bias) */
+  HE_T_BK,            /* bk [layers][kv_dim] f32 */
+  HE_T_BV,            /* bv [layers][kv_dim] f32 */
+  HE_T_COUNT
+};
+
+typedef struct he_engine he_engine;
+
+/* the message of the last failed call on this thread ("" if none) */
+const char *he_last_error(void);
+
+/* ---- the engine: public/forward.js external().start(plan) and the object it returns ---- */
+
+/* start(plan) (public/forward.js:571-590, createForward :626): uploads `size` bytes of checkpoint (host memory) to the
+ * device, the RoPE tables plan.derived.freq_cis_real/imag ([seq_len][head_size/2] float32, host), and makes the
+ * KV cache for the whole context. max_block: the most tokens one he_forward_many call takes (promptBlock). */
+int32_t he_open(const he_config *cfg, const he_tensor *tensors, const void *checkpoint, uint64_t size,
+                const float *rope_cos, const float *rope_sin, int32_t max_block, he_engine **out);
+
+/* The same, with the checkpoint made on the device from a seed rather than uploaded: every matrix N(0, 0.02) by a
+ * counter-based generator (a splitmix64 hash of (seed, tensor, index) whose four 16-bit quarters are summed: a
+ * scaled Irwin-Hall(4) variate, so that host and device make the same float32 bits), quantized by the reference's
+ * quantize()/quantize6() rules, norm weights 1.0, biases N(0, 0.02). For measurements of models too large to make on
+ * the host quickly. `tensors` must place every tensor as Places.take() does (public/llama2_numpy.py:751-775). */
+int32_t he_open_synthetic(const he_config *cfg, const he_tensor *tensors, uint64_t size, uint64_t seed,
+                          const float *rope_cos, const float *rope_sin, int32_t max_block, he_engine **out);
+
+/* engine.forward(token, pos, needLogits) (public/forward.js:1891-1912): one token at position pos through every
+ * layer, its key and value into the cache; with need_logits the logits are computed and, if logits is not NULL,
+ * copied into it (vocab_size floats, host). Blocks until done. */
+int32_t he_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, float *logits);
+
+/* engine.forwardMany(tokens, pos) (public/forward.js:1755-1769): count tokens at pos, pos+1, ... without logits;
+ * every token's numbers are those he_forward gives it alone. count <= he_prompt_block(e). */
+int32_t he_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos);
+
+/* engine.generateMany (public/forward.js:1837-1890) for greedy decoding (temperature 0): `count` steps from token at
+ * pos, each the forward pass with logits and the first index of the largest logit (kernels/kernel.ts:695-699).
+ * ids receives the tokens chosen, a stop token last where one came; *n_ids their number. The logits of the last step
+ * stay readable with he_logits. Returns HE_E_NOTFINITE where a step's largest logit is not finite (nothing of that
+ * step is in ids). */
+int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, int32_t count, const int32_t *stops,
+                         int32_t n_stops, int32_t *ids, int32_t *n_ids);
+
+/* engine.logits() (public/forward.js:1936): the logits of the last step with logits, vocab_size floats (host). */
+int32_t he_logits(he_engine *e, float *out);
+
+/* engine.keysAndValues(from, count) (public/forward.js:1939-1953): the cache at positions from..from+count-1 as
+ * float32 [layers][count][kv_dim], keys then values (host). */
+int32_t he_kv_read(he_engine *e, int32_t from, int32_t count, float *keys, float *values);
+
+/* external().read(offset, length) (public/forward.js:574): bytes of the checkpoint as the device holds them. */
+int32_t he_checkpoint_read(he_engine *e, uint64_t offset, uint64_t length, void *out);
+
+/* engine.promptBlock (public/forward.js:1773-1778): how many tokens he_forward_many takes at once. */
+int32_t he_prompt_block(he_engine *e);
+
+/* engine.memoryBytes() (public/forward.js:1954): the device bytes the engine holds. */
+uint64_t he_device_bytes(he_engine *e);
+
+/* engine.release() (public/forward.js:1918-1935): frees everything the engine holds. */
+int32_t he_close(he_engine *e);
+
+/* ---- kernel level: device pointers, for the standalone matmul and the parity tests ---- */
+
+/* quantize_x (kernels/kernel.ts:129-156) of m rows of n float32 (row stride n): int8 rows (stride n) and float32
+ * scales (stride n/32), bias 64 (q in 1..127) or 0 (q in -127..127). n % 32 == 0. */
+int32_t hk_quantize_x(void *xq, void *xs, const void *x, int32_t m, int32_t n, int32_t bias, void *stream);
+
+/* y[t][r] for m tokens and rows r < rows of an int8 (six = 0) or int6 (six = 1) matrix of K columns, its float32
+ * group scales ws [rows][K/32], against activations xq [m][K] / xs [m][K/32] from hk_quantize_x with the same bias:
+ * matmul_q8r (kernels/kernel_relaxed.ts:34-67) for bias 64, matmul_q8 (kernels/kernel.ts:231-258) for bias 0,
+ * matmul_q6r / matmul_q6 for int6; matmul_q8r_tile (kernels/kernel_relaxed.ts:164-183) is the same per token.
+ * y is [m][rows] float32. m <= 8 runs the decode GEMV, larger m the MFMA GEMM; both give the same bits. */
+int32_t hk_matmul(void *y, const void *xq, const void *xs, const void *w, const void *ws, int32_t m, int32_t rows,
+                  int32_t k, int32_t bias, int32_t six, void *stream);
+
+/* The exact int32 sums the matmuls scale, through the same loaders: for bias 64 one per (token, row, group),
+ * dot(w, q - 64) (kernels/kernel_relaxed.ts:47-55); for bias 0 four per group, the lanes of kernels/kernel.ts:222-229
+ * (lane k: products 2k, 2k+1, 2k+8, 2k+9 of each half of 16). s is [m][rows][K/32] or [m][rows][K/32][4] int32.
+ * gemm = 0 uses the GEMV loader, 1 the MFMA GEMM's. */
+int32_t hk_group_sums(void *s, const void *xq, const void *w, int32_t m, int32_t rows, int32_t k, int32_t bias,
+                      int32_t six, int32_t gemm, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PYODIDE_LLM_HIP_H */

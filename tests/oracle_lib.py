@@ -1,0 +1,255 @@
+"""ctypes over oracle/liboracle.so — TEST INFRASTRUCTURE (the checker and the CPU baseline), never the product."""
+import ctypes
+import os
+
+import numpy as np
+
+from paths import ORACLE_DIR, package
+
+LIB = os.path.join(ORACLE_DIR, "liboracle.so")
+_lib = None
+P, I32, I64, U64, F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(f"{LIB} is not built (make -C oracle)")
+        pk = package()
+        lib = ctypes.CDLL(LIB)
+        cfgp, tp = ctypes.POINTER(pk.HeConfig), ctypes.POINTER(pk.HeTensor)
+        sig = {
+            "or_mix64": (U64, [U64]),
+            "or_synth_factor": (F, [ctypes.c_double]),
+            "or_synth_value": (F, [U64, I32, U64, F]),
+            "or_synth_fill": (None, [P, U64, U64, I32, U64, ctypes.c_double]),
+            "or_group_size": (I32, [I32]),
+            "or_quantize": (None, [P, P, P, I64, I32]),
+            "or_quantize6": (None, [P, P, P, I64]),
+            "or_pack6": (None, [P, P, I64]),
+            "or_unpack6": (None, [P, P, I64]),
+            "or_quantize_x": (None, [P, P, P, I32, I32]),
+            "or_matmul_q8r": (None, [P, P, P, P, P, I32, I32, I32]),
+            "or_matmul_q8": (None, [P, P, P, P, P, I32, I32, I32]),
+            "or_matmul_q6r": (None, [P, P, P, P, P, I32, I32, I32]),
+            "or_matmul_q6": (None, [P, P, P, P, P, I32, I32, I32]),
+            "or_group_sums": (None, [P, P, P, I32, I32, I32, I32]),
+            "or_matmul": (None, [P, P, P, P, P, I32, I32, I32, I32, I32]),
+            "or_rmsnorm": (None, [P, P, P, I32, F]),
+            "or_rope": (None, [P, P, P, I32, I32, I32]),
+            "or_attention": (None, [P, P, P, P, P, I32, I32, I32, I32, I32, I32, I32]),
+            "or_to_f16": (None, [P, P, I32]),
+            "or_from_f16": (None, [P, P, I32]),
+            "or_fexp": (F, [F]),
+            "or_vexp": (None, [P, I32]),
+            "or_swiglu": (None, [P, P, P, I32]),
+            "or_add": (None, [P, P, I32]),
+            "or_argmax": (I32, [P, I32]),
+            "or_places": (I64, [cfgp, tp]),
+            "or_synth_checkpoint": (None, [cfgp, tp, P, I64, U64]),
+            "or_rope_tables": (None, [P, P, I32, I32, ctypes.c_double]),
+            "or_model_open": (P, [cfgp, tp, P, P, P, I32]),
+            "or_model_run": (I32, [P, P, I32, I32, I32]),
+            "or_model_logits": (P, [P]),
+            "or_model_kv": (None, [P, I32, I32, P, P]),
+            "or_model_close": (None, [P]),
+            "or_generate": (I32, [P, P, I32, I32, I32, P, P]),
+            "or_set_threads": (None, [I32]),
+            "or_get_threads": (I32, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = lib
+    return _lib
+
+
+def ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def config(**fields):
+    return package().config(**fields)
+
+
+def places(cfg):
+    t = package().TensorArray()
+    size = load().or_places(ctypes.byref(cfg), t)
+    return t, int(size)
+
+
+def synth_checkpoint(cfg, tensors, size, seed=0):
+    out = np.zeros(size, dtype=np.uint8)
+    load().or_synth_checkpoint(ctypes.byref(cfg), tensors, ptr(out), size, seed)
+    return out
+
+
+def rope_tables(seq_len, hs, theta):
+    cos = np.zeros((seq_len, hs // 2), dtype=np.float32)
+    sin = np.zeros_like(cos)
+    load().or_rope_tables(ptr(cos), ptr(sin), seq_len, hs, theta)
+    return cos, sin
+
+
+def synth(n, seed, stream, sigma, first=0):
+    out = np.zeros(n, dtype=np.float32)
+    load().or_synth_fill(ptr(out), n, seed, stream, first, sigma)
+    return out
+
+
+def quantize(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    group = load().or_group_size(k)
+    q = np.zeros(x.shape, dtype=np.int8)
+    s = np.zeros(x.size // group, dtype=np.float32)
+    load().or_quantize(ptr(q), ptr(s), ptr(x), x.size, group)
+    return q, s
+
+
+def quantize6(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.zeros(x.shape, dtype=np.int8)
+    s = np.zeros(x.size // 32, dtype=np.float32)
+    load().or_quantize6(ptr(q), ptr(s), ptr(x), x.size // 32)
+    return q, s
+
+
+def pack6(q):
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    out = np.zeros((q.size // 32, 24), dtype=np.uint8)
+    load().or_pack6(ptr(out), ptr(q), q.size // 32)
+    return out
+
+
+def unpack6(raw):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.zeros((raw.size // 24, 32), dtype=np.int8)
+    load().or_unpack6(ptr(out), ptr(raw), raw.size // 24)
+    return out
+
+
+def quantize_x(x, bias):
+    """rows of x ([m][n] or [n]) -> (int8 [m][n], scales [m][n/32])"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = x.reshape(-1, x.shape[-1])
+    n = rows.shape[1]
+    q = np.zeros(rows.shape, dtype=np.int8)
+    s = np.zeros((rows.shape[0], n // 32), dtype=np.float32)
+    for i in range(rows.shape[0]):
+        load().or_quantize_x(ptr(q[i]), ptr(s[i]), ptr(rows[i]), n, bias)
+    return q.reshape(x.shape), s.reshape(x.shape[:-1] + (n // 32,))
+
+
+def matmul(xq, xs, w, ws, rows, k, bias, six):
+    """y [m][rows] of the oracle's matmul_q8r / q8 / q6r / q6"""
+    xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, k)
+    xs = np.ascontiguousarray(xs, dtype=np.float32).reshape(-1, k // 32)
+    m = xq.shape[0]
+    y = np.zeros((m, rows), dtype=np.float32)
+    w = np.ascontiguousarray(w)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    load().or_matmul(ptr(y), ptr(xq), ptr(xs), ptr(w), ptr(ws), m, rows, k, bias, six)
+    return y
+
+
+def group_sums(xq, w, rows, k, bias, six):
+    xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, k)
+    per = (k // 32) * (1 if bias else 4)
+    out = np.zeros((xq.shape[0], rows, per), dtype=np.int32)
+    w = np.ascontiguousarray(w)
+    for t in range(xq.shape[0]):
+        load().or_group_sums(ptr(out[t]), ptr(xq[t]), ptr(w), rows, k, bias, six)
+    return out
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros_like(x)
+    load().or_rmsnorm(ptr(out), ptr(x), ptr(np.ascontiguousarray(w, dtype=np.float32)), x.size, eps)
+    return out
+
+
+def fexp(x):
+    return load().or_fexp(float(x))
+
+
+def vexp(x):
+    x = np.array(x, dtype=np.float32)
+    load().or_vexp(ptr(x), x.size)
+    return x
+
+
+def to_f16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.size, dtype=np.uint16)
+    load().or_to_f16(ptr(out), ptr(x), x.size)
+    return out
+
+
+def from_f16(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.zeros(h.size, dtype=np.float32)
+    load().or_from_f16(ptr(out), ptr(h), h.size)
+    return out
+
+
+def attention(q, kc, vc, pos, nh, nkv, hs, half=False):
+    """one token's attention at position pos over the cache rows 0..pos"""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc)
+    vc = np.ascontiguousarray(vc)
+    out = np.zeros(nh * hs, dtype=np.float32)
+    att = np.zeros(nh * (pos + 1), dtype=np.float32)
+    load().or_attention(ptr(out), ptr(q), ptr(kc), ptr(vc), ptr(att), pos, nh, nkv, hs, 0, nh, int(half))
+    return out
+
+
+class Model:
+    """or_model: the reference's run() on the host"""
+
+    def __init__(self, cfg, tensors, checkpoint, cos, sin, max_block=64):
+        self.cfg = cfg
+        self._ck = np.ascontiguousarray(checkpoint, dtype=np.uint8)
+        self._cos = np.ascontiguousarray(cos, dtype=np.float32)
+        self._sin = np.ascontiguousarray(sin, dtype=np.float32)
+        self.max_block = max_block
+        self._h = load().or_model_open(ctypes.byref(cfg), tensors, ptr(self._ck), ptr(self._cos), ptr(self._sin),
+                                       max_block)
+
+    def run(self, tokens, pos0, need_logits):
+        ids = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        code = load().or_model_run(self._h, ptr(ids), ids.size, pos0, int(need_logits))
+        if code:
+            raise RuntimeError("or_model_run refused the call")
+
+    def logits(self):
+        p = load().or_model_logits(self._h)
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)),
+                                     shape=(self.cfg.vocab_size,)).copy()
+
+    def kv(self, start, count):
+        kv_dim = self.cfg.n_kv_heads * self.cfg.head_size
+        keys = np.zeros((self.cfg.n_layers, count, kv_dim), dtype=np.float32)
+        values = np.zeros_like(keys)
+        load().or_model_kv(self._h, start, count, ptr(keys), ptr(values))
+        return keys, values
+
+    def generate(self, prompt, steps, block=None):
+        prompt = np.ascontiguousarray(np.asarray(prompt, dtype=np.int32))
+        out = np.zeros(max(steps, 1), dtype=np.int32)
+        logits = np.zeros(self.cfg.vocab_size, dtype=np.float32)
+        n = load().or_generate(self._h, ptr(prompt), prompt.size, steps, block or self.max_block, ptr(out),
+                               ptr(logits))
+        if n < 0:
+            raise RuntimeError("or_generate refused the call")
+        return out[:n], logits
+
+    def close(self):
+        if self._h:
+            load().or_model_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()

@@ -1,0 +1,87 @@
+"""The oracle's run() (public/forward.js:1011-1090) on tiny synthetic models: the checkpoint bytes the golden script
+fed the reference, the reference NumPy forward's logits within the int8 line (tests/test_quantize.py:81-90: the int8
+path quantizes activations, NumPy does not), and blocks equal to one token at a time to the bit
+(tests/forward-check.mjs:438-452)."""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from paths import GOLDEN_DIR
+
+NF = np.load(os.path.join(GOLDEN_DIR, "numpy_forward.npz"))
+TINY = {
+    "tiny_gqa_int8": (dict(dim=64, hidden_dim=128, n_layers=2, n_heads=4, n_kv_heads=2, head_size=16, vocab_size=320,
+                           seq_len=32, shared_classifier=1, six=0, qkv_bias=0), 10000.0),
+    "tiny_mha_own_cls_int8": (dict(dim=96, hidden_dim=160, n_layers=2, n_heads=3, n_kv_heads=3, head_size=32,
+                                   vocab_size=256, seq_len=32, shared_classifier=0, six=0, qkv_bias=0), 10000.0),
+    "tiny_qwen_int6": (dict(dim=64, hidden_dim=96, n_layers=2, n_heads=4, n_kv_heads=1, head_size=16, vocab_size=288,
+                            seq_len=32, shared_classifier=0, six=1, qkv_bias=1), 1000000.0),
+}
+
+
+def build(name, **extra):
+    fields, theta = TINY[name]
+    cfg = ol.config(**{**fields, **extra})
+    tensors, size = ol.places(cfg)
+    ck = ol.synth_checkpoint(cfg, tensors, size, seed=7)
+    cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, theta)
+    return cfg, tensors, ck, cos, sin
+
+
+@pytest.mark.parametrize("name", sorted(TINY))
+def test_checkpoint_is_the_golden_one(name):
+    _, _, ck, _, _ = build(name)
+    assert np.array_equal(np.frombuffer(hashlib.sha256(ck.tobytes()).digest(), dtype=np.uint8), NF[f"sha256_{name}"])
+
+
+@pytest.mark.parametrize("name", sorted(TINY))
+@pytest.mark.parametrize("relaxed", [1, 0])
+def test_logits_follow_the_reference_numpy_forward(name, relaxed):
+    cfg, tensors, ck, cos, sin = build(name, relaxed=relaxed)
+    model = ol.Model(cfg, tensors, ck, cos, sin, max_block=8)
+    want = NF[f"logits_{name}"]
+    for pos, tok in enumerate(NF["tokens"]):
+        model.run([tok], pos, True)
+        got = model.logits().astype(np.float64)
+        expected = want[pos].astype(np.float64)
+        assert np.abs(got - expected).max() / np.abs(expected).max() < 0.1
+        assert np.corrcoef(got, expected)[0, 1] > 0.99
+
+
+@pytest.mark.parametrize("name", sorted(TINY))
+@pytest.mark.parametrize("half_kv", [0, 1])
+def test_blocks_equal_one_at_a_time(name, half_kv):
+    cfg, tensors, ck, cos, sin = build(name, half_kv=half_kv)
+    tokens = [1, 17, 3, 99, 5, 6, 7, 250, 9, 10, 11]
+    one = ol.Model(cfg, tensors, ck, cos, sin, max_block=8)
+    for pos, tok in enumerate(tokens):
+        one.run([tok], pos, pos == len(tokens) - 1)
+    many = ol.Model(cfg, tensors, ck, cos, sin, max_block=8)
+    many.run(tokens[:3], 0, False)
+    many.run(tokens[3:10], 3, False)
+    many.run(tokens[10:], 10, True)
+    assert np.array_equal(one.logits().view(np.uint32), many.logits().view(np.uint32))
+    k1, v1 = one.kv(0, len(tokens))
+    k2, v2 = many.kv(0, len(tokens))
+    assert np.array_equal(k1.view(np.uint32), k2.view(np.uint32)) and np.array_equal(v1.view(np.uint32), v2.view(np.uint32))
+
+
+def test_generate_is_greedy_over_forward():
+    cfg, tensors, ck, cos, sin = build("tiny_gqa_int8")
+    model = ol.Model(cfg, tensors, ck, cos, sin, max_block=4)
+    prompt = [5, 6, 7, 8, 9]
+    out, last = model.generate(prompt, steps=12)
+    assert out.size == 12 - len(prompt)
+    step = ol.Model(cfg, tensors, ck, cos, sin, max_block=4)
+    fed = [1] + prompt[:-1]
+    for pos, tok in enumerate(fed):
+        step.run([tok], pos, False)
+    token = prompt[-1]
+    for pos in range(len(prompt), 12):
+        step.run([token], pos, True)
+        token = int(np.argmax(step.logits()))
+        assert token == out[pos - len(prompt)]
+    assert np.array_equal(step.logits(), last)
