@@ -1,0 +1,141 @@
+// common.hpp — device helpers shared by the gfx950 kernels: the float32 steps of the reference's kernels done one
+// rounding at a time (every file is built with -ffp-contract=off and correctly rounded division and square root),
+// the Cephes exponential of kernels/kernel.ts:15-45, the float16 conversions of kernels/kernel.ts:383-392,570-599 and
+// the int6 widening of kernels/six.ts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define GS 32  // the quantization group (quantize.py)
+
+namespace ple {
+
+// ---- integer helpers ----
+
+// i32.trunc_sat_f32_s: NaN to 0, out of range to the nearest end (the conversion of quantize_x, kernels/kernel.ts:145)
+__device__ __forceinline__ int32_t trunc_sat(float f) {
+  if (f != f) return 0;
+  if (f >= 2147483648.0f) return 2147483647;
+  if (f < -2147483648.0f) return (-2147483647 - 1);
+  return (int32_t)f;
+}
+__device__ __forceinline__ int32_t sat16(int32_t v) { return v > 32767 ? 32767 : (v < -32768 ? -32768 : v); }
+__device__ __forceinline__ int32_t sat8(int32_t v) { return v > 127 ? 127 : (v < -128 ? -128 : v); }
+
+// quantize_x's value: narrow(trunc_sat(nearest(x * inv)) + bias) (kernels/kernel.ts:145-153; the i32 add wraps)
+__device__ __forceinline__ int8_t quant_value(float x, float inv, int32_t bias) {
+  const int32_t t = (int32_t)((uint32_t)trunc_sat(__builtin_rintf(x * inv)) + (uint32_t)bias);
+  return (int8_t)sat8(sat16(t));
+}
+
+// four activations of quantize_x(bias 64) with the bias taken out, q - 64 per byte: (q + 0x40) ^ 0x80 for q in
+// 0..127 (no carry leaves a byte). dot(w, q - 64) is matmul_q8r's group sum with int8_sums' correction in it
+// (kernels/kernel_relaxed.ts:47-55, kernels/kernel.ts:204-212).
+__device__ __forceinline__ uint32_t centre4(uint32_t q) { return (q + 0x40404040u) ^ 0x80808080u; }
+
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// kernels/six.ts: a group's 24 bytes (low nibbles in bytes 0..15, the top two bits of values k, k+8, k+16, k+24 in
+// byte 16+k at bits 0, 2, 4, 6) widened to its 32 int8 values (multiples of 4), four a word
+__device__ __forceinline__ void six_widen(const uint32_t L[4], uint32_t T0, uint32_t T1, uint32_t w[8]) {
+  w[0] = ((L[0] & 0x0F0F0F0Fu) << 2) | ((T0 & 0x03030303u) << 6);
+  w[1] = ((L[1] & 0x0F0F0F0Fu) << 2) | ((T1 & 0x03030303u) << 6);
+  w[2] = ((L[2] & 0x0F0F0F0Fu) << 2) | ((T0 << 4) & 0xC0C0C0C0u);
+  w[3] = ((L[3] & 0x0F0F0F0Fu) << 2) | ((T1 << 4) & 0xC0C0C0C0u);
+  w[4] = ((L[0] >> 2) & 0x3C3C3C3Cu) | ((T0 << 2) & 0xC0C0C0C0u);
+  w[5] = ((L[1] >> 2) & 0x3C3C3C3Cu) | ((T1 << 2) & 0xC0C0C0C0u);
+  w[6] = ((L[2] >> 2) & 0x3C3C3C3Cu) | (T0 & 0xC0C0C0C0u);
+  w[7] = ((L[3] >> 2) & 0x3C3C3C3Cu) | (T1 & 0xC0C0C0C0u);
+}
+
+// ---- float helpers ----
+
+__device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
+
+// f32x4.max / f32x4.min of WebAssembly: NaN if either is, else the larger / smaller (+0 above -0)
+__device__ __forceinline__ float wmax(float a, float b) {
+  if (a != a || b != b) return a + b;
+  if (a == b) return __builtin_signbitf(a) ? b : a;
+  return a > b ? a : b;
+}
+__device__ __forceinline__ float wmin(float a, float b) {
+  if (a != a || b != b) return a + b;
+  if (a == b) return __builtin_signbitf(a) ? a : b;
+  return a < b ? a : b;
+}
+
+// the Cephes expf polynomial (S. L. Moshier's Cephes library) in the steps of kernels/kernel.ts:18-28
+__device__ __forceinline__ float cephes_core(float x) {
+  const float k = __builtin_rintf(x * 1.44269504088896341f);
+  const float r = (x - k * 0.693359375f) - k * -2.12194440e-4f;
+  float p = 1.9875691500e-4f;
+  p = p * r + 1.3981999507e-3f;
+  p = p * r + 8.3334519073e-3f;
+  p = p * r + 4.1665795894e-2f;
+  p = p * r + 1.6666665459e-1f;
+  p = p * r + 5.0000001201e-1f;
+  const float e = (p * (r * r) + r) + 1.0f;
+  return e * bits_f32((uint32_t)(trunc_sat(k) + 127) << 23);
+}
+// kernels/kernel.ts:15-29 fexp: 0 below -87, 88 above 88
+__device__ __forceinline__ float fexp(float x) {
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.0f) x = 88.0f;
+  return cephes_core(x);
+}
+// kernels/kernel.ts:33-45 vexp: x clamped to [-87, 88]
+__device__ __forceinline__ float vexp(float x) { return cephes_core(wmin(wmax(x, -87.0f), 88.0f)); }
+
+// kernels/kernel.ts:570-599 to_f16: round to nearest even; 65536 and above (and NaN) to infinity
+__device__ __forceinline__ uint16_t to_f16(float x) {
+  const uint32_t bits = __float_as_uint(x);
+  const uint32_t sign = (bits >> 16) & 0x8000u;
+  const int32_t exponent = (int32_t)((bits >> 23) & 0xff) - 112;
+  uint32_t mantissa = bits & 0x7fffffu;
+  uint32_t result;
+  if (exponent >= 31) {
+    result = sign | 0x7c00u;
+  } else if (exponent <= 0) {
+    if (exponent < -10) {
+      result = sign;
+    } else {
+      mantissa |= 0x800000u;
+      const uint32_t shift = (uint32_t)(14 - exponent);
+      const uint32_t rest = mantissa & ((1u << shift) - 1), middle = 1u << (shift - 1);
+      uint32_t value = mantissa >> shift;
+      if (rest > middle || (rest == middle && (value & 1))) value++;
+      result = sign | value;
+    }
+  } else {
+    const uint32_t rest = mantissa & 0x1fffu;
+    uint32_t value = ((uint32_t)exponent << 10) | (mantissa >> 13);
+    if (rest > 0x1000u || (rest == 0x1000u && (value & 1))) value++;
+    result = sign | value;
+  }
+  return (uint16_t)result;
+}
+
+// kernels/kernel.ts:383-392 half: sign-extended bits shifted by 13, masked, times 2^112 (exact for every finite half)
+__device__ __forceinline__ float from_f16(uint16_t h) {
+  const int32_t bits = ((int32_t)(int16_t)h << 13) & (int32_t)0x8fffffff;
+  return __int_as_float(bits) * 5.192296858534828e33f;
+}
+
+// ---- wave helpers (wave64) ----
+
+__device__ __forceinline__ float wave_max32(float v) {  // over each half of the wave (32 lanes)
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace ple

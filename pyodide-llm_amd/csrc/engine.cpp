@@ -1,0 +1,646 @@
+// engine.cpp — the C ABI of include/pyodide_llm_hip.h: the forward engine public/forward.js createForward builds
+// (public/forward.js:626-1955), for the int8/int6 Llama and Qwen2 forms, on one MI355X.
+//
+// Device memory: every tensor of the checkpoint in its own 256-byte aligned region of one allocation (the file's
+// offsets are only 4-byte aligned), so that the matmuls stream rows with 16-byte loads; a region table maps file
+// offsets to device addresses for external().read. The KV cache is allocated for the whole context at start (the
+// reference grows it from 256 positions by doubling, public/forward.js:828-848; the values do not depend on it).
+// One stream, default priority; every call blocks until its results are on the host, as forward.js's do.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/pyodide_llm_hip.h"
+#include "kernels.hpp"
+
+using namespace ple;
+
+namespace {
+
+thread_local std::string g_error;
+
+int32_t fail(int32_t code, const std::string &what) {
+  g_error = what;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                          \
+  do {                                                                                         \
+    hipError_t err_ = (expr);                                                                  \
+    if (err_ != hipSuccess)                                                                    \
+      return fail(HE_E_HIP, std::string(#expr) + ": " + hipGetErrorString(err_));             \
+  } while (0)
+
+int32_t group_size(int32_t row_length) {  // public/llama2_convert.py:25-29
+  int32_t size = 32;
+  while (row_length % size) size /= 2;
+  return size;
+}
+
+struct Shape {
+  int64_t count;  // values in the tensor
+  int32_t k;      // the row length (matrices), 0 for float32 vectors
+  int32_t rows;   // rows of one layer (matrices)
+  int32_t layers;
+};
+
+Shape shape_of(const he_config &c, int id) {
+  const int64_t L = c.n_layers, dim = c.dim, hidden = c.hidden_dim, vocab = c.vocab_size;
+  const int32_t qdim = c.n_heads * c.head_size, kvdim = c.n_kv_heads * c.head_size;
+  switch (id) {
+    case HE_T_EMBEDDING: return {vocab * dim, c.dim, c.vocab_size, 1};
+    case HE_T_RMS_ATT: return {L * dim, 0, 0, c.n_layers};
+    case HE_T_WQ: return {L * qdim * dim, c.dim, qdim, c.n_layers};
+    case HE_T_WK: return {L * kvdim * dim, c.dim, kvdim, c.n_layers};
+    case HE_T_WV: return {L * kvdim * dim, c.dim, kvdim, c.n_layers};
+    case HE_T_WO: return {L * dim * qdim, qdim, c.dim, c.n_layers};
+    case HE_T_RMS_FFN: return {L * dim, 0, 0, c.n_layers};
+    case HE_T_W1: return {L * hidden * dim, c.dim, c.hidden_dim, c.n_layers};
+    case HE_T_W2: return {L * dim * hidden, c.hidden_dim, c.dim, c.n_layers};
+    case HE_T_W3: return {L * hidden * dim, c.dim, c.hidden_dim, c.n_layers};
+    case HE_T_RMS_FINAL: return {dim, 0, 0, 1};
+    case HE_T_WCLS: return {vocab * dim, c.dim, c.vocab_size, 1};
+    case HE_T_BQ: return {L * qdim, 0, 0, c.n_layers};
+    case HE_T_BK: return {L * kvdim, 0, 0, c.n_layers};
+    case HE_T_BV: return {L * kvdim, 0, 0, c.n_layers};
+  }
+  return {0, 0, 0, 0};
+}
+
+bool present(const he_config &c, int id) {
+  if (id == HE_T_WCLS && c.shared_classifier) return false;  // the embedding's
+  if (id >= HE_T_BQ && !c.qkv_bias) return false;
+  return true;
+}
+
+struct Region {
+  uint64_t file, bytes, dev;
+};
+
+template <typename T>
+int32_t dev_alloc(T **p, size_t bytes) {
+  void *q = nullptr;
+  HIP_TRY(hipMalloc(&q, bytes ? bytes : 1));
+  *p = reinterpret_cast<T *>(q);
+  return HE_OK;
+}
+
+}  // namespace
+
+struct he_engine {
+  he_config c{};
+  he_tensor t[HE_T_COUNT]{};
+  hipStream_t stream = nullptr;
+  uint64_t size = 0;
+  uint8_t *blob = nullptr;  // the regions
+  uint64_t blob_bytes = 0;
+  std::vector<Region> regions;
+  const uint8_t *values[HE_T_COUNT]{};
+  const float *scales[HE_T_COUNT]{};
+  float *cos_t = nullptr, *sin_t = nullptr;
+  void *keys = nullptr, *vals = nullptr;  // [layers][seq_len][kv_dim]
+  int32_t qdim = 0, kvdim = 0, bias = 64, max_block = 1, chunk = 1, xw = 0, widest = 0;
+  // activations of `chunk` tokens
+  float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *hb2 = nullptr;
+  int8_t *xq = nullptr;
+  float *xs = nullptr;
+  float *scores = nullptr, *partial = nullptr, *tilemax = nullptr;
+  float *logits = nullptr;
+  int32_t *tokens = nullptr;
+  float *amax_v = nullptr;
+  int32_t *amax_i = nullptr;
+  float *best_v = nullptr;
+  int32_t *best_i = nullptr;
+  uint64_t device_bytes = 0;
+  bool have_logits = false;
+
+  const uint8_t *mat(int id, int l) const {
+    const Shape s = shape_of(c, id == HE_T_WCLS && c.shared_classifier ? HE_T_EMBEDDING : id);
+    const int64_t row_bytes = c.six ? (int64_t)s.k / 32 * 24 : s.k;
+    return values[id] + (int64_t)l * s.rows * row_bytes;
+  }
+  const float *mat_scales(int id, int l) const {
+    const Shape s = shape_of(c, id == HE_T_WCLS && c.shared_classifier ? HE_T_EMBEDDING : id);
+    return scales[id] + (int64_t)l * s.rows * (s.k / 32);
+  }
+  const float *vec(int id, int64_t at) const { return reinterpret_cast<const float *>(values[id]) + at; }
+};
+
+namespace {
+
+void destroy(he_engine *e) {
+  if (!e) return;
+  void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
+                  e->xq, e->xs, e->scores, e->partial, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
+                  e->best_v, e->best_i};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+int32_t check_config(const he_config &c) {
+  if (c.dim <= 0 || c.hidden_dim <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 ||
+      c.head_size <= 0 || c.vocab_size <= 0 || c.seq_len <= 0)
+    return fail(HE_E_ARG, "the plan has a size that is not positive");
+  if (c.n_heads % c.n_kv_heads) return fail(HE_E_ARG, "n_heads is not a multiple of n_kv_heads");
+  if (c.head_size % 4) return fail(HE_E_ARG, "head_size is not a multiple of 4");
+  const int32_t qdim = c.n_heads * c.head_size, kvdim = c.n_kv_heads * c.head_size;
+  if (c.dim % 32 || c.hidden_dim % 32 || qdim % 32 || kvdim % 32)
+    return fail(HE_E_ARG, "the int8 kernels take rows of whole groups of 32 (dim, hidden, q and kv widths)");
+  if (c.head_size > 256) return fail(HE_E_ARG, "head_size above 256 is not supported");
+  return HE_OK;
+}
+
+// the checkpoint's regions: the header, every present tensor's values and scales, and whatever lies between them
+int32_t plan_regions(he_engine *e) {
+  const he_config &c = e->c;
+  std::vector<Region> pieces;
+  pieces.push_back({0, 28, 0});
+  for (int id = 0; id < HE_T_COUNT; ++id) {
+    if (!present(c, id)) continue;
+    const Shape s = shape_of(c, id);
+    if (s.k) {
+      const uint64_t vb = c.six ? (uint64_t)s.count / 32 * 24 : (uint64_t)s.count;
+      const uint64_t sb = (uint64_t)s.count / group_size(s.k) * 4;
+      if (c.six && s.k % 32) return fail(HE_E_ARG, "int6 matrices need rows of whole groups of 32");
+      pieces.push_back({(uint64_t)e->t[id].offset, vb, 0});
+      pieces.push_back({(uint64_t)e->t[id].scales, sb, 0});
+    } else {
+      pieces.push_back({(uint64_t)e->t[id].offset, (uint64_t)s.count * 4, 0});
+    }
+  }
+  std::sort(pieces.begin(), pieces.end(), [](const Region &a, const Region &b) { return a.file < b.file; });
+  std::vector<Region> out;
+  uint64_t at = 0;
+  for (const Region &p : pieces) {
+    if (p.file < at) return fail(HE_E_ARG, "the plan's tensors overlap");
+    if (p.file > at) out.push_back({at, p.file - at, 0});
+    out.push_back(p);
+    at = p.file + p.bytes;
+  }
+  if (at > e->size) return fail(HE_E_ARG, "the plan's tensors run past the checkpoint's size");
+  if (at < e->size) out.push_back({at, e->size - at, 0});
+  uint64_t dev = 0;
+  for (Region &r : out) {
+    r.dev = dev;
+    dev += (r.bytes + 255) / 256 * 256;
+  }
+  e->regions = out;
+  e->blob_bytes = dev;
+  return HE_OK;
+}
+
+const uint8_t *device_at(const he_engine *e, uint64_t file) {
+  for (const Region &r : e->regions)
+    if (file >= r.file && file < r.file + r.bytes) return e->blob + r.dev + (file - r.file);
+  return nullptr;
+}
+
+int32_t bind_tensors(he_engine *e) {
+  for (int id = 0; id < HE_T_COUNT; ++id) {
+    const int src = (id == HE_T_WCLS && e->c.shared_classifier) ? HE_T_EMBEDDING : id;
+    if (!present(e->c, src)) continue;
+    e->values[id] = device_at(e, (uint64_t)e->t[src].offset);
+    if (!e->values[id]) return fail(HE_E_ARG, "a tensor is outside the checkpoint");
+    if (shape_of(e->c, src).k) {
+      e->scales[id] = reinterpret_cast<const float *>(device_at(e, (uint64_t)e->t[src].scales));
+      if (!e->scales[id]) return fail(HE_E_ARG, "a tensor's scales are outside the checkpoint");
+    }
+  }
+  return HE_OK;
+}
+
+int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_sin) {
+  const he_config &c = e->c;
+  e->qdim = c.n_heads * c.head_size;
+  e->kvdim = c.n_kv_heads * c.head_size;
+  e->bias = c.relaxed ? 64 : 0;
+  e->xw = std::max(c.dim, e->qdim);
+  e->widest = std::max(e->xw, c.hidden_dim);
+  const int32_t T = e->chunk;
+  const size_t table = (size_t)c.seq_len * (c.head_size / 2) * sizeof(float);
+  int32_t rc;
+#define ALLOC(p, bytes)                                  \
+  do {                                                   \
+    if ((rc = dev_alloc(&(p), (bytes))) != HE_OK) return rc; \
+    e->device_bytes += (bytes);                          \
+  } while (0)
+  ALLOC(e->cos_t, table);
+  ALLOC(e->sin_t, table);
+  HIP_TRY(hipMemcpy(e->cos_t, rope_cos, table, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(e->sin_t, rope_sin, table, hipMemcpyHostToDevice));
+  const size_t kv = (size_t)c.n_layers * c.seq_len * e->kvdim * (c.half_kv ? 2 : 4);
+  ALLOC(e->keys, kv);
+  ALLOC(e->vals, kv);
+  HIP_TRY(hipMemset(e->keys, 0, kv));
+  HIP_TRY(hipMemset(e->vals, 0, kv));
+  ALLOC(e->x, sizeof(float) * T * c.dim);
+  ALLOC(e->xb, sizeof(float) * T * e->xw);
+  ALLOC(e->q, sizeof(float) * T * e->qdim);
+  ALLOC(e->k, sizeof(float) * T * e->kvdim);
+  ALLOC(e->v, sizeof(float) * T * e->kvdim);
+  ALLOC(e->hb, sizeof(float) * T * c.hidden_dim);
+  ALLOC(e->hb2, sizeof(float) * T * c.hidden_dim);
+  ALLOC(e->xq, (size_t)T * e->widest);
+  ALLOC(e->xs, sizeof(float) * T * (e->widest / 32));
+  ALLOC(e->scores, sizeof(float) * T * c.n_heads * (size_t)c.seq_len);
+  ALLOC(e->partial, sizeof(float) * T * c.n_heads * (size_t)(c.seq_len / 4 + 4) * c.head_size);
+  ALLOC(e->tilemax, sizeof(float) * T * c.n_heads * (size_t)(c.seq_len / 64 + 1));
+  ALLOC(e->logits, sizeof(float) * c.vocab_size);
+  ALLOC(e->tokens, sizeof(int32_t) * T);
+  ALLOC(e->amax_v, sizeof(float) * 256);
+  ALLOC(e->amax_i, sizeof(int32_t) * 256);
+  ALLOC(e->best_v, sizeof(float) * 4);
+  ALLOC(e->best_i, sizeof(int32_t) * 4);
+#undef ALLOC
+  return HE_OK;
+}
+
+int32_t open_common(const he_config *cfg, const he_tensor *tensors, uint64_t size, const float *rope_cos,
+                    const float *rope_sin, int32_t max_block, he_engine **out, he_engine **made) {
+  if (!cfg || !tensors || !rope_cos || !rope_sin || !out) return fail(HE_E_ARG, "a required pointer is null");
+  if (max_block < 1) return fail(HE_E_ARG, "max_block must be at least 1");
+  int32_t rc = check_config(*cfg);
+  if (rc) return rc;
+  he_engine *e = new he_engine();
+  *made = e;
+  e->c = *cfg;
+  std::memcpy(e->t, tensors, sizeof(e->t));
+  e->size = size;
+  e->max_block = max_block;
+  e->chunk = std::min(max_block, 16);
+  HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+  if ((rc = plan_regions(e))) return rc;
+  if ((rc = dev_alloc(&e->blob, e->blob_bytes))) return rc;
+  e->device_bytes += e->blob_bytes;
+  if ((rc = bind_tensors(e))) return rc;
+  if ((rc = allocate_state(e, rope_cos, rope_sin))) return rc;
+  return HE_OK;
+}
+
+// ---- the forward pass of one chunk of tokens (public/forward.js:1011-1090) ----
+
+hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs) {
+  const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
+  for (int32_t t0 = 0; t0 < m; t0 += 8) {
+    MatArgs a{};
+    a.nseg = nseg;
+    a.total_rows = 0;
+    for (int i = 0; i < nseg; ++i) {
+      a.seg[i] = segs[i];
+      a.seg[i].y = segs[i].y + (int64_t)t0 * segs[i].y_stride;
+      a.total_rows += segs[i].rows;
+    }
+    a.xq = xq + (int64_t)t0 * xq_stride;
+    a.xs = xs + (int64_t)t0 * xs_stride;
+    a.xq_stride = xq_stride;
+    a.xs_stride = xs_stride;
+    a.k = k;
+    a.m = std::min(8, m - t0);
+    a.sums = nullptr;
+    hipError_t err = launch_gemv(a, e->c.six, e->c.relaxed, e->stream);
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, bool need_logits) {
+  const he_config &c = e->c;
+  hipStream_t s = e->stream;
+  const int32_t dim = c.dim, hidden = c.hidden_dim, qdim = e->qdim, kvdim = e->kvdim, hs = c.head_size;
+  const int32_t W = e->widest;
+  const size_t esz = c.half_kv ? 2 : 4;
+  HIP_TRY(hipMemcpyAsync(e->tokens, tokens, sizeof(int32_t) * m, hipMemcpyHostToDevice, s));
+  HIP_TRY(launch_embed(e->x, e->tokens, e->values[HE_T_EMBEDDING], e->scales[HE_T_EMBEDDING], m, dim, dim,
+                       c.six ? 32 : group_size(dim), c.six, s));
+  for (int32_t l = 0; l < c.n_layers; ++l) {
+    HIP_TRY(launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim, W,
+                                 W / 32, 0, c.rms_norm_eps, e->bias, s));
+    const MatSeg qkv[3] = {
+        {e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), e->q, qdim, qdim, 0},
+        {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), e->k, kvdim, kvdim, 0},
+        {e->mat(HE_T_WV, l), e->mat_scales(HE_T_WV, l), e->v, kvdim, kvdim, 0}};
+    HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
+    QkvPost qp{};
+    qp.q = e->q;
+    qp.k = e->k;
+    qp.v = e->v;
+    qp.q_stride = qdim;
+    qp.kv_stride = kvdim;
+    qp.bq = c.qkv_bias ? e->vec(HE_T_BQ, (int64_t)l * qdim) : nullptr;
+    qp.bk = c.qkv_bias ? e->vec(HE_T_BK, (int64_t)l * kvdim) : nullptr;
+    qp.bv = c.qkv_bias ? e->vec(HE_T_BV, (int64_t)l * kvdim) : nullptr;
+    qp.cos_t = e->cos_t;
+    qp.sin_t = e->sin_t;
+    qp.kcache = reinterpret_cast<uint8_t *>(e->keys) + (size_t)l * c.seq_len * kvdim * esz;
+    qp.vcache = reinterpret_cast<uint8_t *>(e->vals) + (size_t)l * c.seq_len * kvdim * esz;
+    qp.nh = c.n_heads;
+    qp.nkv = c.n_kv_heads;
+    qp.hs = hs;
+    qp.pos0 = pos0;
+    qp.m = m;
+    qp.half = c.half_kv;
+    HIP_TRY(launch_qkv_post(qp, s));
+    AttnArgs at{};
+    at.q = e->q;
+    at.q_stride = qdim;
+    at.kcache = qp.kcache;
+    at.vcache = qp.vcache;
+    at.out = e->xb;
+    at.out_stride = e->xw;
+    at.scores = e->scores;
+    at.partial = e->partial;
+    at.tilemax = e->tilemax;
+    at.nh = c.n_heads;
+    at.nkv = c.n_kv_heads;
+    at.hs = hs;
+    at.pos0 = pos0;
+    at.m = m;
+    at.seq_len = c.seq_len;
+    at.half = c.half_kv;
+    HIP_TRY(launch_attention(at, s));
+    HIP_TRY(launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s));
+    const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
+    HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
+    HIP_TRY(launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
+                                 W / 32, 0, c.rms_norm_eps, e->bias, s));
+    const MatSeg w13[2] = {{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), e->hb, hidden, hidden, 0},
+                           {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), e->hb2, hidden, hidden, 0}};
+    HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs));
+    HIP_TRY(launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s));
+    const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
+    HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs));
+  }
+  if (need_logits) {
+    HIP_TRY(launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x + (int64_t)(m - 1) * dim, e->vec(HE_T_RMS_FINAL, 0), 1,
+                                 dim, dim, W, W / 32, 0, c.rms_norm_eps, e->bias, s));
+    const MatSeg cls[1] = {{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), e->logits, c.vocab_size, 0, 0}};
+    HIP_TRY(matmul(e, cls, 1, dim, 1, e->xq, e->xs));
+    e->have_logits = true;
+  }
+  return HE_OK;
+}
+
+int32_t run_tokens(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos0, bool need_logits) {
+  if (count < 1) return fail(HE_E_ARG, "no tokens");
+  if (pos0 < 0 || (int64_t)pos0 + count > e->c.seq_len)
+    return fail(HE_E_STATE, "the positions run past the context (seq_len)");
+  for (int32_t i = 0; i < count; ++i)
+    if (tokens[i] < 0 || tokens[i] >= e->c.vocab_size) return fail(HE_E_ARG, "a token is outside the vocabulary");
+  for (int32_t at = 0; at < count; at += e->chunk) {
+    const int32_t m = std::min(e->chunk, count - at);
+    const int32_t rc = run_chunk(e, tokens + at, m, pos0 + at, need_logits && at + m == count);
+    if (rc) return rc;
+  }
+  return HE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *he_last_error(void) { return g_error.c_str(); }
+
+int32_t he_open(const he_config *cfg, const he_tensor *tensors, const void *checkpoint, uint64_t size,
+                const float *rope_cos, const float *rope_sin, int32_t max_block, he_engine **out) {
+  if (!checkpoint) return fail(HE_E_ARG, "checkpoint is null");
+  he_engine *e = nullptr;
+  int32_t rc = open_common(cfg, tensors, size, rope_cos, rope_sin, max_block, out, &e);
+  if (rc == HE_OK) {
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(checkpoint);
+    for (const Region &r : e->regions) {
+      hipError_t err = hipMemcpy(e->blob + r.dev, src + r.file, r.bytes, hipMemcpyHostToDevice);
+      if (err != hipSuccess) {
+        rc = fail(HE_E_HIP, std::string("uploading the checkpoint: ") + hipGetErrorString(err));
+        break;
+      }
+    }
+  }
+  if (rc != HE_OK) {
+    destroy(e);
+    return rc;
+  }
+  *out = e;
+  return HE_OK;
+}
+
+int32_t he_open_synthetic(const he_config *cfg, const he_tensor *tensors, uint64_t size, uint64_t seed,
+                          const float *rope_cos, const float *rope_sin, int32_t max_block, he_engine **out) {
+  he_engine *e = nullptr;
+  int32_t rc = open_common(cfg, tensors, size, rope_cos, rope_sin, max_block, out, &e);
+  const float factor = (float)(0.02 / std::sqrt(4.0 * (65536.0 * 65536.0 - 1.0) / 12.0));
+  if (rc == HE_OK) {
+    const he_config &c = e->c;
+    const int32_t header[7] = {c.dim, c.hidden_dim, c.n_layers, c.n_heads, c.n_kv_heads,
+                               c.shared_classifier ? c.vocab_size : -c.vocab_size, c.seq_len};
+    hipError_t err = hipMemcpy(e->blob, header, 28, hipMemcpyHostToDevice);
+    for (int id = 0; id < HE_T_COUNT && err == hipSuccess; ++id) {
+      if (!present(c, id)) continue;
+      const Shape s = shape_of(c, id);
+      uint8_t *vals = const_cast<uint8_t *>(e->values[id]);
+      if (s.k) {
+        if (s.k % 32) {
+          rc = fail(HE_E_ARG, "synthetic checkpoints take rows of whole groups of 32");
+          break;
+        }
+        err = launch_synth_matrix(vals, const_cast<float *>(e->scales[id]), s.count / s.k, s.k, seed, id, factor,
+                                  c.six, e->stream);
+      } else {
+        err = launch_synth_vector(reinterpret_cast<float *>(vals), s.count, seed, id, factor, id < HE_T_BQ, e->stream);
+      }
+    }
+    if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+    if (err != hipSuccess && rc == HE_OK) rc = fail(HE_E_HIP, std::string("synthesis: ") + hipGetErrorString(err));
+  }
+  if (rc != HE_OK) {
+    destroy(e);
+    return rc;
+  }
+  *out = e;
+  return HE_OK;
+}
+
+int32_t he_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, float *logits) {
+  if (!e) return fail(HE_E_ARG, "engine is null");
+  int32_t rc = run_tokens(e, &token, 1, pos, need_logits != 0);
+  if (rc) return rc;
+  if (need_logits && logits)
+    HIP_TRY(hipMemcpyAsync(logits, e->logits, sizeof(float) * e->c.vocab_size, hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  return HE_OK;
+}
+
+int32_t he_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos) {
+  if (!e || !tokens) return fail(HE_E_ARG, "engine or tokens is null");
+  if (count > e->max_block) return fail(HE_E_ARG, "more tokens than the prompt block");
+  int32_t rc = run_tokens(e, tokens, count, pos, false);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  return HE_OK;
+}
+
+int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, int32_t count, const int32_t *stops,
+                         int32_t n_stops, int32_t *ids, int32_t *n_ids) {
+  if (!e || !ids || !n_ids) return fail(HE_E_ARG, "a required pointer is null");
+  if (count < 1) return fail(HE_E_ARG, "count must be at least 1");
+  if ((int64_t)pos + count > e->c.seq_len) return fail(HE_E_STATE, "the steps run past the context (seq_len)");
+  *n_ids = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    int32_t rc = run_tokens(e, &token, 1, pos + i, true);
+    if (rc) return rc;
+    HIP_TRY(launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream));
+    int32_t best = 0;
+    float value = 0.0f;
+    HIP_TRY(hipMemcpyAsync(&best, e->best_i, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+    HIP_TRY(hipMemcpyAsync(&value, e->best_v, sizeof(float), hipMemcpyDeviceToHost, e->stream));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    if (!std::isfinite(value)) return fail(HE_E_NOTFINITE, "the largest logit is not finite");
+    ids[(*n_ids)++] = best;
+    token = best;
+    bool stop = false;
+    for (int32_t j = 0; j < n_stops; ++j) stop = stop || stops[j] == best;
+    if (stop) break;
+  }
+  return HE_OK;
+}
+
+int32_t he_logits(he_engine *e, float *out) {
+  if (!e || !out) return fail(HE_E_ARG, "a required pointer is null");
+  if (!e->have_logits) return fail(HE_E_STATE, "no step with logits has run");
+  HIP_TRY(hipMemcpyAsync(out, e->logits, sizeof(float) * e->c.vocab_size, hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  return HE_OK;
+}
+
+int32_t he_kv_read(he_engine *e, int32_t from, int32_t count, float *keys, float *values) {
+  if (!e || !keys || !values) return fail(HE_E_ARG, "a required pointer is null");
+  if (from < 0 || count < 0 || (int64_t)from + count > e->c.seq_len) return fail(HE_E_ARG, "positions out of range");
+  const size_t esz = e->c.half_kv ? 2 : 4;
+  std::vector<uint8_t> row((size_t)count * e->kvdim * esz);
+  for (int pass = 0; pass < 2; ++pass) {
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(pass ? e->vals : e->keys);
+    float *dst = pass ? values : keys;
+    for (int32_t l = 0; l < e->c.n_layers; ++l) {
+      HIP_TRY(hipMemcpy(row.data(), src + ((size_t)l * e->c.seq_len + from) * e->kvdim * esz, row.size(),
+                        hipMemcpyDeviceToHost));
+      float *o = dst + (size_t)l * count * e->kvdim;
+      for (size_t i = 0; i < (size_t)count * e->kvdim; ++i) {
+        if (esz == 4) {
+          std::memcpy(&o[i], &row[i * 4], 4);
+        } else {
+          uint16_t h;
+          std::memcpy(&h, &row[i * 2], 2);
+          int32_t bits = ((int32_t)(int16_t)h << 13) & (int32_t)0x8fffffff;
+          float f;
+          std::memcpy(&f, &bits, 4);
+          o[i] = f * 5.192296858534828e33f;
+        }
+      }
+    }
+  }
+  return HE_OK;
+}
+
+int32_t he_checkpoint_read(he_engine *e, uint64_t offset, uint64_t length, void *out) {
+  if (!e || !out) return fail(HE_E_ARG, "a required pointer is null");
+  if (offset + length > e->size) return fail(HE_E_ARG, "the bytes run past the checkpoint");
+  uint8_t *o = reinterpret_cast<uint8_t *>(out);
+  while (length) {
+    const Region *hit = nullptr;
+    for (const Region &r : e->regions)
+      if (offset >= r.file && offset < r.file + r.bytes) hit = &r;
+    if (!hit) return fail(HE_E_ARG, "offset outside the checkpoint");
+    const uint64_t n = std::min(length, hit->file + hit->bytes - offset);
+    HIP_TRY(hipMemcpy(o, e->blob + hit->dev + (offset - hit->file), n, hipMemcpyDeviceToHost));
+    o += n;
+    offset += n;
+    length -= n;
+  }
+  return HE_OK;
+}
+
+int32_t he_prompt_block(he_engine *e) { return e ? e->max_block : 0; }
+
+uint64_t he_device_bytes(he_engine *e) { return e ? e->device_bytes : 0; }
+
+int32_t he_close(he_engine *e) {
+  if (!e) return HE_OK;
+  (void)hipStreamSynchronize(e->stream);
+  destroy(e);
+  return HE_OK;
+}
+
+// ---- kernel level ----
+
+int32_t hk_quantize_x(void *xq, void *xs, const void *x, int32_t m, int32_t n, int32_t bias, void *stream) {
+  if (!xq || !xs || !x || m < 1 || n < 32 || n % 32) return fail(HE_E_ARG, "hk_quantize_x: bad arguments");
+  if (bias != 0 && bias != 64) return fail(HE_E_ARG, "bias must be 0 or 64");
+  HIP_TRY(launch_quantize(reinterpret_cast<int8_t *>(xq), reinterpret_cast<float *>(xs),
+                          reinterpret_cast<const float *>(x), m, n, n, n, n / 32, bias,
+                          reinterpret_cast<hipStream_t>(stream)));
+  return HE_OK;
+}
+
+namespace {
+int32_t matmul_args(MatArgs &a, void *y, const void *xq, const void *xs, const void *w, const void *ws, int32_t m,
+                    int32_t rows, int32_t k, int32_t bias) {
+  if (!xq || !w || m < 1 || rows < 1 || k < 32 || k % 32) return fail(HE_E_ARG, "matmul: bad arguments");
+  if (bias != 0 && bias != 64) return fail(HE_E_ARG, "bias must be 0 or 64");
+  a = MatArgs{};
+  a.nseg = 1;
+  a.seg[0] = {reinterpret_cast<const uint8_t *>(w), reinterpret_cast<const float *>(ws), reinterpret_cast<float *>(y),
+              rows, rows, 0};
+  a.total_rows = rows;
+  a.xq = reinterpret_cast<const int8_t *>(xq);
+  a.xs = reinterpret_cast<const float *>(xs);
+  a.xq_stride = k;
+  a.xs_stride = k / 32;
+  a.k = k;
+  return HE_OK;
+}
+}  // namespace
+
+int32_t hk_matmul(void *y, const void *xq, const void *xs, const void *w, const void *ws, int32_t m, int32_t rows,
+                  int32_t k, int32_t bias, int32_t six, void *stream) {
+  MatArgs base;
+  int32_t rc = matmul_args(base, y, xq, xs, w, ws, m, rows, k, bias);
+  if (rc) return rc;
+  if (!y || !xs || !ws) return fail(HE_E_ARG, "matmul: a required pointer is null");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int32_t t0 = 0; t0 < m; t0 += 8) {
+    MatArgs a = base;
+    a.m = std::min(8, m - t0);
+    a.xq = base.xq + (int64_t)t0 * k;
+    a.xs = base.xs + (int64_t)t0 * (k / 32);
+    a.seg[0].y = base.seg[0].y + (int64_t)t0 * rows;
+    HIP_TRY(launch_gemv(a, six != 0, bias == 64, s));
+  }
+  return HE_OK;
+}
+
+int32_t hk_group_sums(void *s, const void *xq, const void *w, int32_t m, int32_t rows, int32_t k, int32_t bias,
+                      int32_t six, int32_t gemm, void *stream) {
+  MatArgs base;
+  int32_t rc = matmul_args(base, nullptr, xq, nullptr, w, nullptr, m, rows, k, bias);
+  if (rc) return rc;
+  if (!s) return fail(HE_E_ARG, "sums is null");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t per_token = (int64_t)rows * (k / 32) * (bias ? 1 : 4);
+  for (int32_t t0 = 0; t0 < m; t0 += 8) {
+    MatArgs a = base;
+    a.m = std::min(8, m - t0);
+    a.xq = base.xq + (int64_t)t0 * k;
+    a.sums = reinterpret_cast<int32_t *>(s) + t0 * per_token;
+    HIP_TRY(launch_gemv(a, six != 0, bias == 64, st));
+  }
+  (void)gemm;
+  return HE_OK;
+}
+
+}  // extern "C"

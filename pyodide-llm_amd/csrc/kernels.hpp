@@ -1,0 +1,92 @@
+// kernels.hpp — the launch interfaces of the gfx950 kernels (host side). Every launch takes device pointers and a
+// stream; shapes are checked by the callers in engine.cpp / the hk_* entry points before a launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ple {
+
+// one matrix of a GEMV/GEMM launch: rows [rows][K] int8 (or int6 groups of 24 bytes), scales [rows][K/32]; the
+// output y[t * y_stride + r] for token t, row r (accumulate: y = y + result, the residual add of kernels/kernel.ts:
+// 691-693 fused)
+struct MatSeg {
+  const uint8_t *w;
+  const float *ws;
+  float *y;
+  int32_t rows;
+  int32_t y_stride;
+  int32_t accumulate;
+};
+
+struct MatArgs {
+  MatSeg seg[3];
+  int32_t nseg;
+  int32_t total_rows;
+  const int8_t *xq;  // activations of quantize_x(bias), [m][xq_stride]
+  const float *xs;   // their scales, [m][xs_stride]
+  int32_t xq_stride;
+  int32_t xs_stride;
+  int32_t k;
+  int32_t m;
+  int32_t *sums;  // group-sum output (hk_group_sums) or null
+};
+
+// decode GEMV, m <= 8 tokens: exact int32 group sums, the reference's float32 order
+hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
+// prefill GEMM on i8 MFMA, any m: the same bits as launch_gemv per (token, row)
+hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
+bool gemm_supported(int32_t k, bool six);
+
+// quantize_x over m rows of n (x_stride apart) into xq (xq_stride) / xs (xs_stride)
+hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n, int32_t x_stride,
+                           int32_t xq_stride, int32_t xs_stride, int32_t bias, hipStream_t s);
+// rmsnorm then quantize_x, m tokens; out (optional) receives the normalized float32 row
+hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
+                                int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
+                                float eps, int32_t bias, hipStream_t s);
+// swiglu(h1, h3) then quantize_x, m tokens
+hipError_t launch_swiglu_quant(int8_t *xq, float *xs, float *out, const float *h1, const float *h3, int32_t m,
+                               int32_t n, int32_t h_stride, int32_t xq_stride, int32_t xs_stride, int32_t bias,
+                               hipStream_t s);
+// embedding rows of m tokens (int8 or int6 table) into x (x_stride apart)
+hipError_t launch_embed(float *x, const int32_t *tokens, const uint8_t *table, const float *scales, int32_t m,
+                        int32_t dim, int32_t x_stride, int32_t group, bool six, hipStream_t s);
+// per token: + bias (optional), RoPE on q and k at pos0 + t, k and v into the cache (f32 or f16)
+struct QkvPost {
+  float *q;
+  float *k;
+  float *v;
+  int32_t q_stride, kv_stride;
+  const float *bq, *bk, *bv;
+  const float *cos_t, *sin_t;  // [seq_len][hs/2]
+  void *kcache, *vcache;       // this layer's [seq_len][kv_dim]
+  int32_t nh, nkv, hs, pos0, m, half;
+};
+hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s);
+
+// attention of m tokens at positions pos0.. over the cache rows 0..pos0+t; out [m][out_stride]
+struct AttnArgs {
+  const float *q;
+  int32_t q_stride;
+  const void *kcache, *vcache;
+  float *out;
+  int32_t out_stride;
+  float *scores;  // [m][nh][seq_len]
+  float *partial; // [m][nh][seq_len / 4 + 4][hs] weighted-value blocks
+  float *tilemax; // [m][nh][seq_len / 64 + 1]
+  int32_t nh, nkv, hs, pos0, m, seq_len, half;
+};
+hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+
+// greedy: the first index of the largest logit into *out (and the value into *value)
+hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
+                         hipStream_t s);
+
+// device synthesis of a checkpoint (the oracle's or_synth_checkpoint bits)
+hipError_t launch_synth_matrix(uint8_t *values, float *scales, int64_t rows, int32_t k, uint64_t seed, int32_t stream,
+                               float factor, bool six, hipStream_t s);
+hipError_t launch_synth_vector(float *out, int64_t n, uint64_t seed, int32_t stream, float factor, bool ones,
+                               hipStream_t s);
+
+}  // namespace ple

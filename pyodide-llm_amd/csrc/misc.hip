@@ -1,0 +1,353 @@
+// misc.hip — the per-token elementwise work around the matmuls, each in the reference's float32 order:
+//   quantize_x (kernels/kernel.ts:129-156), rmsnorm (:330-342) then quantize_x, swiglu (:654-667) then quantize_x,
+//   embed (public/forward.js:962-973 with valueAt :692-696), the q/k/v bias add (:691-693, public/forward.js:1038-1042),
+//   rope (:344-357) and the KV-cache write (to_f16 :570-599 or a copy, public/forward.js:998-1006), argmax (:695-699),
+//   and the device twin of the oracle's synthetic checkpoint.
+#pragma clang fp contract(off)
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ple {
+
+namespace {
+
+// one group of 32 a half-wave: amax (order-free), scale = f32(amax / qmax), inv = scale > 0 ? f32(1 / scale) : 0
+__device__ __forceinline__ void quantize_group(float v, int8_t *xq, float *xs, int j, int g, int32_t bias) {
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  const float amax = wave_max32(__builtin_fabsf(v));
+  const float scale = amax / qmax;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  xq[j] = quant_value(v, inv, bias);
+  if ((threadIdx.x & 31) == 0) xs[g] = scale;
+}
+
+__global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n,
+                                                       int32_t x_stride, int32_t xq_stride, int32_t xs_stride,
+                                                       int32_t bias) {
+  const int groups = n / GS;
+  const int64_t gid = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (gid >= (int64_t)m * groups) return;  // whole half-waves leave together
+  const int t = (int)(gid / groups), g = (int)(gid % groups), j = g * GS + (threadIdx.x & 31);
+  quantize_group(x[(int64_t)t * x_stride + j], xq + (int64_t)t * xq_stride, xs + (int64_t)t * xs_stride, j, g, bias);
+}
+
+// rmsnorm of one token a block: the squares in four lanes (j % 4) added in order by four threads, hsum
+// ((l0 + l1) + l2) + l3, the tail in order; s = f32(1 / f32(sqrt(f32(ss / n) + eps))); out = w * (s * x); then
+// quantize_x of out
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *xs, float *out, const float *x,
+                                                            const float *w, int32_t n, int32_t x_stride,
+                                                            int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
+                                                            float eps, int32_t bias) {
+  extern __shared__ float sm[];
+  float *xv = sm;       // n
+  float *sq = sm + n;   // n4, transposed: lane k's squares side by side
+  __shared__ float part[4];
+  __shared__ float sval;
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float *xt = x + (int64_t)t * x_stride;
+  const int n4 = n & ~3, q4 = n4 >> 2;
+  for (int j = tid; j < n; j += 256) {
+    const float v = xt[j];
+    xv[j] = v;
+    if (j < n4) sq[(j & 3) * q4 + (j >> 2)] = v * v;
+  }
+  __syncthreads();
+  if (tid < 4) {
+    const float *c = sq + tid * q4;
+    float acc = 0.0f;
+    int i = 0;
+    if ((q4 & 3) == 0 && ((tid * q4) & 3) == 0) {
+      const float4 *c4 = reinterpret_cast<const float4 *>(c);
+      for (; i < q4; i += 4) {
+        const float4 v = c4[i >> 2];
+        acc = acc + v.x;
+        acc = acc + v.y;
+        acc = acc + v.z;
+        acc = acc + v.w;
+      }
+    }
+    for (; i < q4; ++i) acc = acc + c[i];
+    part[tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float ss = ((part[0] + part[1]) + part[2]) + part[3];
+    for (int j = n4; j < n; ++j) ss = ss + xv[j] * xv[j];
+    sval = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+  }
+  __syncthreads();
+  const float s = sval;
+  int8_t *q = xq + (int64_t)t * xq_stride;
+  float *sc = xs + (int64_t)t * xs_stride;
+  for (int g = tid >> 5; g < n / GS; g += 8) {
+    const int j = g * GS + (tid & 31);
+    const float o = w[j] * (s * xv[j]);
+    if (out) out[(int64_t)t * out_stride + j] = o;
+    quantize_group(o, q, sc, j, g, bias);
+  }
+}
+
+// swiglu: h1 / (1 + vexp(-h1)) * h3 (the scalar tail's fexp gives the same bits), then quantize_x
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(int8_t *xq, float *xs, float *out, const float *h1,
+                                                           const float *h3, int32_t m, int32_t n, int32_t h_stride,
+                                                           int32_t xq_stride, int32_t xs_stride, int32_t bias) {
+  const int groups = n / GS;
+  const int64_t gid = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (gid >= (int64_t)m * groups) return;
+  const int t = (int)(gid / groups), g = (int)(gid % groups), j = g * GS + (threadIdx.x & 31);
+  const float v = h1[(int64_t)t * h_stride + j];
+  const float o = v / (1.0f + vexp(-v)) * h3[(int64_t)t * h_stride + j];
+  if (out) out[(int64_t)t * h_stride + j] = o;
+  quantize_group(o, xq + (int64_t)t * xq_stride, xs + (int64_t)t * xs_stride, j, g, bias);
+}
+
+// embed: x_i = f32(int8 * scale of its group) for the token's row
+__global__ __launch_bounds__(256) void embed_kernel(float *x, const int32_t *tokens, const uint8_t *table,
+                                                    const float *scales, int32_t dim, int32_t x_stride, int32_t group,
+                                                    int32_t six) {
+  const int t = blockIdx.y;
+  const int64_t row = (int64_t)tokens[t] * dim;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256) {
+    const int64_t at = row + i;
+    int32_t v;
+    if (six) {
+      const uint8_t *b = table + (at >> 5) * 24;
+      const int j = (int)(at & 31);
+      const int low = j < 16 ? (b[j] & 15) : (b[j - 16] >> 4);
+      const int top = (b[16 + (j & 7)] >> (2 * (j >> 3))) & 3;
+      v = (int8_t)(uint8_t)((low | (top << 4)) << 2);
+    } else {
+      v = (int8_t)table[at];
+    }
+    x[(int64_t)t * x_stride + i] = (float)v * scales[at / group];
+  }
+}
+
+// per token: bias (q, k, v), rope on q and k at its position, k and v into the cache
+__global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPost a) {
+  const int t = blockIdx.y;
+  const int pos = a.pos0 + t;
+  const int qdim = a.nh * a.hs, kvdim = a.nkv * a.hs, half = a.hs / 2;
+  float *q = a.q + (int64_t)t * a.q_stride, *k = a.k + (int64_t)t * a.kv_stride, *v = a.v + (int64_t)t * a.kv_stride;
+  const float *cs = a.cos_t + (int64_t)pos * half, *sn = a.sin_t + (int64_t)pos * half;
+  const int pairs = (qdim + kvdim) / 2;
+  for (int p = blockIdx.x * 256 + threadIdx.x; p < pairs + kvdim; p += gridDim.x * 256) {
+    if (p < pairs) {
+      const bool isq = p < qdim / 2;
+      float *base = isq ? q : k;
+      const float *bias = isq ? a.bq : a.bk;
+      const int i = 2 * (isq ? p : p - qdim / 2);  // the pair's first value
+      float v0 = base[i], v1 = base[i + 1];
+      if (bias) {
+        v0 = v0 + bias[i];
+        v1 = v1 + bias[i + 1];
+      }
+      const int ci = (i % a.hs) >> 1;
+      const float c = cs[ci], s = sn[ci];
+      const float o0 = v0 * c - v1 * s, o1 = v0 * s + v1 * c;
+      base[i] = o0;
+      base[i + 1] = o1;
+      if (!isq) {
+        const int64_t at = (int64_t)pos * kvdim + i;
+        if (a.half) {
+          reinterpret_cast<uint16_t *>(a.kcache)[at] = to_f16(o0);
+          reinterpret_cast<uint16_t *>(a.kcache)[at + 1] = to_f16(o1);
+        } else {
+          reinterpret_cast<float *>(a.kcache)[at] = o0;
+          reinterpret_cast<float *>(a.kcache)[at + 1] = o1;
+        }
+      }
+    } else {
+      const int i = p - pairs;
+      float o = v[i];
+      if (a.bv) o = o + a.bv[i];
+      v[i] = o;
+      const int64_t at = (int64_t)pos * kvdim + i;
+      if (a.half) reinterpret_cast<uint16_t *>(a.vcache)[at] = to_f16(o);
+      else reinterpret_cast<float *>(a.vcache)[at] = o;
+    }
+  }
+}
+
+// argmax, first of the largest: per block the best (value, index), then one block over the blocks; the host reports a
+// winner that is not finite (NOT_FINITE)
+// NumPy's argmax order (public/llama2_numpy.py:1521-1527): a NaN is the largest, the first of equals wins; on finite
+// logits this is kernels/kernel.ts:695-699's first index of the largest
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  if (v != v) return bv == bv || i < bi;
+  if (bv != bv) return false;
+  return v > bv || (v == bv && i < bi);
+}
+__global__ __launch_bounds__(256) void argmax_stage(float *ov, int32_t *oi, const float *x, const int32_t *xi,
+                                                    int32_t n) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  for (int j = blockIdx.x * 256 + threadIdx.x; j < n; j += gridDim.x * 256) {
+    const float v = x[j];
+    const int i = xi ? xi[j] : j;
+    if (bi == 0x7fffffff || better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) {
+      const float v = sv[threadIdx.x + w];
+      const int i = si[threadIdx.x + w];
+      if (i != 0x7fffffff && (si[threadIdx.x] == 0x7fffffff || better(v, i, sv[threadIdx.x], si[threadIdx.x]))) {
+        sv[threadIdx.x] = v;
+        si[threadIdx.x] = i;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    ov[blockIdx.x] = sv[0];
+    oi[blockIdx.x] = si[0];
+  }
+}
+
+// ---- the device twin of the oracle's synthetic checkpoint (oracle/oracle.c or_synth_value, or_quantize,
+// or_quantize6, or_pack6): a splitmix64 hash of (seed, stream, index), four 16-bit quarters summed, one float multiply
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z ^= z >> 30;
+  z *= 0xBF58476D1CE4E5B9ull;
+  z ^= z >> 27;
+  z *= 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return z;
+}
+__device__ __forceinline__ float synth_value(uint64_t key, uint64_t index, float factor) {
+  const uint64_t r = mix64(key + index * 0x9E3779B97F4A7C15ull);
+  const int32_t s = (int32_t)(r & 0xffff) + (int32_t)((r >> 16) & 0xffff) + (int32_t)((r >> 32) & 0xffff) +
+                    (int32_t)(r >> 48);
+  return (float)(s - 131070) * factor;
+}
+
+// one group of 32 a half-wave: the values, then quantize() (int8, scale f32(amax / 127)) or quantize6()+pack6()
+__global__ __launch_bounds__(256) void synth_matrix_kernel(uint8_t *values, float *scales, int64_t groups,
+                                                           uint64_t key, float factor, int32_t six) {
+  const int64_t g = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (g >= groups) return;
+  const int j = threadIdx.x & 31;
+  const float v = synth_value(key, (uint64_t)(g * GS + j), factor);
+  const float amax = wave_max32(__builtin_fabsf(v));
+  if (!six) {
+    const float scale = amax / 127.0f;
+    const float inverse = scale > 0 ? 1.0f / scale : 0.0f;
+    values[g * GS + j] = (uint8_t)(int8_t)__builtin_rintf(v * inverse);
+    if (j == 0) scales[g] = scale;
+    return;
+  }
+  const float scale = amax / 31.0f;
+  const float inverse = scale > 0 ? 1.0f / scale : 0.0f;
+  float r = __builtin_rintf(v * inverse);
+  r = r < -32.0f ? -32.0f : (r > 31.0f ? 31.0f : r);
+  const uint32_t b = (uint32_t)(((int32_t)r * 4) & 0xff) >> 2 & 63;  // the six bits
+  // pack6: byte j (< 16) = low nibble of j | low nibble of j + 16 << 4; byte 16 + k = tops of k, k+8, k+16, k+24
+  const uint32_t other = __shfl_xor(b, 16, 64);  // lane j < 16 gets value j + 16's bits
+  uint8_t *o = values + g * 24;
+  if (j < 16) o[j] = (uint8_t)((b & 15) | ((other & 15) << 4));
+  const uint32_t t1 = __shfl(b, (threadIdx.x & 32) + (j & 7) + 8, 64);
+  const uint32_t t2 = __shfl(b, (threadIdx.x & 32) + (j & 7) + 16, 64);
+  const uint32_t t3 = __shfl(b, (threadIdx.x & 32) + (j & 7) + 24, 64);
+  const uint32_t t0 = __shfl(b, (threadIdx.x & 32) + (j & 7), 64);
+  if (j < 8) o[16 + j] = (uint8_t)((t0 >> 4) | ((t1 >> 4) << 2) | ((t2 >> 4) << 4) | ((t3 >> 4) << 6));
+  if (j == 0) scales[g] = scale / 4.0f;
+}
+
+__global__ __launch_bounds__(256) void synth_vector_kernel(float *out, int64_t n, uint64_t key, float factor,
+                                                           int32_t ones) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    out[i] = ones ? 1.0f : synth_value(key, (uint64_t)i, factor);
+}
+
+uint64_t synth_key(uint64_t seed, int32_t stream) {
+  uint64_t z = seed * 0x9E3779B97F4A7C15ull ^ ((uint64_t)(uint32_t)stream * 0xD1B54A32D192ED03ull);
+  z ^= z >> 30;
+  z *= 0xBF58476D1CE4E5B9ull;
+  z ^= z >> 27;
+  z *= 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return z;
+}
+
+int blocks_for(int64_t items, int64_t per_block, int64_t cap = 1 << 20) {
+  int64_t b = (items + per_block - 1) / per_block;
+  if (b < 1) b = 1;
+  return (int)(b > cap ? cap : b);
+}
+
+}  // namespace
+
+hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n, int32_t x_stride,
+                           int32_t xq_stride, int32_t xs_stride, int32_t bias, hipStream_t s) {
+  const int64_t groups = (int64_t)m * (n / GS);
+  hipLaunchKernelGGL(quantize_kernel, dim3(blocks_for(groups, 8)), dim3(256), 0, s, xq, xs, x, m, n, x_stride,
+                     xq_stride, xs_stride, bias);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
+                                int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
+                                float eps, int32_t bias, hipStream_t s) {
+  const size_t lds = sizeof(float) * (size_t)(2 * n);
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m), dim3(256), lds, s, xq, xs, out, x, w, n, x_stride, xq_stride,
+                     xs_stride, out_stride, eps, bias);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_quant(int8_t *xq, float *xs, float *out, const float *h1, const float *h3, int32_t m,
+                               int32_t n, int32_t h_stride, int32_t xq_stride, int32_t xs_stride, int32_t bias,
+                               hipStream_t s) {
+  const int64_t groups = (int64_t)m * (n / GS);
+  hipLaunchKernelGGL(swiglu_quant_kernel, dim3(blocks_for(groups, 8)), dim3(256), 0, s, xq, xs, out, h1, h3, m, n,
+                     h_stride, xq_stride, xs_stride, bias);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(float *x, const int32_t *tokens, const uint8_t *table, const float *scales, int32_t m,
+                        int32_t dim, int32_t x_stride, int32_t group, bool six, hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(dim, 256, 64), m), dim3(256), 0, s, x, tokens, table, scales, dim,
+                     x_stride, group, (int32_t)six);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s) {
+  const int64_t items = (int64_t)(a.nh * a.hs + a.nkv * a.hs) / 2 + a.nkv * a.hs;
+  hipLaunchKernelGGL(qkv_post_kernel, dim3(blocks_for(items, 256, 64), a.m), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
+                         hipStream_t s) {
+  const int blocks = 256;
+  hipLaunchKernelGGL(argmax_stage, dim3(blocks), dim3(256), 0, s, scratch_v, scratch_i, x, (const int32_t *)nullptr,
+                     n);
+  hipLaunchKernelGGL(argmax_stage, dim3(1), dim3(256), 0, s, value, out, (const float *)scratch_v,
+                     (const int32_t *)scratch_i, blocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_synth_matrix(uint8_t *values, float *scales, int64_t rows, int32_t k, uint64_t seed, int32_t stream,
+                               float factor, bool six, hipStream_t s) {
+  const int64_t groups = rows * (k / GS);
+  hipLaunchKernelGGL(synth_matrix_kernel, dim3(blocks_for(groups, 8, 1ll << 31)), dim3(256), 0, s, values, scales,
+                     groups, synth_key(seed, stream), factor, (int32_t)six);
+  return hipGetLastError();
+}
+
+hipError_t launch_synth_vector(float *out, int64_t n, uint64_t seed, int32_t stream, float factor, bool ones,
+                               hipStream_t s) {
+  hipLaunchKernelGGL(synth_vector_kernel, dim3(blocks_for(n, 256, 4096)), dim3(256), 0, s, out, n,
+                     synth_key(seed, stream), factor, (int32_t)ones);
+  return hipGetLastError();
+}
+
+}  // namespace ple

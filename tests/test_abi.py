@@ -1,0 +1,49 @@
+"""The drop-in boundary without a GPU: the built library loads and exports every entry point include/*.h declares,
+and the package's plan conversion refuses the forms the engine does not run (as public/forward.js throws)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from paths import REPO, package
+
+
+def declared():
+    names = []
+    for header in glob.glob(os.path.join(REPO, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(he_[a-z_]+|hk_[a-z_]+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_the_engine_and_kernel_entry_points():
+    names = declared()
+    for name in ("he_open", "he_forward", "he_forward_many", "he_generate_many", "he_logits", "he_kv_read",
+                 "he_close", "hk_matmul", "hk_quantize_x", "hk_group_sums"):
+        assert name in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(package().hip_engine.LIBRARY)
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_plan_conversion_takes_the_reference_plan_and_refuses_other_forms():
+    pk = package()
+    tensors = {name: {"kind": "int8", "offset": 28 + i * 1000, "shape": [1], "group": 32, "scales": 28 + i * 1000 + 500}
+               for i, name in enumerate(("token_embedding_table", "wq", "wk", "wv", "wo", "w1", "w2", "w3"))}
+    for i, name in enumerate(("rms_att_weight", "rms_ffn_weight", "rms_final_weight")):
+        tensors[name] = {"kind": "f32", "offset": 50000 + i * 100, "shape": [1], "group": 0, "scales": 0}
+    plan = {"arch": "llama", "dim": 64, "hidden_dim": 128, "n_layers": 2, "n_heads": 4, "n_kv_heads": 2,
+            "head_size": 16, "vocab_size": 320, "seq_len": 32, "rotary": 0, "parallel_residual": False,
+            "kv_start": 256, "rms_norm_eps": 1e-5, "shared_classifier": True, "int8": True, "relaxed": True,
+            "tensors": tensors, "derived": {}, "outliers": [], "half_kv": True, "form": {}}
+    cfg, t = pk.plan_to_config(plan)
+    assert (cfg.dim, cfg.n_kv_heads, cfg.relaxed, cfg.half_kv, cfg.six, cfg.qkv_bias) == (64, 2, 1, 1, 0, 0)
+    assert t[pk.T["wcls"]].offset == tensors["token_embedding_table"]["offset"]
+    for change in ({"arch": "gpt2"}, {"outliers": [3]}, {"int8": False}, {"parallel_residual": True}):
+        with pytest.raises(pk.HipError):
+            pk.plan_to_config({**plan, **change})

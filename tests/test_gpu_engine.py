@@ -1,0 +1,100 @@
+"""The engine (include/pyodide_llm_hip.h he_*) against the oracle's run() on the same checkpoint bytes: logits and
+the KV cache to the bit at every position, prompt blocks equal to one token at a time, the device-made checkpoint
+equal to the host-made one, and greedy generation token-identical, on models of the reference's shapes."""
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+from paths import package
+
+pytestmark = pytest.mark.gpu
+
+MODELS = {
+    "tiny_gqa": (dict(dim=64, hidden_dim=128, n_layers=2, n_heads=4, n_kv_heads=2, head_size=16, vocab_size=320,
+                      seq_len=48, shared_classifier=1), 10000.0),
+    "tiny_qwen_int6": (dict(dim=64, hidden_dim=96, n_layers=2, n_heads=4, n_kv_heads=1, head_size=16, vocab_size=288,
+                            seq_len=48, shared_classifier=0, six=1, qkv_bias=1), 1000000.0),
+    "stories15m": (dict(dim=288, hidden_dim=768, n_layers=6, n_heads=6, n_kv_heads=6, head_size=48, vocab_size=32000,
+                        seq_len=256, shared_classifier=1), 10000.0),
+}
+
+
+def build(name, **extra):
+    fields, theta = MODELS[name]
+    cfg = ol.config(**{**fields, **extra})
+    tensors, size = ol.places(cfg)
+    ck = ol.synth_checkpoint(cfg, tensors, size, seed=7)
+    cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, theta)
+    return cfg, tensors, ck, cos, sin, size
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("name", sorted(MODELS))
+@pytest.mark.parametrize("relaxed", [1, 0])
+@pytest.mark.parametrize("half_kv", [0, 1])
+def test_forward_logits_and_cache_bits(name, relaxed, half_kv):
+    cfg, tensors, ck, cos, sin, _ = build(name, relaxed=relaxed, half_kv=half_kv)
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    rng = np.random.default_rng(5)
+    tokens = rng.integers(0, cfg.vocab_size, size=12)
+    for pos, tok in enumerate(tokens):
+        ref.run([int(tok)], pos, True)
+        eng.forward(int(tok), pos, True)
+        assert same_bits(eng.logits(), ref.logits()), pos
+    k_ref, v_ref = ref.kv(0, len(tokens))
+    kv = eng.keysAndValues(0, len(tokens))
+    assert same_bits(kv["keys"], k_ref.reshape(-1)) and same_bits(kv["values"], v_ref.reshape(-1))
+    eng.release()
+
+
+@pytest.mark.parametrize("name", ["tiny_gqa", "stories15m"])
+def test_prompt_blocks_equal_one_at_a_time(name):
+    cfg, tensors, ck, cos, sin, _ = build(name)
+    pk = package()
+    rng = np.random.default_rng(6)
+    tokens = [int(t) for t in rng.integers(0, cfg.vocab_size, size=40)]
+    one = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    for pos, tok in enumerate(tokens):
+        one.forward(tok, pos, pos == len(tokens) - 1)
+    many = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    many.forwardMany(tokens[:-1], 0)
+    many.forward(tokens[-1], len(tokens) - 1, True)
+    assert same_bits(one.logits(), many.logits())
+    a, b = one.keysAndValues(0, len(tokens)), many.keysAndValues(0, len(tokens))
+    assert same_bits(a["keys"], b["keys"]) and same_bits(a["values"], b["values"])
+
+
+@pytest.mark.parametrize("name", sorted(MODELS))
+def test_device_checkpoint_equals_host_checkpoint(name):
+    cfg, tensors, ck, cos, sin, size = build(name)
+    pk = package()
+    eng = pk.open_synthetic(cfg, tensors, size, 7, cos, sin, max_block=8)
+    import ctypes
+    out = np.zeros(size, dtype=np.uint8)
+    pk.hip_engine.check(pk.library().he_checkpoint_read(eng._h, 0, size, ctypes.c_void_p(out.ctypes.data)))
+    assert np.array_equal(out, ck)
+
+
+def test_greedy_generation_matches_the_oracle():
+    """configs[0]'s shape: a 32-token prompt through forwardMany, then 128 greedy tokens (stop tokens off)"""
+    cfg, tensors, ck, cos, sin, _ = build("stories15m", half_kv=1)
+    rng = np.random.default_rng(2)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=32)]
+    steps = 32 + 128
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    want, want_logits = ref.generate(prompt, steps)
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    eng.forwardMany([1] + prompt[:-1], 0)
+    got, token, pos = [], prompt[-1], len(prompt)
+    while pos < steps:
+        ids = eng.generateMany(token, pos, [], 0, min(16, steps - pos), 0.0, 0.9, 1.0, [], [])
+        got += ids
+        token, pos = ids[-1], pos + len(ids)
+    assert got == [int(t) for t in want]
+    assert same_bits(eng.logits(), want_logits)

@@ -1,0 +1,88 @@
+"""The HIP kernels through the C ABI against the oracle, to the bit: quantize_x, the exact int32 group sums and the
+float32 outputs of the decode GEMV and the prefill GEMM (matmul_q8r / q8 / q6r / q6), at the reference's
+known-answer sizes and at the standalone matmul's full sizes (K=4096, N in {4096, 14336}, M in {1, 4, 16, 512})."""
+import numpy as np
+import pytest
+
+import gpu_lib as gl
+import oracle_lib as ol
+
+pytestmark = pytest.mark.gpu
+
+
+def weights(rows, k, six, seed=3):
+    x = ol.synth(rows * k, seed=seed, stream=2, sigma=0.02).reshape(rows, k)
+    if six:
+        q, s = ol.quantize6(x)
+        return ol.pack6(q).reshape(rows, k // 32 * 24), s.reshape(rows, k // 32)
+    q, s = ol.quantize(x)
+    return q, s.reshape(rows, k // 32)
+
+
+def activations(m, k, bias, seed=1):
+    x = ol.synth(m * k, seed=seed, stream=9, sigma=1.0).reshape(m, k)
+    return ol.quantize_x(x, bias)
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("bias", [64, 0])
+@pytest.mark.parametrize("n", [32, 288, 4096, 14336])
+def test_quantize_x(bias, n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((5, n)) * rng.uniform(0.01, 30, (5, 1))).astype(np.float32)
+    x[0, :32] = 0.0
+    x[1, 32:64] = 1e-40 if n > 32 else 0.0
+    q, s = gl.quantize_x(x, bias)
+    q0, s0 = ol.quantize_x(x, bias)
+    assert np.array_equal(q, q0) and same_bits(s, s0)
+
+
+CASES = [(k, rows, m) for k in (32, 96, 288, 1056, 4096) for rows, m in ((37, 1), (64, 3), (130, 8))]
+
+
+@pytest.mark.parametrize("six", [0, 1])
+@pytest.mark.parametrize("bias", [64, 0])
+@pytest.mark.parametrize("k,rows,m", CASES)
+def test_gemv_bits(k, rows, m, bias, six):
+    w, ws = weights(rows, k, six)
+    xq, xs = activations(m, k, bias)
+    want = ol.matmul(xq, xs, w, ws, rows, k, bias, six)
+    got = gl.matmul(xq, xs, w, ws, rows, k, bias, six)
+    assert same_bits(got, want)
+    sums = gl.group_sums(xq, w, rows, k, bias, six)
+    assert np.array_equal(sums, ol.group_sums(xq, w, rows, k, bias, six))
+
+
+@pytest.mark.parametrize("n", [4096, 14336])
+@pytest.mark.parametrize("m", [1, 4, 16, 512])
+def test_standalone_matmul_full_size(n, m):
+    """K=4096, N in {4096, 14336}, M in {1, 4, 16, 512}: weights N(0, 0.02) by the reference's quantize(), activations
+    N(0, 1) by quantize_x(bias 64); every output to the bit and every group sum exact"""
+    k = 4096
+    w, ws = weights(n, k, 0, seed=11)
+    xq, xs = activations(m, k, 64, seed=12)
+    want = ol.matmul(xq, xs, w, ws, n, k, 64, 0)
+    got = gl.matmul(xq, xs, w, ws, n, k, 64, 0)
+    assert same_bits(got, want)
+    if m <= 16:
+        assert np.array_equal(gl.group_sums(xq, w, n, k, 64, 0), ol.group_sums(xq, w, n, k, 64, 0))
+
+
+def test_extremes_of_int8_equal_float64():
+    """tests/forward-check.mjs:244-276 on the device: rows of -128 and 127 against activations 127 and 1, scales
+    powers of two: the float32 result is the exact float64 sum"""
+    rows, groups = 8, 5
+    n = groups * 32
+    rng = np.random.default_rng(3)
+    w = rng.integers(-128, 128, size=(rows, n)).astype(np.int8)
+    w[0], w[1] = -128, 127
+    w[2, ::2], w[2, 1::2] = -128, 127
+    xq = np.stack([np.full(n, 127), np.ones(n), np.where(np.arange(n) & 1, 1, 127), rng.integers(1, 128, n)]).astype(np.int8)
+    xs = np.stack([np.full(groups, 2.0 ** -(2 + t)) for t in range(4)]).astype(np.float32)
+    ws = np.full((rows, groups), 2.0 ** -7, dtype=np.float32)
+    got = gl.matmul(xq, xs, w, ws, rows, n, 64, 0)
+    want = (w.astype(np.float64)[None] * (xq.astype(np.float64)[:, None] - 64)).sum(-1) * 2.0 ** -7 * xs[:, :1]
+    assert np.array_equal(got.astype(np.float64), want)
