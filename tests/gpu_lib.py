@@ -1,32 +1,64 @@
-"""The kernel-level C ABI (hk_*) driven from NumPy through device buffers that torch allocates (torch is plumbing
-here: memory and the default stream)."""
+"""The kernel-level C ABI (hk_*) driven from NumPy through device buffers from the HIP runtime (hipMalloc/hipMemcpy
+over ctypes: plumbing for the tests, on the default stream)."""
 import ctypes
 
 import numpy as np
 
 from paths import package
 
-
-def torch_cuda():
-    import torch
-    if not torch.cuda.is_available():
-        raise RuntimeError("no GPU")
-    return torch
+_hip = None
 
 
-def dev(a):
-    torch = torch_cuda()
-    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+def hip():
+    global _hip
+    if _hip is None:
+        lib = ctypes.CDLL("libamdhip64.so")
+        lib.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        lib.hipFree.argtypes = [ctypes.c_void_p]
+        lib.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        lib.hipDeviceSynchronize.argtypes = []
+        lib.hipGetErrorString.restype = ctypes.c_char_p
+        _hip = lib
+    return _hip
 
 
-def host(t):
-    torch = torch_cuda()
-    torch.cuda.synchronize()
-    return t.cpu().numpy()
+def hip_check(code):
+    if code != 0:
+        raise RuntimeError("HIP: " + hip().hipGetErrorString(code).decode())
 
 
-def vp(t):
-    return ctypes.c_void_p(t.data_ptr())
+class Dev:
+    """a device buffer with a NumPy dtype and shape"""
+
+    def __init__(self, shape, dtype, init=None):
+        self.shape, self.dtype = tuple(np.atleast_1d(shape)) if not isinstance(shape, tuple) else shape, np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = ctypes.c_void_p()
+        hip_check(hip().hipMalloc(ctypes.byref(self.ptr), max(self.nbytes, 1)))
+        if init is not None:
+            a = np.ascontiguousarray(init, dtype=self.dtype)
+            assert a.nbytes == self.nbytes
+            hip_check(hip().hipMemcpy(self.ptr, ctypes.c_void_p(a.ctypes.data), self.nbytes, 1))  # host to device
+        else:
+            zeros = np.zeros(self.shape, dtype=self.dtype)
+            hip_check(hip().hipMemcpy(self.ptr, ctypes.c_void_p(zeros.ctypes.data), self.nbytes, 1))
+
+    def numpy(self):
+        hip_check(hip().hipDeviceSynchronize())
+        out = np.zeros(self.shape, dtype=self.dtype)
+        hip_check(hip().hipMemcpy(ctypes.c_void_p(out.ctypes.data), self.ptr, self.nbytes, 2))  # device to host
+        return out
+
+    def __del__(self):
+        if self.ptr:
+            hip().hipDeviceSynchronize()  # never free what a queued kernel may still read
+            hip().hipFree(self.ptr)
+            self.ptr = None
+
+
+def upload(a):
+    a = np.ascontiguousarray(a)
+    return Dev(a.shape, a.dtype, a)
 
 
 def check(code):
@@ -34,33 +66,35 @@ def check(code):
 
 
 def quantize_x(x, bias):
-    torch = torch_cuda()
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, np.shape(x)[-1])
     m, n = x.shape
-    xd = dev(x)
-    q = torch.zeros((m, n), dtype=torch.int8, device="cuda")
-    s = torch.zeros((m, n // 32), dtype=torch.float32, device="cuda")
-    check(package().library().hk_quantize_x(vp(q), vp(s), vp(xd), m, n, bias, None))
-    return host(q), host(s)
+    xd = upload(x)
+    q, s = Dev((m, n), np.int8), Dev((m, n // 32), np.float32)
+    check(package().library().hk_quantize_x(q.ptr, s.ptr, xd.ptr, m, n, bias, None))
+    out = q.numpy(), s.numpy()
+    del xd
+    return out
 
 
 def matmul(xq, xs, w, ws, rows, k, bias, six):
-    torch = torch_cuda()
     xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, k)
     m = xq.shape[0]
-    y = torch.zeros((m, rows), dtype=torch.float32, device="cuda")
-    args = [dev(xq), dev(np.ascontiguousarray(xs, dtype=np.float32).reshape(m, k // 32)), dev(np.ascontiguousarray(w)),
-            dev(np.ascontiguousarray(ws, dtype=np.float32))]
-    check(package().library().hk_matmul(vp(y), *(vp(a) for a in args), m, rows, k, bias, six, None))
-    return host(y)
+    y = Dev((m, rows), np.float32)
+    args = [upload(xq), upload(np.ascontiguousarray(xs, dtype=np.float32).reshape(m, k // 32)), upload(w),
+            upload(np.ascontiguousarray(ws, dtype=np.float32))]
+    check(package().library().hk_matmul(y.ptr, *(a.ptr for a in args), m, rows, k, bias, six, None))
+    out = y.numpy()  # synchronizes before the inputs are freed
+    del args
+    return out
 
 
 def group_sums(xq, w, rows, k, bias, six, gemm=0):
-    torch = torch_cuda()
     xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, k)
     m = xq.shape[0]
     per = (k // 32) * (1 if bias else 4)
-    s = torch.zeros((m, rows, per), dtype=torch.int32, device="cuda")
-    check(package().library().hk_group_sums(vp(s), vp(dev(xq)), vp(dev(np.ascontiguousarray(w))), m, rows, k, bias,
-                                            six, gemm, None))
-    return host(s)
+    s = Dev((m, rows, per), np.int32)
+    xd, wd = upload(xq), upload(w)  # kept alive until the kernel has run
+    check(package().library().hk_group_sums(s.ptr, xd.ptr, wd.ptr, m, rows, k, bias, six, gemm, None))
+    out = s.numpy()
+    del xd, wd
+    return out

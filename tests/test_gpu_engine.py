@@ -12,8 +12,8 @@ pytestmark = pytest.mark.gpu
 MODELS = {
     "tiny_gqa": (dict(dim=64, hidden_dim=128, n_layers=2, n_heads=4, n_kv_heads=2, head_size=16, vocab_size=320,
                       seq_len=48, shared_classifier=1), 10000.0),
-    "tiny_qwen_int6": (dict(dim=64, hidden_dim=96, n_layers=2, n_heads=4, n_kv_heads=1, head_size=16, vocab_size=288,
-                            seq_len=48, shared_classifier=0, six=1, qkv_bias=1), 1000000.0),
+    "tiny_qwen_int6": (dict(dim=128, hidden_dim=96, n_layers=2, n_heads=4, n_kv_heads=1, head_size=32,
+                            vocab_size=288, seq_len=48, shared_classifier=0, six=1, qkv_bias=1), 1000000.0),
     "stories15m": (dict(dim=288, hidden_dim=768, n_layers=6, n_heads=6, n_kv_heads=6, head_size=48, vocab_size=32000,
                         seq_len=256, shared_classifier=1), 10000.0),
 }
