@@ -133,6 +133,24 @@ uint64_t he_device_bytes(he_engine *e);
 /* engine.release() (public/forward.js:1918-1935): frees everything the engine holds. */
 int32_t he_close(he_engine *e);
 
+/* The kinds of kernel he_profile_forward reports on */
+enum {
+  HE_K_GEMV = 0,   /* the decode matmuls (m <= 8 tokens) */
+  HE_K_GEMM,       /* the prefill matmuls on MFMA */
+  HE_K_ATTENTION,  /* scores, softmax, weighted values */
+  HE_K_NORM,       /* rmsnorm with quantize_x, quantize_x alone */
+  HE_K_ELEMENTWISE,/* embed, bias + RoPE + cache write, swiglu with quantize_x */
+  HE_K_ARGMAX,     /* greedy selection */
+  HE_K_COUNT
+};
+
+/* One forward step timed by kind of kernel: the counterpart of the profiling wrap of public/forward.js:646-647 that
+ * tests/profile.mjs uses. Runs he_forward(token, pos, need_logits) with a HIP event pair around every launch on the
+ * engine's stream, and fills ms[HE_K_COUNT] (device time), bytes[HE_K_COUNT] (the algorithmic bytes the launches
+ * read and write: weights, scales, activations, cache rows) and launches[HE_K_COUNT]. */
+int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, double *ms, double *bytes,
+                           int32_t *launches);
+
 /* ---- kernel level: device pointers, for the standalone matmul and the parity tests ---- */
 
 /* quantize_x (kernels/kernel.ts:129-156) of m rows of n float32 (row stride n): int8 rows (stride n) and float32

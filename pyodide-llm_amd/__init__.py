@@ -1,8 +1,9 @@
 """pyodide-llm's quantized forward path on MI355X: HIP kernels for gfx950 behind the interface public/forward.js gives
 its Python caller. The directory's name is not a Python identifier: load it with pkg() below, or through
 importlib under the name pyodide_llm_amd."""
-from .hip_engine import (HeConfig, HeTensor, HipError, TensorArray, TENSORS, T, Engine, External, config, external,
-                         library, open_config, open_synthetic, plan_to_config, start)
+from .hip_engine import (KINDS, HeConfig, HeTensor, HipError, TensorArray, TENSORS, T, Engine, External, config,
+                         external, group_size, library, open_config, open_synthetic, places, plan_to_config,
+                         rope_tables, start)
 
-__all__ = ["HeConfig", "HeTensor", "HipError", "TensorArray", "TENSORS", "T", "Engine", "External", "config",
+__all__ = ["KINDS", "group_size", "places", "rope_tables", "HeConfig", "HeTensor", "HipError", "TensorArray", "TENSORS", "T", "Engine", "External", "config",
            "external", "library", "open_config", "open_synthetic", "plan_to_config", "start"]

@@ -118,6 +118,14 @@ struct he_engine {
   int32_t *best_i = nullptr;
   uint64_t device_bytes = 0;
   bool have_logits = false;
+  // he_profile_forward: event pairs around every launch while `profiling` is set
+  struct Mark {
+    int kind;
+    double bytes;
+    hipEvent_t a, b;
+  };
+  bool profiling = false;
+  std::vector<Mark> marks;
 
   const uint8_t *mat(int id, int l) const {
     const Shape s = shape_of(c, id == HE_T_WCLS && c.shared_classifier ? HE_T_EMBEDDING : id);
@@ -286,7 +294,33 @@ int32_t open_common(const he_config *cfg, const he_tensor *tensors, uint64_t siz
 
 // ---- the forward pass of one chunk of tokens (public/forward.js:1011-1090) ----
 
-hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs) {
+// a launch (or a few) of one kind, bracketed by events while profiling
+template <class F>
+hipError_t timed(he_engine *e, int kind, double bytes, F &&launch) {
+  if (!e->profiling) return launch();
+  he_engine::Mark mk{kind, bytes, nullptr, nullptr};
+  hipError_t err = hipEventCreate(&mk.a);
+  if (err == hipSuccess) err = hipEventCreate(&mk.b);
+  if (err == hipSuccess) err = hipEventRecord(mk.a, e->stream);
+  if (err == hipSuccess) err = launch();
+  if (err == hipSuccess) err = hipEventRecord(mk.b, e->stream);
+  e->marks.push_back(mk);
+  return err;
+}
+
+// the algorithmic bytes of a matmul of m tokens: every row's values and scales once, the activations and their
+// scales, the outputs (read as well where they accumulate)
+double matmul_bytes(const he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m) {
+  double b = (double)m * k + (double)m * (k / 32) * 4;
+  for (int i = 0; i < nseg; ++i) {
+    const double row = (e->c.six ? (double)k / 32 * 24 : (double)k) + (double)k / 32 * 4;
+    b += segs[i].rows * row + (double)m * segs[i].rows * 4 * (segs[i].accumulate ? 2 : 1);
+  }
+  return b;
+}
+
+hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
+                         const float *xs) {
   const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
   for (int32_t t0 = 0; t0 < m; t0 += 8) {
     MatArgs a{};
@@ -310,6 +344,11 @@ hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t
   return hipSuccess;
 }
 
+hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs) {
+  return timed(e, HE_K_GEMV, matmul_bytes(e, segs, nseg, k, m),
+               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs); });
+}
+
 int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, bool need_logits) {
   const he_config &c = e->c;
   hipStream_t s = e->stream;
@@ -317,11 +356,15 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
   const int32_t W = e->widest;
   const size_t esz = c.half_kv ? 2 : 4;
   HIP_TRY(hipMemcpyAsync(e->tokens, tokens, sizeof(int32_t) * m, hipMemcpyHostToDevice, s));
-  HIP_TRY(launch_embed(e->x, e->tokens, e->values[HE_T_EMBEDDING], e->scales[HE_T_EMBEDDING], m, dim, dim,
-                       c.six ? 32 : group_size(dim), c.six, s));
+  HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * dim * (c.six ? 0.75 + 0.125 + 4 : 1 + 0.125 + 4), [&] {
+    return launch_embed(e->x, e->tokens, e->values[HE_T_EMBEDDING], e->scales[HE_T_EMBEDDING], m, dim, dim,
+                        c.six ? 32 : group_size(dim), c.six, s);
+  }));
   for (int32_t l = 0; l < c.n_layers; ++l) {
-    HIP_TRY(launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim, W,
-                                 W / 32, 0, c.rms_norm_eps, e->bias, s));
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim, W,
+                                  W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
     const MatSeg qkv[3] = {
         {e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), e->q, qdim, qdim, 0},
         {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), e->k, kvdim, kvdim, 0},
@@ -346,7 +389,8 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     qp.pos0 = pos0;
     qp.m = m;
     qp.half = c.half_kv;
-    HIP_TRY(launch_qkv_post(qp, s));
+    HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * (qdim + 2 * kvdim) * 8 + (double)m * 2 * kvdim * esz,
+                  [&] { return launch_qkv_post(qp, s); }));
     AttnArgs at{};
     at.q = e->q;
     at.q_stride = qdim;
@@ -364,22 +408,32 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.m = m;
     at.seq_len = c.seq_len;
     at.half = c.half_kv;
-    HIP_TRY(launch_attention(at, s));
-    HIP_TRY(launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s));
+    double kv_rows = 0;
+    for (int32_t t = 0; t < m; ++t) kv_rows += pos0 + t + 1;
+    HIP_TRY(timed(e, HE_K_ATTENTION, kv_rows * 2 * kvdim * esz + (double)m * qdim * 8,
+                  [&] { return launch_attention(at, s); }));
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * qdim * (4 + 1 + 0.125),
+                  [&] { return launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s); }));
     const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
     HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
-    HIP_TRY(launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
-                                 W / 32, 0, c.rms_norm_eps, e->bias, s));
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
+                                  W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
     const MatSeg w13[2] = {{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), e->hb, hidden, hidden, 0},
                            {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), e->hb2, hidden, hidden, 0}};
     HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs));
-    HIP_TRY(launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s));
+    HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * hidden * (8 + 1 + 0.125), [&] {
+      return launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s);
+    }));
     const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
     HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs));
   }
   if (need_logits) {
-    HIP_TRY(launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x + (int64_t)(m - 1) * dim, e->vec(HE_T_RMS_FINAL, 0), 1,
-                                 dim, dim, W, W / 32, 0, c.rms_norm_eps, e->bias, s));
+    HIP_TRY(timed(e, HE_K_NORM, (double)dim * (8 + 1 + 0.125), [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x + (int64_t)(m - 1) * dim, e->vec(HE_T_RMS_FINAL, 0), 1,
+                                  dim, dim, W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
     const MatSeg cls[1] = {{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), e->logits, c.vocab_size, 0, 0}};
     HIP_TRY(matmul(e, cls, 1, dim, 1, e->xq, e->xs));
     e->have_logits = true;
@@ -507,6 +561,39 @@ int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, int32_t count
     for (int32_t j = 0; j < n_stops; ++j) stop = stop || stops[j] == best;
     if (stop) break;
   }
+  return HE_OK;
+}
+
+int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, double *ms, double *bytes,
+                           int32_t *launches) {
+  if (!e || !ms || !bytes || !launches) return fail(HE_E_ARG, "a required pointer is null");
+  for (int k = 0; k < HE_K_COUNT; ++k) {
+    ms[k] = 0;
+    bytes[k] = 0;
+    launches[k] = 0;
+  }
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  e->profiling = true;
+  e->marks.clear();
+  int32_t rc = run_tokens(e, &token, 1, pos, need_logits != 0);
+  if (rc == HE_OK && need_logits)
+    rc = timed(e, HE_K_ARGMAX, (double)e->c.vocab_size * 4, [&] {
+           return launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream);
+         }) == hipSuccess ? HE_OK : fail(HE_E_HIP, "argmax launch failed");
+  e->profiling = false;
+  hipError_t err = hipStreamSynchronize(e->stream);
+  for (auto &mk : e->marks) {
+    float t = 0;
+    if (err == hipSuccess && mk.a && mk.b) err = hipEventElapsedTime(&t, mk.a, mk.b);
+    ms[mk.kind] += t;
+    bytes[mk.kind] += mk.bytes;
+    launches[mk.kind] += 1;
+    if (mk.a) (void)hipEventDestroy(mk.a);
+    if (mk.b) (void)hipEventDestroy(mk.b);
+  }
+  e->marks.clear();
+  if (rc) return rc;
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("profile: ") + hipGetErrorString(err));
   return HE_OK;
 }
 

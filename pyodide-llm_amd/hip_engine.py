@@ -21,6 +21,7 @@ TENSORS = ("token_embedding_table", "rms_att_weight", "wq", "wk", "wv", "wo", "r
            "rms_final_weight", "wcls", "bq", "bk", "bv")
 T = {name: i for i, name in enumerate(TENSORS)}
 HE_OK, HE_E_ARG, HE_E_HIP, HE_E_STATE, HE_E_NOTFINITE = 0, -1, -2, -3, -4
+KINDS = ("gemv", "gemm", "attention", "norm", "elementwise", "argmax")  # include/pyodide_llm_hip.h HE_K_*
 NOT_FINITE = ("The model computed logits that are not finite numbers (NaN or infinity), so no token can be drawn: "
               "its weights are broken or its numbers overflowed.")  # public/llama2_numpy.py:548
 
@@ -80,6 +81,7 @@ def library():
             "he_prompt_block": (I32, [P]),
             "he_device_bytes": (U64, [P]),
             "he_close": (I32, [P]),
+            "he_profile_forward": (I32, [P, I32, I32, I32, P, P, P]),
             "hk_quantize_x": (I32, [P, P, P, I32, I32, I32, P]),
             "hk_matmul": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, P]),
             "hk_group_sums": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, P]),
@@ -213,6 +215,15 @@ class Engine:
         check(library().he_kv_read(self._h, int(start), int(count), _ptr(keys), _ptr(values)))
         return {"keys": keys.reshape(-1), "values": values.reshape(-1)}
 
+    def profile(self, token, pos, need_logits=True):
+        """one forward step timed by kind of kernel: {kind: (ms, algorithmic bytes, launches)}"""
+        ms = np.zeros(len(KINDS), dtype=np.float64)
+        nbytes = np.zeros(len(KINDS), dtype=np.float64)
+        launches = np.zeros(len(KINDS), dtype=np.int32)
+        check(library().he_profile_forward(self._h, int(token), int(pos), int(bool(need_logits)), _ptr(ms),
+                                           _ptr(nbytes), _ptr(launches)))
+        return {k: (float(ms[i]), float(nbytes[i]), int(launches[i])) for i, k in enumerate(KINDS)}
+
     def memoryBytes(self):
         return int(library().he_device_bytes(self._h))
 
@@ -242,6 +253,63 @@ class Engine:
             self.release()
         except Exception:
             pass
+
+
+def group_size(row_length):
+    """public/llama2_convert.py:25-29"""
+    size = 32
+    while row_length % size:
+        size //= 2
+    return size
+
+
+def places(cfg):
+    """public/llama2_numpy.py:751-775 Places.take over the Llama/Qwen2 tensor order (:1149-1179) of an int8 or int6
+    checkpoint (which leaves the RoPE tables out): (HeTensor array, file size)"""
+    t = TensorArray()
+    offset = 28
+    L, dim, hidden, vocab = cfg.n_layers, cfg.dim, cfg.hidden_dim, cfg.vocab_size
+    qdim, kvdim = cfg.n_heads * cfg.head_size, cfg.n_kv_heads * cfg.head_size
+
+    def matrix(name, count, last):
+        nonlocal offset
+        stored = count * 3 // 4 if cfg.six else count
+        t[T[name]].offset, t[T[name]].scales = offset, offset + stored
+        offset += stored + 4 * (count // group_size(last))
+
+    def vector(name, count):
+        nonlocal offset
+        t[T[name]].offset, t[T[name]].scales = offset, 0
+        offset += 4 * count
+
+    matrix("token_embedding_table", vocab * dim, dim)
+    vector("rms_att_weight", L * dim)
+    matrix("wq", L * qdim * dim, dim)
+    matrix("wk", L * kvdim * dim, dim)
+    matrix("wv", L * kvdim * dim, dim)
+    matrix("wo", L * dim * qdim, qdim)
+    vector("rms_ffn_weight", L * dim)
+    matrix("w1", L * hidden * dim, dim)
+    matrix("w2", L * dim * hidden, hidden)
+    matrix("w3", L * hidden * dim, dim)
+    vector("rms_final_weight", dim)
+    if cfg.shared_classifier:
+        t[T["wcls"]].offset, t[T["wcls"]].scales = t[0].offset, t[0].scales
+    else:
+        matrix("wcls", vocab * dim, dim)
+    if cfg.qkv_bias:
+        vector("bq", L * qdim)
+        vector("bk", L * kvdim)
+        vector("bv", L * kvdim)
+    return t, offset
+
+
+def rope_tables(seq_len, head_size, theta):
+    """public/llama2_numpy.py:484-542 rope_tables() without scaling, as float32 (:1177-1179): what a caller hands the
+    engine as plan.derived"""
+    freq = 1.0 / theta ** (np.arange(0, head_size, 2, dtype=np.float64) / head_size)
+    angles = np.arange(seq_len, dtype=np.float64)[:, None] * freq
+    return np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
 
 
 def start(plan, checkpoint, max_block=2048):

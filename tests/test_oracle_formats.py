@@ -123,3 +123,24 @@ def test_package_config_structs_match_the_header():
     assert ctypes.sizeof(pk.HeConfig) == 14 * 4
     assert ctypes.sizeof(pk.HeTensor) == 16
     assert len(pk.TENSORS) == 15
+
+
+@pytest.mark.parametrize("name", sorted(PLANS))
+def test_package_places_equal_the_reference_plans(name):
+    """the package's own Places (what bench.py and synthetic engines use) against external_tensors()"""
+    entry = PLANS[name]
+    cfg = plan_config(entry)
+    tensors, size = package().places(cfg)
+    assert size == entry["size"]
+    for tname, plan in entry["tensors"].items():
+        if tname in ("freq_cis_real", "freq_cis_imag"):
+            continue
+        assert (tensors[NAMES[tname]].offset, tensors[NAMES[tname]].scales) == (plan["offset"], plan["scales"])
+
+
+@pytest.mark.parametrize("tag", ["256_48_10000", "512_128_500000"])
+def test_package_rope_tables_equal_the_reference(tag):
+    """NumPy float64 cos/sin cast to float32, as llama2_numpy computes them"""
+    seq, hs, theta = (int(v) for v in tag.split("_"))
+    cos, sin = package().rope_tables(seq, hs, float(theta))
+    assert np.array_equal(cos, RT[f"cos_{tag}"]) and np.array_equal(sin, RT[f"sin_{tag}"])
