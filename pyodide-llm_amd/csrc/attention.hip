@@ -6,9 +6,11 @@
 //           in four lanes (t % 4) in order, hsum ((l0 + l1) + l2) + l3, the tail added in order; p = e * f32(1 / sum);
 //   out_j: blocks of four positions in order, out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), then the positions past
 //           the fours one at a time, out = out + p v.
-// Four launches, each wide over positions so that every CU streams the cache: (A) scores and per-tile maxima,
-// (B) the softmax of each (token, head), (C) the four-position blocks of weighted values, (D) the ordered sums over
-// the blocks. Keys and values are staged in LDS once per kv head for the nh / nkv query heads that share them.
+// Three launches: (A) the scores of 64-position tiles, every CU streaming keys once for the nh / nkv query heads
+// that share them, with each tile's maxima; (B) one wave a (token, head): the exponentials, their ordered sum from
+// LDS, the weights; (C) one block a (token, kv head, 8 of the head's columns): 512-position chunks of values and
+// weights staged in LDS (the next chunk's loads in flight while this one is used), the four-position products, and
+// the ordered sums over the blocks, one thread a (head, column).
 #pragma clang fp contract(off)
 
 #include "common.hpp"
@@ -18,41 +20,58 @@ namespace ple {
 
 namespace {
 
-constexpr int TILE = 64;  // positions a block of (A) and (C)
+constexpr int TILE = 64;   // positions a block of (A)
+constexpr int MAXMUL = 8;  // query heads a kv head at most
+constexpr int PVJ = 8;     // columns a block of (C)
+constexpr int CH = 512;    // positions a chunk of (C)
 
-__device__ __forceinline__ float cache_at(const void *c, int64_t i, int half) {
-  return half ? from_f16(reinterpret_cast<const uint16_t *>(c)[i]) : reinterpret_cast<const float *>(c)[i];
+template <bool HALF>
+__device__ __forceinline__ float4 cache4(const void *c, int64_t i) {  // four values from element i (i % 4 == 0)
+  if constexpr (HALF) {
+    const uint2 h = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(c) + i);
+    return make_float4(from_f16((uint16_t)(h.x & 0xffff)), from_f16((uint16_t)(h.x >> 16)),
+                       from_f16((uint16_t)(h.y & 0xffff)), from_f16((uint16_t)(h.y >> 16)));
+  } else {
+    return *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(c) + i);
+  }
+}
+template <bool HALF>
+__device__ __forceinline__ float cache1(const void *c, int64_t i) {
+  if constexpr (HALF) return from_f16(reinterpret_cast<const uint16_t *>(c)[i]);
+  else return reinterpret_cast<const float *>(c)[i];
 }
 
 // (A) grid (tiles, nkv, m)
+template <int HS, bool HALF>
 __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
-  extern __shared__ float sm[];
+  constexpr int LD = HS + 4, C4 = HS / 4;
+  __shared__ float ks[TILE * LD];
+  __shared__ float qs[MAXMUL * HS];
   const int tile = blockIdx.x, kh = blockIdx.y, t = blockIdx.z;
   const int count = a.pos0 + t + 1;
   const int p0 = tile * TILE;
   if (p0 >= count) return;
-  const int hs = a.hs, kvdim = a.nkv * hs, mul = a.nh / a.nkv, ld = hs + 4;
-  float *ks = sm;                   // [TILE][hs + 4]
-  float *qs = sm + TILE * ld;       // [mul][hs]
+  const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
   const int np = min(TILE, count - p0);
-  for (int i = threadIdx.x; i < np * hs; i += 256) {
-    const int p = i / hs, j = i % hs;
-    ks[p * ld + j] = cache_at(a.kcache, (int64_t)(p0 + p) * kvdim + kh * hs + j, a.half);
+  for (int i = threadIdx.x; i < np * C4; i += 256) {
+    const int p = i / C4, c = i % C4;
+    *reinterpret_cast<float4 *>(ks + p * LD + 4 * c) =
+        cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
   }
-  const float *q = a.q + (int64_t)t * a.q_stride + (int64_t)kh * mul * hs;
-  for (int i = threadIdx.x; i < mul * hs; i += 256) qs[i] = q[i];
+  const float *q = a.q + (int64_t)t * a.q_stride + (int64_t)kh * mul * HS;
+  for (int i = threadIdx.x; i < mul * C4; i += 256)
+    *reinterpret_cast<float4 *>(qs + 4 * i) = *reinterpret_cast<const float4 *>(q + 4 * i);
   __syncthreads();
-  const float isq = 1.0f / __builtin_sqrtf((float)hs);
-  const int hs4 = hs & ~3;
+  const float isq = 1.0f / __builtin_sqrtf((float)HS);
   float *scores = a.scores + (int64_t)t * a.nh * a.seq_len;
   for (int idx = threadIdx.x; idx < mul * TILE; idx += 256) {
     const int hl = idx / TILE, p = idx % TILE;
     float sc = -__builtin_inff();
     if (p < np) {
-      const float *kr = ks + p * ld, *qr = qs + hl * hs;
+      const float *kr = ks + p * LD, *qr = qs + hl * HS;
       float l0 = 0.0f, l1 = 0.0f, l2 = 0.0f, l3 = 0.0f;
-      int j = 0;
-      for (; j < hs4; j += 4) {
+#pragma unroll 8
+      for (int j = 0; j < HS; j += 4) {
         const float4 kv = *reinterpret_cast<const float4 *>(kr + j);
         const float4 qv = *reinterpret_cast<const float4 *>(qr + j);
         l0 = l0 + qv.x * kv.x;
@@ -60,157 +79,144 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
         l2 = l2 + qv.z * kv.z;
         l3 = l3 + qv.w * kv.w;
       }
-      sc = (l0 + l2) + (l1 + l3);
-      for (; j < hs; ++j) sc = sc + qr[j] * kr[j];
-      sc = sc * isq;
+      sc = ((l0 + l2) + (l1 + l3)) * isq;
       scores[(int64_t)(kh * mul + hl) * a.seq_len + p0 + p] = sc;
     }
-    // the tile's largest of this head: p runs over one wave's lanes when TILE == 64
-    float mx = sc;
+    float mx = sc;  // the tile's largest of this head (a wave is one head's 64 positions)
     for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
     if (p == 0) a.tilemax[((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1) + tile] = mx;
   }
 }
 
-// (B) one block a (head, token)
-__global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
-  extern __shared__ float sm[];  // count4 exponentials, transposed: lane k's side by side
-  __shared__ float part[4];
-  __shared__ float shared_max, shared_inv;
-  const int h = blockIdx.x, t = blockIdx.y;
-  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2;
+// (B) one wave a (head, token): grid (nh, m), block 64
+__global__ __launch_bounds__(64) void softmax_kernel(const AttnArgs a) {
+  extern __shared__ float e4[];  // 4 rows of q4s exponentials (lane k's positions t % 4 == k), then the tail
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = (q4 + 3) & ~3;
   const int tiles = (count + TILE - 1) / TILE;
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
-  if (threadIdx.x < 64) {
-    float mx = -3.4028234663852886e38f;
-    for (int i = threadIdx.x; i < tiles; i += 64) mx = wmax(mx, tm[i]);
-    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-    if (threadIdx.x == 0) shared_max = mx;
-  }
-  __syncthreads();
-  const float mx = shared_max;
-  for (int i = threadIdx.x; i < count; i += 256) {
+  float mx = -3.4028234663852886e38f;
+  for (int i = lane; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+  for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+  float *tail = e4 + 4 * q4s;
+  for (int i = lane; i < count; i += 64) {
     const float d = scores[i] - mx;
-    if (i < count4) {
-      const float e = vexp(d);
-      scores[i] = e;
-      sm[(i & 3) * q4 + (i >> 2)] = e;
-    } else {
-      scores[i] = fexp(d);
-    }
+    if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
+    else tail[i - count4] = fexp(d);
   }
-  __syncthreads();
-  if (threadIdx.x < 4) {
-    const float *c = sm + threadIdx.x * q4;
-    float acc = 0.0f;
-    int i = 0;
-    if ((q4 & 3) == 0) {
-      const float4 *c4 = reinterpret_cast<const float4 *>(c);
-      for (; i < q4; i += 4) {
-        const float4 v = c4[i >> 2];
-        acc = acc + v.x;
-        acc = acc + v.y;
-        acc = acc + v.z;
-        acc = acc + v.w;
+  wave_sync_lds();
+  float part = 0.0f;
+  if (lane < 4) part = lds_chain(e4 + lane * q4s, q4, 0.0f);
+  const float p1 = __shfl(part, 1, 64), p2 = __shfl(part, 2, 64), p3 = __shfl(part, 3, 64);
+  float sum = ((part + p1) + p2) + p3;  // lane 0's is the one
+  for (int i = 0; i < count - count4; ++i) sum = sum + tail[i];
+  const float inv = __shfl(1.0f / sum, 0, 64);
+  for (int i = lane; i < count; i += 64) {
+    const float e = i < count4 ? e4[(i & 3) * q4s + (i >> 2)] : tail[i - count4];
+    scores[i] = e * inv;
+  }
+}
+
+// (C) grid (hs / PVJ, nkv, m), block 256: the weighted values of columns j0..j0+7 of the nh / nkv heads of kv head kh
+template <int HS, bool HALF>
+__global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
+  constexpr int NB = CH / 4;  // four-position blocks a chunk
+  __shared__ float vs[CH * PVJ];            // [position][column]
+  __shared__ float ps[MAXMUL * CH];         // [head][position]
+  __shared__ float bs[MAXMUL * PVJ * NB];   // [head][column][block]
+  const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const int count = a.pos0 + t + 1, count4 = count & ~3;
+  const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
+  const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
+  const int chains = mul * PVJ;
+  const int hl_me = tid / PVJ, j_me = tid % PVJ;
+  float acc = 0.0f;
+  // per chunk: CH * PVJ / 4 float4 of values (4 a thread) and mul * CH / 4 float4 of weights (<= 4 a thread)
+  static_assert(CH * PVJ / 4 == 4 * 256 && MAXMUL * CH / 4 <= 4 * 256, "the chunk's loads are four a thread");
+  float4 vreg[4], preg[4];
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = tid + u * 256;  // float4 i: position i / 2, columns 4 (i % 2)..
+      const int p = c0 + (i >> 1);
+      vreg[u] = p < count4 ? cache4<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + 4 * (i & 1))
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = tid + u * 256;  // float4 i of [head][position / 4]
+      const int hl = i / (CH / 4), p = c0 + 4 * (i % (CH / 4));
+      preg[u] = (hl < mul && p < count4) ? *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  if (count4 > 0) fetch(0);
+  for (int c0 = 0; c0 < count4; c0 += CH) {
+    const int nb = min(CH, count4 - c0) >> 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) reinterpret_cast<float4 *>(vs)[tid + u * 256] = vreg[u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (tid + u * 256 < mul * CH / 4) reinterpret_cast<float4 *>(ps)[tid + u * 256] = preg[u];
+    __syncthreads();
+    if (c0 + CH < count4) fetch(c0 + CH);  // the next chunk's loads fly while this one is used
+    for (int i = tid; i < mul * PVJ * NB; i += 256) {
+      const int b = i % NB, j = (i / NB) % PVJ, hl = i / (NB * PVJ);
+      if (hl < mul && b < nb) {
+        const float *pp = ps + hl * CH + 4 * b, *vv = vs + 4 * b * PVJ + j;
+        const float pair0 = pp[0] * vv[0] + pp[1] * vv[PVJ];
+        const float pair1 = pp[2] * vv[2 * PVJ] + pp[3] * vv[3 * PVJ];
+        bs[(hl * PVJ + j) * NB + b] = pair0 + pair1;
       }
     }
-    for (; i < q4; ++i) acc = acc + c[i];
-    part[threadIdx.x] = acc;
+    __syncthreads();
+    if (tid < chains) acc = lds_chain(bs + (hl_me * PVJ + j_me) * NB, nb, acc);
+    __syncthreads();
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = ((part[0] + part[1]) + part[2]) + part[3];
-    for (int i = count4; i < count; ++i) sum = sum + scores[i];
-    shared_inv = 1.0f / sum;
-  }
-  __syncthreads();
-  const float inv = shared_inv;
-  for (int i = threadIdx.x; i < count; i += 256) scores[i] = scores[i] * inv;
-}
-
-// (C) grid (tiles, nkv, m): block b of a head, (p0 v0 + p1 v1) + (p2 v2 + p3 v3), and the single products past the
-// fours, into partial[t][h][b][j]
-__global__ __launch_bounds__(256) void blocks_kernel(const AttnArgs a) {
-  extern __shared__ float sm[];
-  const int tile = blockIdx.x, kh = blockIdx.y, t = blockIdx.z;
-  const int count = a.pos0 + t + 1, count4 = count & ~3;
-  const int p0 = tile * TILE;
-  if (p0 >= count) return;
-  const int hs = a.hs, kvdim = a.nkv * hs, mul = a.nh / a.nkv;
-  const int np = min(TILE, count - p0);
-  float *vs = sm;               // [TILE][hs]
-  float *ps = sm + TILE * hs;   // [mul][TILE]
-  for (int i = threadIdx.x; i < np * hs; i += 256) {
-    const int p = i / hs, j = i % hs;
-    vs[p * hs + j] = cache_at(a.vcache, (int64_t)(p0 + p) * kvdim + kh * hs + j, a.half);
-  }
-  const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len;
-  for (int i = threadIdx.x; i < mul * TILE; i += 256) {
-    const int hl = i / TILE, p = i % TILE;
-    ps[i] = p < np ? scores[(int64_t)(kh * mul + hl) * a.seq_len + p0 + p] : 0.0f;
-  }
-  __syncthreads();
-  const int nblocks = TILE / 4;
-  const int64_t per_head = (int64_t)(a.seq_len / 4 + 4) * hs;
-  for (int idx = threadIdx.x; idx < mul * nblocks * hs; idx += 256) {
-    const int j = idx % hs, b = (idx / hs) % nblocks, hl = idx / (hs * nblocks);
-    const int pb = p0 + 4 * b;  // the block's first position
-    float *out = a.partial + ((int64_t)t * a.nh + kh * mul + hl) * per_head;
-    const float *pp = ps + hl * TILE + 4 * b;
-    const float *vv = vs + 4 * b * hs + j;
-    if (pb + 4 <= count4) {
-      const float pair0 = pp[0] * vv[0] + pp[1] * vv[hs];
-      const float pair1 = pp[2] * vv[2 * hs] + pp[3] * vv[3 * hs];
-      out[(int64_t)(pb >> 2) * hs + j] = pair0 + pair1;
-    } else if (pb < count) {
-      // positions past the fours: one product each, after the blocks (index count4 / 4 + i)
-      for (int i = 0; i < 4; ++i)
-        if (pb + i >= count4 && pb + i < count)
-          out[(int64_t)((count4 >> 2) + (pb + i - count4)) * hs + j] = pp[i] * vv[i * hs];
-    }
+  if (tid < chains) {
+    const int h = kh * mul + hl_me, j = j0 + j_me;
+    for (int p = count4; p < count; ++p)
+      acc = acc + scores[(int64_t)hl_me * a.seq_len + p] * cache1<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j);
+    a.out[(int64_t)t * a.out_stride + h * HS + j] = acc;
   }
 }
 
-// (D) one thread a (token, head, j): the blocks added in order, then the single products
-__global__ __launch_bounds__(256) void chain_kernel(const AttnArgs a) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int hs = a.hs;
-  if (idx >= (int64_t)a.m * a.nh * hs) return;
-  const int j = (int)(idx % hs), h = (int)((idx / hs) % a.nh), t = (int)(idx / ((int64_t)hs * a.nh));
-  const int count = a.pos0 + t + 1, count4 = count & ~3, nb = count4 >> 2;
-  const int64_t per_head = (int64_t)(a.seq_len / 4 + 4) * hs;
-  const float *pb = a.partial + ((int64_t)t * a.nh + h) * per_head + j;
-  float acc = 0.0f;
-  int b = 0;
-  for (; b + 8 <= nb; b += 8) {
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = pb[(int64_t)(b + i) * hs];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc = acc + v[i];
+template <int HS, bool HALF>
+hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
+  const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
+  hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
+  const int most4 = (a.pos0 + a.m) & ~3;
+  const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
+  hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(64), lds_b, s, a);
+  hipLaunchKernelGGL((pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <bool HALF>
+hipError_t launch_half(const AttnArgs &a, hipStream_t s) {
+  switch (a.hs) {
+    case 16: return launch_hs<16, HALF>(a, s);
+    case 32: return launch_hs<32, HALF>(a, s);
+    case 48: return launch_hs<48, HALF>(a, s);
+    case 64: return launch_hs<64, HALF>(a, s);
+    case 96: return launch_hs<96, HALF>(a, s);
+    case 128: return launch_hs<128, HALF>(a, s);
+    case 256: return launch_hs<256, HALF>(a, s);
+    default: return hipErrorInvalidValue;
   }
-  for (; b < nb; ++b) acc = acc + pb[(int64_t)b * hs];
-  for (int i = 0; i < count - count4; ++i) acc = acc + pb[(int64_t)(nb + i) * hs];
-  a.out[(int64_t)t * a.out_stride + h * hs + j] = acc;
 }
 
 }  // namespace
 
+bool attention_supported(int32_t hs, int32_t nh, int32_t nkv) {
+  const bool sizes = hs == 16 || hs == 32 || hs == 48 || hs == 64 || hs == 96 || hs == 128 || hs == 256;
+  return sizes && nkv > 0 && nh % nkv == 0 && nh / nkv <= MAXMUL;
+}
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
-  if (a.hs % 4 != 0 || a.nh % a.nkv != 0) return hipErrorInvalidValue;
-  const int mul = a.nh / a.nkv;
-  const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
-  const size_t lds_a = sizeof(float) * (size_t)(TILE * (a.hs + 4) + mul * a.hs);
-  hipLaunchKernelGGL(scores_kernel, dim3(tiles, a.nkv, a.m), dim3(256), lds_a, s, a);
-  const int most = a.pos0 + a.m;
-  const size_t lds_b = sizeof(float) * (size_t)(most & ~3);
-  hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
-  const size_t lds_c = sizeof(float) * (size_t)(TILE * a.hs + mul * TILE);
-  hipLaunchKernelGGL(blocks_kernel, dim3(tiles, a.nkv, a.m), dim3(256), lds_c, s, a);
-  const int64_t threads = (int64_t)a.m * a.nh * a.hs;
-  hipLaunchKernelGGL(chain_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a);
-  return hipGetLastError();
+  if (!attention_supported(a.hs, a.nh, a.nkv)) return hipErrorInvalidValue;
+  return a.half ? launch_half<true>(a, s) : launch_half<false>(a, s);
 }
 
 }  // namespace ple

@@ -132,6 +132,48 @@ __device__ __forceinline__ float wave_max32(float v) {  // over each half of the
   return v;
 }
 
+// acc + c[0] + c[1] + ... + c[n-1] in order (every add rounded), the values read from LDS 32 at a time with the
+// next 32 already requested: c 16-byte aligned. The dependent adds run back to back instead of waiting on each load.
+__device__ __forceinline__ float lds_chain(const float *c, int n, float acc) {
+  const float4 *c4 = reinterpret_cast<const float4 *>(c);
+  const int n4 = n >> 2;
+  int i = 0;
+  if (n4 >= 8) {
+    float4 cur[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cur[u] = c4[u];
+    for (i = 8; i + 8 <= n4; i += 8) {
+      float4 nxt[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) nxt[u] = c4[i + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        acc = acc + cur[u].x;
+        acc = acc + cur[u].y;
+        acc = acc + cur[u].z;
+        acc = acc + cur[u].w;
+        cur[u] = nxt[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc = acc + cur[u].x;
+      acc = acc + cur[u].y;
+      acc = acc + cur[u].z;
+      acc = acc + cur[u].w;
+    }
+  }
+  for (; i < n4; ++i) {
+    const float4 v = c4[i];
+    acc = acc + v.x;
+    acc = acc + v.y;
+    acc = acc + v.z;
+    acc = acc + v.w;
+  }
+  for (int j = n4 << 2; j < n; ++j) acc = acc + c[j];
+  return acc;
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();

@@ -161,7 +161,9 @@ int32_t check_config(const he_config &c) {
   const int32_t qdim = c.n_heads * c.head_size, kvdim = c.n_kv_heads * c.head_size;
   if (c.dim % 32 || c.hidden_dim % 32 || qdim % 32 || kvdim % 32)
     return fail(HE_E_ARG, "the int8 kernels take rows of whole groups of 32 (dim, hidden, q and kv widths)");
-  if (c.head_size > 256) return fail(HE_E_ARG, "head_size above 256 is not supported");
+  if (!attention_supported(c.head_size, c.n_heads, c.n_kv_heads))
+    return fail(HE_E_ARG, "attention takes head sizes 16, 32, 48, 64, 96, 128, 256 and at most 8 query heads a kv head");
+  if (c.seq_len % 4) return fail(HE_E_ARG, "seq_len must be a multiple of 4");
   return HE_OK;
 }
 

@@ -78,6 +78,8 @@ struct AttnArgs {
   int32_t nh, nkv, hs, pos0, m, seq_len, half;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+// the head sizes and grouping the attention kernels take (hs in {16, 32, 48, 64, 96, 128, 256}, nh / nkv <= 8)
+bool attention_supported(int32_t hs, int32_t nh, int32_t nkv);
 
 // greedy: the first index of the largest logit into *out (and the value into *value)
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,

@@ -41,35 +41,19 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
                                                             float eps, int32_t bias) {
   extern __shared__ float sm[];
   float *xv = sm;       // n
-  float *sq = sm + n;   // n4, transposed: lane k's squares side by side
+  const int n4 = n & ~3, q4 = n4 >> 2, qs = (q4 + 3) & ~3;
+  float *sq = sm + n;   // 4 * qs, transposed: lane k's squares side by side (16-byte aligned rows)
   __shared__ float part[4];
   __shared__ float sval;
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *xt = x + (int64_t)t * x_stride;
-  const int n4 = n & ~3, q4 = n4 >> 2;
   for (int j = tid; j < n; j += 256) {
     const float v = xt[j];
     xv[j] = v;
-    if (j < n4) sq[(j & 3) * q4 + (j >> 2)] = v * v;
+    if (j < n4) sq[(j & 3) * qs + (j >> 2)] = v * v;
   }
   __syncthreads();
-  if (tid < 4) {
-    const float *c = sq + tid * q4;
-    float acc = 0.0f;
-    int i = 0;
-    if ((q4 & 3) == 0 && ((tid * q4) & 3) == 0) {
-      const float4 *c4 = reinterpret_cast<const float4 *>(c);
-      for (; i < q4; i += 4) {
-        const float4 v = c4[i >> 2];
-        acc = acc + v.x;
-        acc = acc + v.y;
-        acc = acc + v.z;
-        acc = acc + v.w;
-      }
-    }
-    for (; i < q4; ++i) acc = acc + c[i];
-    part[tid] = acc;
-  }
+  if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
   __syncthreads();
   if (tid == 0) {
     float ss = ((part[0] + part[1]) + part[2]) + part[3];
@@ -297,7 +281,7 @@ hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int
 hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s) {
-  const size_t lds = sizeof(float) * (size_t)(2 * n);
+  const size_t lds = sizeof(float) * (size_t)(2 * n + 16);
   hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m), dim3(256), lds, s, xq, xs, out, x, w, n, x_stride, xq_stride,
                      xs_stride, out_stride, eps, bias);
   return hipGetLastError();

@@ -98,3 +98,26 @@ def test_greedy_generation_matches_the_oracle():
         token, pos = ids[-1], pos + len(ids)
     assert got == [int(t) for t in want]
     assert same_bits(eng.logits(), want_logits)
+
+
+@pytest.mark.parametrize("half_kv", [0, 1])
+def test_long_context_crosses_attention_chunks(half_kv):
+    """positions past 512 and 1024 (the value kernel's chunks) and every count % 4, against the oracle to the bit"""
+    fields, theta = MODELS["tiny_gqa"]
+    cfg = ol.config(**{**fields, "seq_len": 1200, "half_kv": half_kv})
+    tensors, size = ol.places(cfg)
+    ck = ol.synth_checkpoint(cfg, tensors, size, seed=9)
+    cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, theta)
+    rng = np.random.default_rng(11)
+    tokens = [int(t) for t in rng.integers(0, cfg.vocab_size, size=1100)]
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=1100)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=1100)
+    eng.forwardMany(tokens[:1090], 0)
+    ref.run(tokens[:1090], 0, False)
+    for pos in range(1090, 1100):
+        eng.forward(tokens[pos], pos, True)
+        ref.run([tokens[pos]], pos, True)
+        assert same_bits(eng.logits(), ref.logits()), pos
+    a, (k, v) = eng.keysAndValues(0, 1100), ref.kv(0, 1100)
+    assert same_bits(a["keys"], k.reshape(-1)) and same_bits(a["values"], v.reshape(-1))
