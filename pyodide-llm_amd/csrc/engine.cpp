@@ -324,7 +324,9 @@ double matmul_bytes(const he_engine *e, const MatSeg *segs, int nseg, int32_t k,
 hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
                          const float *xs) {
   const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
-  for (int32_t t0 = 0; t0 < m; t0 += 8) {
+  const int32_t step = gemv_tokens(k, e->c.relaxed);
+  if (step < 1) return hipErrorInvalidValue;
+  for (int32_t t0 = 0; t0 < m; t0 += step) {
     MatArgs a{};
     a.nseg = nseg;
     a.total_rows = 0;
@@ -338,7 +340,7 @@ hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, 
     a.xq_stride = xq_stride;
     a.xs_stride = xs_stride;
     a.k = k;
-    a.m = std::min(8, m - t0);
+    a.m = std::min(step, m - t0);
     a.sums = nullptr;
     hipError_t err = launch_gemv(a, e->c.six, e->c.relaxed, e->stream);
     if (err != hipSuccess) return err;
@@ -702,9 +704,11 @@ int32_t hk_matmul(void *y, const void *xq, const void *xs, const void *w, const 
   if (rc) return rc;
   if (!y || !xs || !ws) return fail(HE_E_ARG, "matmul: a required pointer is null");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  for (int32_t t0 = 0; t0 < m; t0 += 8) {
+  const int32_t step = gemv_tokens(k, bias == 64);
+  if (step < 1) return fail(HE_E_ARG, "matmul: rows too long for the GEMV");
+  for (int32_t t0 = 0; t0 < m; t0 += step) {
     MatArgs a = base;
-    a.m = std::min(8, m - t0);
+    a.m = std::min(step, m - t0);
     a.xq = base.xq + (int64_t)t0 * k;
     a.xs = base.xs + (int64_t)t0 * (k / 32);
     a.seg[0].y = base.seg[0].y + (int64_t)t0 * rows;

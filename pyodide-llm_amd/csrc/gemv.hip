@@ -6,10 +6,10 @@
 //   bias 0:  kernels/kernel.ts:231-258 matmul_q8 (and :261-278 matmul_q6): four int32 lane sums a group (lane k:
 //            products 2k, 2k+1, 2k+8, 2k+9 of each half), each scaled into its own accumulator over every group in
 //            order, the four added in order.
-// Layout: one wave streams one row (grid-stride over rows). An int8 row is read 16 bytes a lane (a group is a lane
-// pair, 1 KiB a wave step); an int6 row 24 bytes a lane (a group a lane, 1.5 KiB a step). The int32 sums come from
-// v_dot4_i32_i8; the products go through LDS to the lanes that hold the float32 accumulators (4 per token), which add
-// them in the reference's order while the next step's loads are in flight.
+// Layout: one wave a row. An int8 row is read 16 bytes a lane (a group is a lane pair, 1 KiB a wave step), an int6
+// row 24 bytes a lane (a group a lane, 1.5 KiB a step); a wave requests up to 8 steps of its row (8 or 12 KiB) before
+// it uses the first, so that HBM sees whole rows in flight. The int32 sums come from v_dot4_i32_i8; the products of
+// the whole row go to LDS, laid out so that the lane holding accumulator k of token t reads its groups in order.
 #pragma clang fp contract(off)
 
 #include "common.hpp"
@@ -20,60 +20,80 @@ namespace ple {
 namespace {
 
 constexpr int WAVES = 4;
+constexpr int CHUNK = 8;  // wave steps requested at once
 
-template <int M, bool SIX, bool RELAXED>
-struct GemvShape {
-  static constexpr int GPI = SIX ? 64 : 32;                   // groups a wave step
-  static constexpr int PER = RELAXED ? GPI : GPI * 4;          // products a token a step
+struct RowLayout {  // a token's products in LDS: 4 accumulator rows of q floats, then the (up to 3) tail groups
+  int q, stride;
 };
+__host__ __device__ inline RowLayout row_layout(int k, bool relaxed) {
+  const int g = k / GS;
+  const int q = relaxed ? (((g & ~3) / 4 + 3) & ~3) : ((g + 3) & ~3);
+  return {q, 4 * q + 4};
+}
 
 template <int M, bool SIX, bool RELAXED, bool SUMS>
 __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
-  using Sh = GemvShape<M, SIX, RELAXED>;
-  constexpr int GPI = Sh::GPI;
-  __shared__ float prod[WAVES][M * Sh::PER];
-  __shared__ float tail[WAVES][M * 4];
+  constexpr int GPI = SIX ? 64 : 32;  // groups a wave step
+  constexpr int NW = SIX ? 8 : 4;     // words of weights a lane a step
+  extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float *P = prod[wave];
+  const int row = blockIdx.x * WAVES + wave;
+  if (row >= a.total_rows) return;  // a whole wave leaves: nothing below waits on the block
   const int K = a.k, G = K / GS, G4 = G & ~3;
-  const int iters = (G + GPI - 1) / GPI;
+  const RowLayout lay = row_layout(K, RELAXED);
+  float *P = smem + wave * M * lay.stride;
+  const int steps = (G + GPI - 1) / GPI;
   const bool holder = SIX ? true : ((lane & 1) == 0);
-  const int mylocal = SIX ? lane : (lane >> 1);  // this lane's group within a step
+  const int mylocal = SIX ? lane : (lane >> 1);
 
-  for (int row = blockIdx.x * WAVES + wave; row < a.total_rows; row += gridDim.x * WAVES) {
-    int s = 0, r = row;
-    while (s + 1 < a.nseg && r >= a.seg[s].rows) {
-      r -= a.seg[s].rows;
-      ++s;
-    }
-    const MatSeg sg = a.seg[s];
-    const uint8_t *wrow = sg.w + (int64_t)r * (SIX ? (int64_t)G * 24 : (int64_t)K);
-    const float *srow = sg.ws + (int64_t)r * G;
-    float chain = 0.0f;  // lane 4t + k (t < M): accumulator k of token t
+  int s = 0, r = row;
+  while (s + 1 < a.nseg && r >= a.seg[s].rows) {
+    r -= a.seg[s].rows;
+    ++s;
+  }
+  const MatSeg sg = a.seg[s];
+  const uint8_t *wrow = sg.w + (int64_t)r * (SIX ? (int64_t)G * 24 : (int64_t)K);
+  const float *srow = SUMS ? nullptr : sg.ws + (int64_t)r * G;
 
-    for (int it = 0; it < iters; ++it) {
-      const int g = it * GPI + mylocal;
-      const bool active = g < G;
-      int32_t S[M][RELAXED ? 1 : 4];
+  for (int c0 = 0; c0 < steps; c0 += CHUNK) {
+    uint32_t wv[CHUNK][NW];
+    float wsv[CHUNK];
+    // every load of the chunk first
 #pragma unroll
-      for (int t = 0; t < M; ++t)
-#pragma unroll
-        for (int k = 0; k < (RELAXED ? 1 : 4); ++k) S[t][k] = 0;
-      if (active) {
-        uint32_t w[SIX ? 8 : 4];
+    for (int u = 0; u < CHUNK; ++u) {
+      const int g = (c0 + u) * GPI + mylocal;
+      if (c0 + u < steps && g < G) {
         if constexpr (SIX) {
           const uint2 *p = reinterpret_cast<const uint2 *>(wrow + (int64_t)g * 24);
           const uint2 l0 = p[0], l1 = p[1], tops = p[2];
-          const uint32_t L[4] = {l0.x, l0.y, l1.x, l1.y};
-          six_widen(L, tops.x, tops.y, w);
+          wv[u][0] = l0.x; wv[u][1] = l0.y; wv[u][2] = l1.x; wv[u][3] = l1.y; wv[u][4] = tops.x; wv[u][5] = tops.y;
         } else {
           const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (int64_t)g * 32 + (lane & 1) * 16);
-          w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+          wv[u][0] = v.x; wv[u][1] = v.y; wv[u][2] = v.z; wv[u][3] = v.w;
         }
+        if constexpr (!SUMS) wsv[u] = holder ? srow[g] : 0.0f;
+      }
+    }
 #pragma unroll
-        for (int t = 0; t < M; ++t) {
+    for (int u = 0; u < CHUNK; ++u) {
+      if (c0 + u >= steps) break;
+      const int g = (c0 + u) * GPI + mylocal;
+      const bool active = g < G;
+      uint32_t w[8];
+      if constexpr (SIX) {
+        const uint32_t L[4] = {wv[u][0], wv[u][1], wv[u][2], wv[u][3]};
+        six_widen(L, wv[u][4], wv[u][5], w);
+      } else {
+        w[0] = wv[u][0]; w[1] = wv[u][1]; w[2] = wv[u][2]; w[3] = wv[u][3];
+      }
+      int32_t S[M][RELAXED ? 1 : 4];
+#pragma unroll
+      for (int t = 0; t < M; ++t) {
+#pragma unroll
+        for (int k = 0; k < (RELAXED ? 1 : 4); ++k) S[t][k] = 0;
+        if (active) {
           const int8_t *xt = a.xq + (int64_t)t * a.xq_stride + g * 32;
-          uint32_t x[SIX ? 8 : 4];
+          uint32_t x[8];
           if constexpr (SIX) {
             const uint4 x0 = reinterpret_cast<const uint4 *>(xt)[0], x1 = reinterpret_cast<const uint4 *>(xt)[1];
             x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
@@ -81,16 +101,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
             const uint4 x0 = *reinterpret_cast<const uint4 *>(xt + (lane & 1) * 16);
             x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
           }
-          constexpr int NW = SIX ? 8 : 4;
+          constexpr int NX = SIX ? 8 : 4;
           if constexpr (RELAXED) {
             int32_t acc = 0;
 #pragma unroll
-            for (int i = 0; i < NW; ++i) acc = dot4(w[i], centre4(x[i]), acc);
+            for (int i = 0; i < NX; ++i) acc = dot4(w[i], centre4(x[i]), acc);
             S[t][0] = acc;
           } else {
             // lane k of kernels/kernel.ts:222-229: bytes {2k, 2k+1} of words 0/2 (k < 2) or 1/3 (k >= 2) of each half
 #pragma unroll
-            for (int h = 0; h < NW; h += 4) {
+            for (int h = 0; h < NX; h += 4) {
               const int32_t even = dot4(w[h], x[h], dot4(w[h + 2], x[h + 2], 0));
               const int32_t odd = dot4(w[h + 1], x[h + 1], dot4(w[h + 3], x[h + 3], 0));
               const int32_t l0 = dot4(w[h] & 0xFFFFu, x[h], dot4(w[h + 2] & 0xFFFFu, x[h + 2], 0));
@@ -102,76 +122,62 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
             }
           }
         }
-      }
-      if constexpr (!SIX) {
-#pragma unroll
-        for (int t = 0; t < M; ++t)
+        if constexpr (!SIX) {
 #pragma unroll
           for (int k = 0; k < (RELAXED ? 1 : 4); ++k) S[t][k] += __shfl_xor(S[t][k], 1, 64);
-      }
-      if constexpr (SUMS) {
-        if (holder && active) {
-#pragma unroll
-          for (int t = 0; t < M; ++t) {
-            int32_t *o = a.sums + (((int64_t)t * a.total_rows + row) * G + g) * (RELAXED ? 1 : 4);
-#pragma unroll
-            for (int k = 0; k < (RELAXED ? 1 : 4); ++k) o[k] = S[t][k];
-          }
         }
-        continue;
       }
-      if (holder && active) {
-        const float wsg = srow[g];
+      if (!(holder && active)) continue;
+      if constexpr (SUMS) {
 #pragma unroll
         for (int t = 0; t < M; ++t) {
-          const float scale = wsg * a.xs[(int64_t)t * a.xs_stride + g];
+          int32_t *o = a.sums + (((int64_t)t * a.total_rows + row) * G + g) * (RELAXED ? 1 : 4);
+#pragma unroll
+          for (int k = 0; k < (RELAXED ? 1 : 4); ++k) o[k] = S[t][k];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+          const float scale = wsv[u] * a.xs[(int64_t)t * a.xs_stride + g];
+          float *pt = P + t * lay.stride;
           if constexpr (RELAXED) {
             const float p = (float)S[t][0] * scale;
-            if (g < G4) P[t * GPI + (mylocal & 3) * (GPI / 4) + (mylocal >> 2)] = p;
-            else tail[wave][t * 4 + (g - G4)] = p;
+            if (g < G4) pt[(g & 3) * lay.q + (g >> 2)] = p;
+            else pt[4 * lay.q + (g - G4)] = p;
           } else {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) P[t * GPI * 4 + k * GPI + mylocal] = (float)S[t][k] * scale;
+            for (int k = 0; k < 4; ++k) pt[k * lay.q + g] = (float)S[t][k] * scale;
           }
         }
       }
-      wave_sync_lds();
-      if (lane < 4 * M) {
-        const int t = lane >> 2, k = lane & 3;
-        if constexpr (RELAXED) {
-          const int n = min(GPI, G4 - it * GPI);  // groups of this step below G4 (a multiple of 4, or <= 0)
-          const float *c = P + t * GPI + k * (GPI / 4);
-          for (int j = 0; j < n / 4; ++j) chain = chain + c[j];
-        } else {
-          const int n = min(GPI, G - it * GPI);
-          const float *c = P + t * GPI * 4 + k * GPI;
-          for (int j = 0; j < n; ++j) chain = chain + c[j];
-        }
-      }
-      wave_sync_lds();
     }
-    if constexpr (SUMS) continue;
-    const int src = (lane < M ? lane : 0) * 4;
-    const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
-    const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
-    if (lane < M) {
-      float sum = ((c0 + c1) + c2) + c3;
-      if constexpr (RELAXED) {
-        for (int g = G4; g < G; ++g) sum = sum + tail[wave][lane * 4 + (g - G4)];
-      }
-      float *y = sg.y + (int64_t)lane * sg.y_stride + r;
-      *y = sg.accumulate ? *y + sum : sum;
+  }
+  if constexpr (SUMS) return;
+  wave_sync_lds();
+  float chain = 0.0f;  // lane 4t + k (t < M): accumulator k of token t
+  if (lane < 4 * M) {
+    const int t = lane >> 2, k = lane & 3;
+    chain = lds_chain(P + t * lay.stride + k * lay.q, RELAXED ? G4 / 4 : G, 0.0f);
+  }
+  const int src = (lane < M ? lane : 0) * 4;
+  const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
+  const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
+  if (lane < M) {
+    float sum = ((c0 + c1) + c2) + c3;
+    if constexpr (RELAXED) {
+      const float *tl = P + lane * lay.stride + 4 * lay.q;
+      for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
     }
-    wave_sync_lds();
+    float *y = sg.y + (int64_t)lane * sg.y_stride + r;
+    *y = sg.accumulate ? *y + sum : sum;
   }
 }
 
 template <int M, bool SIX, bool RELAXED, bool SUMS>
 hipError_t launch_m(const MatArgs &a, hipStream_t s) {
-  const int64_t waves = a.total_rows;
-  int blocks = (int)((waves + WAVES - 1) / WAVES);
-  if (blocks > 16384) blocks = 16384;
-  hipLaunchKernelGGL((gemv_kernel<M, SIX, RELAXED, SUMS>), dim3(blocks), dim3(64 * WAVES), 0, s, a);
+  const int blocks = (a.total_rows + WAVES - 1) / WAVES;
+  const size_t lds = SUMS ? 0 : sizeof(float) * WAVES * M * (size_t)row_layout(a.k, RELAXED).stride;
+  hipLaunchKernelGGL((gemv_kernel<M, SIX, RELAXED, SUMS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }
 
@@ -192,8 +198,16 @@ hipError_t launch_sel(const MatArgs &a, hipStream_t s) {
 
 }  // namespace
 
+int32_t gemv_tokens(int32_t k, bool relaxed) {
+  // the most tokens one launch takes: 8, fewer where a block's products would pass 64 KiB of LDS
+  const size_t per_token = sizeof(float) * WAVES * (size_t)row_layout(k, relaxed).stride;
+  int32_t m = (int32_t)((64 * 1024) / per_token);
+  return m < 1 ? 0 : (m > 8 ? 8 : m);
+}
+
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
+  if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;
   if (six) {
     if (relaxed) return sums ? launch_sel<true, true, true>(a, s) : launch_sel<true, true, false>(a, s);
     return sums ? launch_sel<true, false, true>(a, s) : launch_sel<true, false, false>(a, s);

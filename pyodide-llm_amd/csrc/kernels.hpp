@@ -34,6 +34,8 @@ struct MatArgs {
 
 // decode GEMV, m <= 8 tokens: exact int32 group sums, the reference's float32 order
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
+// the most tokens one launch_gemv takes for rows of k (its products of a row fit the block's LDS)
+int32_t gemv_tokens(int32_t k, bool relaxed);
 // prefill GEMM on i8 MFMA, any m: the same bits as launch_gemv per (token, row)
 hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
 bool gemm_supported(int32_t k, bool six);

@@ -34,23 +34,37 @@ __global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, co
 
 // rmsnorm of one token a block: the squares in four lanes (j % 4) added in order by four threads, hsum
 // ((l0 + l1) + l2) + l3, the tail in order; s = f32(1 / f32(sqrt(f32(ss / n) + eps))); out = w * (s * x); then
-// quantize_x of out
+// quantize_x of out. x and w are staged in LDS first, so that no global load waits inside the ordered parts.
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *xs, float *out, const float *x,
                                                             const float *w, int32_t n, int32_t x_stride,
                                                             int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                                             float eps, int32_t bias) {
   extern __shared__ float sm[];
-  float *xv = sm;       // n
   const int n4 = n & ~3, q4 = n4 >> 2, qs = (q4 + 3) & ~3;
-  float *sq = sm + n;   // 4 * qs, transposed: lane k's squares side by side (16-byte aligned rows)
+  float *xv = sm;            // n
+  float *wv = sm + n;        // n
+  float *sq = sm + 2 * n;    // 4 * qs, transposed: lane k's squares side by side (16-byte aligned rows)
   __shared__ float part[4];
   __shared__ float sval;
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *xt = x + (int64_t)t * x_stride;
-  for (int j = tid; j < n; j += 256) {
-    const float v = xt[j];
-    xv[j] = v;
-    if (j < n4) sq[(j & 3) * qs + (j >> 2)] = v * v;
+  if ((n & 3) == 0) {
+    for (int j4 = tid; j4 < n / 4; j4 += 256) {
+      const float4 v = reinterpret_cast<const float4 *>(xt)[j4];
+      reinterpret_cast<float4 *>(xv)[j4] = v;
+      reinterpret_cast<float4 *>(wv)[j4] = reinterpret_cast<const float4 *>(w)[j4];
+      sq[0 * qs + j4] = v.x * v.x;
+      sq[1 * qs + j4] = v.y * v.y;
+      sq[2 * qs + j4] = v.z * v.z;
+      sq[3 * qs + j4] = v.w * v.w;
+    }
+  } else {
+    for (int j = tid; j < n; j += 256) {
+      const float v = xt[j];
+      xv[j] = v;
+      wv[j] = w[j];
+      if (j < n4) sq[(j & 3) * qs + (j >> 2)] = v * v;
+    }
   }
   __syncthreads();
   if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
@@ -66,7 +80,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
   float *sc = xs + (int64_t)t * xs_stride;
   for (int g = tid >> 5; g < n / GS; g += 8) {
     const int j = g * GS + (tid & 31);
-    const float o = w[j] * (s * xv[j]);
+    const float o = wv[j] * (s * xv[j]);
     if (out) out[(int64_t)t * out_stride + j] = o;
     quantize_group(o, q, sc, j, g, bias);
   }
@@ -281,7 +295,7 @@ hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int
 hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s) {
-  const size_t lds = sizeof(float) * (size_t)(2 * n + 16);
+  const size_t lds = sizeof(float) * (size_t)(3 * n + 16);
   hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m), dim3(256), lds, s, xq, xs, out, x, w, n, x_stride, xq_stride,
                      xs_stride, out_stride, eps, bias);
   return hipGetLastError();
