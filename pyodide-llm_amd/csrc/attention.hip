@@ -53,10 +53,17 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   if (p0 >= count) return;
   const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
   const int np = min(TILE, count - p0);
-  for (int i = threadIdx.x; i < np * C4; i += 256) {
-    const int p = i / C4, c = i % C4;
-    *reinterpret_cast<float4 *>(ks + p * LD + 4 * c) =
-        cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
+  constexpr int NL = (TILE * C4 + 255) / 256;  // float4 of keys a thread, requested together
+  float4 kr4[NL];
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int i = threadIdx.x + u * 256, p = i / C4, c = i % C4;
+    if (p < np) kr4[u] = cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
+  }
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int i = threadIdx.x + u * 256, p = i / C4, c = i % C4;
+    if (p < np) *reinterpret_cast<float4 *>(ks + p * LD + 4 * c) = kr4[u];
   }
   const float *q = a.q + (int64_t)t * a.q_stride + (int64_t)kh * mul * HS;
   for (int i = threadIdx.x; i < mul * C4; i += 256)
@@ -97,13 +104,31 @@ __global__ __launch_bounds__(64) void softmax_kernel(const AttnArgs a) {
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
   float mx = -3.4028234663852886e38f;
-  for (int i = lane; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+  {
+    float tv[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) tv[u] = lane + 64 * u < tiles ? tm[lane + 64 * u] : mx;
+    mx = wmax(tv[0], tv[1]);
+    for (int i = lane + 128; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+  }
   for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
   float *tail = e4 + 4 * q4s;
-  for (int i = lane; i < count; i += 64) {
-    const float d = scores[i] - mx;
-    if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
-    else tail[i - count4] = fexp(d);
+  for (int base = 0; base < count; base += 64 * 16) {
+    float sv[16];  // sixteen scores a lane requested together
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = base + lane + 64 * u;
+      if (i < count) sv[u] = scores[i];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = base + lane + 64 * u;
+      if (i < count) {
+        const float d = sv[u] - mx;
+        if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
+        else tail[i - count4] = fexp(d);
+      }
+    }
   }
   wave_sync_lds();
   float part = 0.0f;

@@ -20,7 +20,10 @@ namespace ple {
 namespace {
 
 constexpr int WAVES = 4;
-constexpr int CHUNK = 8;  // wave steps requested at once
+// wave steps requested at once: 8 (8 KiB of an int8 row a wave) for one or two tokens, fewer where every token's
+// activations ride along in registers
+template <int M>
+constexpr int chunk_of() { return M <= 2 ? 8 : (M <= 4 ? 4 : 2); }
 
 struct RowLayout {  // a token's products in LDS: 4 accumulator rows of q floats, then the (up to 3) tail groups
   int q, stride;
@@ -35,6 +38,8 @@ template <int M, bool SIX, bool RELAXED, bool SUMS>
 __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   constexpr int GPI = SIX ? 64 : 32;  // groups a wave step
   constexpr int NW = SIX ? 8 : 4;     // words of weights a lane a step
+  constexpr int NX = SIX ? 8 : 4;     // words of a token's activations a lane a step
+  constexpr int CHUNK = chunk_of<M>();
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * WAVES + wave;
@@ -57,8 +62,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 
   for (int c0 = 0; c0 < steps; c0 += CHUNK) {
     uint32_t wv[CHUNK][NW];
-    float wsv[CHUNK];
-    // every load of the chunk first
+    uint32_t xv[CHUNK][M][NX];
+    float wsv[CHUNK], xsv[CHUNK][M];
+    // every load of the chunk first: the row's weights and scales, the tokens' activations and scales
 #pragma unroll
     for (int u = 0; u < CHUNK; ++u) {
       const int g = (c0 + u) * GPI + mylocal;
@@ -71,7 +77,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
           const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (int64_t)g * 32 + (lane & 1) * 16);
           wv[u][0] = v.x; wv[u][1] = v.y; wv[u][2] = v.z; wv[u][3] = v.w;
         }
-        if constexpr (!SUMS) wsv[u] = holder ? srow[g] : 0.0f;
+        if constexpr (!SUMS) {
+          wsv[u] = holder ? srow[g] : 0.0f;
+#pragma unroll
+          for (int t = 0; t < M; ++t) xsv[u][t] = holder ? a.xs[(int64_t)t * a.xs_stride + g] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+          const int8_t *xt = a.xq + (int64_t)t * a.xq_stride + g * 32;
+          if constexpr (SIX) {
+            const uint4 x0 = reinterpret_cast<const uint4 *>(xt)[0], x1 = reinterpret_cast<const uint4 *>(xt)[1];
+            xv[u][t][0] = x0.x; xv[u][t][1] = x0.y; xv[u][t][2] = x0.z; xv[u][t][3] = x0.w;
+            xv[u][t][4] = x1.x; xv[u][t][5] = x1.y; xv[u][t][6] = x1.z; xv[u][t][7] = x1.w;
+          } else {
+            const uint4 x0 = *reinterpret_cast<const uint4 *>(xt + (lane & 1) * 16);
+            xv[u][t][0] = x0.x; xv[u][t][1] = x0.y; xv[u][t][2] = x0.z; xv[u][t][3] = x0.w;
+          }
+        }
       }
     }
 #pragma unroll
@@ -92,16 +114,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 #pragma unroll
         for (int k = 0; k < (RELAXED ? 1 : 4); ++k) S[t][k] = 0;
         if (active) {
-          const int8_t *xt = a.xq + (int64_t)t * a.xq_stride + g * 32;
-          uint32_t x[8];
-          if constexpr (SIX) {
-            const uint4 x0 = reinterpret_cast<const uint4 *>(xt)[0], x1 = reinterpret_cast<const uint4 *>(xt)[1];
-            x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w; x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
-          } else {
-            const uint4 x0 = *reinterpret_cast<const uint4 *>(xt + (lane & 1) * 16);
-            x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
-          }
-          constexpr int NX = SIX ? 8 : 4;
+          const uint32_t *x = xv[u][t];
           if constexpr (RELAXED) {
             int32_t acc = 0;
 #pragma unroll
@@ -138,7 +151,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
       } else {
 #pragma unroll
         for (int t = 0; t < M; ++t) {
-          const float scale = wsv[u] * a.xs[(int64_t)t * a.xs_stride + g];
+          const float scale = wsv[u] * xsv[u][t];
           float *pt = P + t * lay.stride;
           if constexpr (RELAXED) {
             const float p = (float)S[t][0] * scale;

@@ -48,15 +48,29 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
   __shared__ float sval;
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *xt = x + (int64_t)t * x_stride;
-  if ((n & 3) == 0) {
-    for (int j4 = tid; j4 < n / 4; j4 += 256) {
-      const float4 v = reinterpret_cast<const float4 *>(xt)[j4];
-      reinterpret_cast<float4 *>(xv)[j4] = v;
-      reinterpret_cast<float4 *>(wv)[j4] = reinterpret_cast<const float4 *>(w)[j4];
-      sq[0 * qs + j4] = v.x * v.x;
-      sq[1 * qs + j4] = v.y * v.y;
-      sq[2 * qs + j4] = v.z * v.z;
-      sq[3 * qs + j4] = v.w * v.w;
+  if ((n & 3) == 0 && n <= 8 * 1024) {
+    // every load first (up to 8 float4 of x and of w a thread), then the stores
+    float4 xr[8], wr[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j4 = tid + u * 256;
+      if (j4 < n / 4) {
+        xr[u] = reinterpret_cast<const float4 *>(xt)[j4];
+        wr[u] = reinterpret_cast<const float4 *>(w)[j4];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j4 = tid + u * 256;
+      if (j4 < n / 4) {
+        const float4 v = xr[u];
+        reinterpret_cast<float4 *>(xv)[j4] = v;
+        reinterpret_cast<float4 *>(wv)[j4] = wr[u];
+        sq[0 * qs + j4] = v.x * v.x;
+        sq[1 * qs + j4] = v.y * v.y;
+        sq[2 * qs + j4] = v.z * v.z;
+        sq[3 * qs + j4] = v.w * v.w;
+      }
     }
   } else {
     for (int j = tid; j < n; j += 256) {
