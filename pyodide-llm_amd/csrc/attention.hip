@@ -7,7 +7,7 @@
 //   out_j: blocks of four positions in order, out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), then the positions past
 //           the fours one at a time, out = out + p v.
 // Three launches: (A) the scores of 64-position tiles, every CU streaming keys once for the nh / nkv query heads
-// that share them, with each tile's maxima; (B) one wave a (token, head): the exponentials, their ordered sum from
+// that share them, with each tile's maxima; (B) one block a (token, head): the exponentials, their ordered sum from
 // LDS, the weights; (C) one block a (token, kv head, 8 of the head's columns): 512-position chunks of values and
 // weights staged in LDS (the next chunk's loads in flight while this one is used), the four-position products, and
 // the ordered sums over the blocks, one thread a (head, column).
@@ -95,34 +95,43 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   }
 }
 
-// (B) one wave a (head, token): grid (nh, m), block 64
-__global__ __launch_bounds__(64) void softmax_kernel(const AttnArgs a) {
-  extern __shared__ float e4[];  // 4 rows of q4s exponentials (lane k's positions t % 4 == k), then the tail
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+// (B) one block a (head, token): grid (nh, m), block 256. The scores requested at once, the exponentials by every
+// thread into LDS (lane k's positions t % 4 == k side by side), the four ordered sums by four threads, the weights.
+__global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
+  extern __shared__ float e4[];  // 4 rows of q4s exponentials, then the tail
+  __shared__ float part[4];
+  __shared__ float shared_mx, shared_inv;
+  const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = (q4 + 3) & ~3;
   const int tiles = (count + TILE - 1) / TILE;
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
-  float mx = -3.4028234663852886e38f;
-  {
-    float tv[2];
+  float sv[16];  // up to 16 scores a thread, requested with the tile maxima
 #pragma unroll
-    for (int u = 0; u < 2; ++u) tv[u] = lane + 64 * u < tiles ? tm[lane + 64 * u] : mx;
-    mx = wmax(tv[0], tv[1]);
-    for (int i = lane + 128; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+  for (int u = 0; u < 16; ++u) {
+    const int i = tid + 256 * u;
+    if (i < count) sv[u] = scores[i];
   }
-  for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+  if (tid < 64) {
+    float mx = -3.4028234663852886e38f;
+    for (int i = tid; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+    if (tid == 0) shared_mx = mx;
+  }
+  __syncthreads();
+  const float mx = shared_mx;
   float *tail = e4 + 4 * q4s;
-  for (int base = 0; base < count; base += 64 * 16) {
-    float sv[16];  // sixteen scores a lane requested together
+  for (int base = 0; base < count; base += 256 * 16) {
+    if (base > 0) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int i = base + lane + 64 * u;
-      if (i < count) sv[u] = scores[i];
+      for (int u = 0; u < 16; ++u) {
+        const int i = base + tid + 256 * u;
+        if (i < count) sv[u] = scores[i];
+      }
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int i = base + lane + 64 * u;
+      const int i = base + tid + 256 * u;
       if (i < count) {
         const float d = sv[u] - mx;
         if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
@@ -130,14 +139,17 @@ __global__ __launch_bounds__(64) void softmax_kernel(const AttnArgs a) {
       }
     }
   }
-  wave_sync_lds();
-  float part = 0.0f;
-  if (lane < 4) part = lds_chain(e4 + lane * q4s, q4, 0.0f);
-  const float p1 = __shfl(part, 1, 64), p2 = __shfl(part, 2, 64), p3 = __shfl(part, 3, 64);
-  float sum = ((part + p1) + p2) + p3;  // lane 0's is the one
-  for (int i = 0; i < count - count4; ++i) sum = sum + tail[i];
-  const float inv = __shfl(1.0f / sum, 0, 64);
-  for (int i = lane; i < count; i += 64) {
+  __syncthreads();
+  if (tid < 4) part[tid] = lds_chain(e4 + tid * q4s, q4, 0.0f);
+  __syncthreads();
+  if (tid == 0) {
+    float sum = ((part[0] + part[1]) + part[2]) + part[3];
+    for (int i = 0; i < count - count4; ++i) sum = sum + tail[i];
+    shared_inv = 1.0f / sum;
+  }
+  __syncthreads();
+  const float inv = shared_inv;
+  for (int i = tid; i < count; i += 256) {
     const float e = i < count4 ? e4[(i & 3) * q4s + (i >> 2)] : tail[i - count4];
     scores[i] = e * inv;
   }
@@ -147,9 +159,10 @@ __global__ __launch_bounds__(64) void softmax_kernel(const AttnArgs a) {
 template <int HS, bool HALF>
 __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
   constexpr int NB = CH / 4;  // four-position blocks a chunk
+  constexpr int PS = CH + 4, BS = NB + 4;   // padded rows: heads and columns fall on different LDS banks
   __shared__ float vs[CH * PVJ];            // [position][column]
-  __shared__ float ps[MAXMUL * CH];         // [head][position]
-  __shared__ float bs[MAXMUL * PVJ * NB];   // [head][column][block]
+  __shared__ float ps[MAXMUL * PS];         // [head][position]
+  __shared__ float bs[MAXMUL * PVJ * BS];   // [head][column][block]
   const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
   const int count = a.pos0 + t + 1, count4 = count & ~3;
   const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
@@ -182,21 +195,22 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) reinterpret_cast<float4 *>(vs)[tid + u * 256] = vreg[u];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (tid + u * 256 < mul * CH / 4) reinterpret_cast<float4 *>(ps)[tid + u * 256] = preg[u];
-    __syncthreads();
-    if (c0 + CH < count4) fetch(c0 + CH);  // the next chunk's loads fly while this one is used
-    for (int i = tid; i < mul * PVJ * NB; i += 256) {
-      const int b = i % NB, j = (i / NB) % PVJ, hl = i / (NB * PVJ);
-      if (hl < mul && b < nb) {
-        const float *pp = ps + hl * CH + 4 * b, *vv = vs + 4 * b * PVJ + j;
-        const float pair0 = pp[0] * vv[0] + pp[1] * vv[PVJ];
-        const float pair1 = pp[2] * vv[2 * PVJ] + pp[3] * vv[3 * PVJ];
-        bs[(hl * PVJ + j) * NB + b] = pair0 + pair1;
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int i = tid + u * 256;
+      if (i < mul * CH / 4) reinterpret_cast<float4 *>(ps + (i / (CH / 4)) * PS)[i % (CH / 4)] = preg[u];
     }
     __syncthreads();
-    if (tid < chains) acc = lds_chain(bs + (hl_me * PVJ + j_me) * NB, nb, acc);
+    if (c0 + CH < count4) fetch(c0 + CH);  // the next chunk's loads fly while this one is used
+    for (int i = tid; i < mul * PVJ * nb; i += 256) {
+      // the column fastest, then the head, then the block: a wave reads few value rows and broadcasts the weights
+      const int j = i % PVJ, hl = (i / PVJ) % mul, b = i / (PVJ * mul);
+      const float *pp = ps + hl * PS + 4 * b, *vv = vs + 4 * b * PVJ + j;
+      const float pair0 = pp[0] * vv[0] + pp[1] * vv[PVJ];
+      const float pair1 = pp[2] * vv[2 * PVJ] + pp[3] * vv[3 * PVJ];
+      bs[(hl * PVJ + j) * BS + b] = pair0 + pair1;
+    }
+    __syncthreads();
+    if (tid < chains) acc = lds_chain(bs + (hl_me * PVJ + j_me) * BS, nb, acc);
     __syncthreads();
   }
   if (tid < chains) {
@@ -213,7 +227,7 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
   const int most4 = (a.pos0 + a.m) & ~3;
   const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
-  hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(64), lds_b, s, a);
+  hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
   hipLaunchKernelGGL((pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
   return hipGetLastError();
 }
