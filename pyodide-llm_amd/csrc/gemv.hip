@@ -186,127 +186,113 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   }
 }
 
-// The decode path proper (one token, int8, bias 64): each wave keeps the token's activations in registers and walks
-// rows grid-stride, the next row's weights and scales requested before the current row is reduced, so that every wave
-// has a whole row in flight at all times. NS: wave steps (1 KiB of a row) the kernel holds, NS * 1024 >= K.
-template <int NS>
+// The decode path proper (one token, int8, bias 64): a wave takes R consecutive rows (about 16 KiB of weights) and
+// requests all of them, with their scales and the token's activations, before it uses any; the R rows' products go
+// to LDS and 4R lanes add them in the reference's order at once. NS: wave steps (1 KiB of a row), NS * 1024 >= K.
+template <int R, int NS>
 __global__ __launch_bounds__(256) void gemv1_kernel(const MatArgs a) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int K = a.k, G = K / GS, G4 = G & ~3;
   const int steps = (G + 31) / 32;
   const RowLayout lay = row_layout(K, true);
-  float *P = smem + wave * lay.stride;
+  float *P = smem + wave * R * lay.stride;
   const bool holder = (lane & 1) == 0;
   const int half = (lane & 1) * 16;
-  uint32_t xr[NS][4];
-  float xsr[NS];
+  const int row0 = (blockIdx.x * WAVES + wave) * R;
+  if (row0 >= a.total_rows) return;
+  uint32_t wr[R][NS][4], xr[NS][4];
+  float wsr[R][NS], xsr[NS];
 #pragma unroll
-  for (int u = 0; u < NS; ++u) {
-    const int g = u * 32 + (lane >> 1);
-    if (u < steps && g < G) {
-      const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq + g * 32 + half);
-      xr[u][0] = centre4(x0.x); xr[u][1] = centre4(x0.y); xr[u][2] = centre4(x0.z); xr[u][3] = centre4(x0.w);
-      xsr[u] = a.xs[g];
-    }
-  }
-  int row = blockIdx.x * WAVES + wave;
-  const int nwaves = gridDim.x * WAVES;
-  if (row >= a.total_rows) return;
-  auto locate = [&](int rw, const uint8_t *&w, const float *&ws, int &seg, int &r) {
-    seg = 0;
-    r = rw;
+  for (int i = 0; i < R; ++i) {
+    const int row = row0 + i;
+    if (row >= a.total_rows) continue;
+    int seg = 0, r = row;
     while (seg + 1 < a.nseg && r >= a.seg[seg].rows) {
       r -= a.seg[seg].rows;
       ++seg;
     }
-    w = a.seg[seg].w + (int64_t)r * K;
-    ws = a.seg[seg].ws + (int64_t)r * G;
-  };
-  uint32_t cur[NS][4], nxt[NS][4];
-  float wcur[NS], wnxt[NS];
-  auto fetch = [&](int rw, uint32_t (&wv)[NS][4], float (&sv)[NS]) {
-    const uint8_t *w;
-    const float *ws;
-    int seg, r;
-    locate(rw, w, ws, seg, r);
+    const uint8_t *w = a.seg[seg].w + (int64_t)r * K;
+    const float *ws = a.seg[seg].ws + (int64_t)r * G;
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
       const int g = u * 32 + (lane >> 1);
       if (u < steps && g < G) {
         const uint4 v = *reinterpret_cast<const uint4 *>(w + (int64_t)g * 32 + half);
-        wv[u][0] = v.x; wv[u][1] = v.y; wv[u][2] = v.z; wv[u][3] = v.w;
-        sv[u] = holder ? ws[g] : 0.0f;
+        wr[i][u][0] = v.x; wr[i][u][1] = v.y; wr[i][u][2] = v.z; wr[i][u][3] = v.w;
+        wsr[i][u] = holder ? ws[g] : 0.0f;
       }
     }
-  };
-  fetch(row, cur, wcur);
-  for (;;) {
-    const int next = row + nwaves;
-    const bool more = next < a.total_rows;
-    if (more) fetch(next, nxt, wnxt);
+  }
 #pragma unroll
-    for (int u = 0; u < NS; ++u) {
-      const int g = u * 32 + (lane >> 1);
-      if (u < steps) {
-        int32_t S = 0;
-        if (g < G) {
+  for (int u = 0; u < NS; ++u) {
+    const int g = u * 32 + (lane >> 1);
+    if (u < steps && g < G) {
+      const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq + g * 32 + half);
+      xr[u][0] = x0.x; xr[u][1] = x0.y; xr[u][2] = x0.z; xr[u][3] = x0.w;
+      xsr[u] = holder ? a.xs[g] : 0.0f;
+    }
+  }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) S = dot4(cur[u][i], xr[u][i], S);
-        }
-        S += __shfl_xor(S, 1, 64);
-        if (holder && g < G) {
-          const float p = (float)S * (wcur[u] * xsr[u]);
-          if (g < G4) P[(g & 3) * lay.q + (g >> 2)] = p;
-          else P[4 * lay.q + (g - G4)] = p;
-        }
+  for (int u = 0; u < NS; ++u) {
+    if (u >= steps) break;
+    const int g = u * 32 + (lane >> 1);
+    uint32_t xc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xc[j] = centre4(xr[u][j]);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      int32_t S = 0;
+      if (g < G) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S = dot4(wr[i][u][j], xc[j], S);
+      }
+      S += __shfl_xor(S, 1, 64);
+      if (holder && g < G) {
+        const float p = (float)S * (wsr[i][u] * xsr[u]);
+        float *pi = P + i * lay.stride;
+        if (g < G4) pi[(g & 3) * lay.q + (g >> 2)] = p;
+        else pi[4 * lay.q + (g - G4)] = p;
       }
     }
-    wave_sync_lds();
-    float chain = 0.0f;
-    if (lane < 4) chain = lds_chain(P + lane * lay.q, G4 / 4, 0.0f);
-    const float c1 = __shfl(chain, 1, 64), c2 = __shfl(chain, 2, 64), c3 = __shfl(chain, 3, 64);
-    if (lane == 0) {
-      float sum = ((chain + c1) + c2) + c3;
-      for (int g = G4; g < G; ++g) sum = sum + P[4 * lay.q + (g - G4)];
-      const uint8_t *w;
-      const float *ws;
-      int seg, r;
-      locate(row, w, ws, seg, r);
-      float *y = a.seg[seg].y + r;
-      *y = a.seg[seg].accumulate ? *y + sum : sum;
+  }
+  wave_sync_lds();
+  float chain = 0.0f;  // lane 4i + k: accumulator k of row row0 + i
+  if (lane < 4 * R) chain = lds_chain(P + (lane >> 2) * lay.stride + (lane & 3) * lay.q, G4 / 4, 0.0f);
+  const int src = (lane < R ? lane : 0) * 4;
+  const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
+  const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
+  if (lane < R && row0 + lane < a.total_rows) {
+    float sum = ((c0 + c1) + c2) + c3;
+    const float *tl = P + lane * lay.stride + 4 * lay.q;
+    for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
+    int seg = 0, r = row0 + lane;
+    while (seg + 1 < a.nseg && r >= a.seg[seg].rows) {
+      r -= a.seg[seg].rows;
+      ++seg;
     }
-    wave_sync_lds();
-    if (!more) break;
-    row = next;
-#pragma unroll
-    for (int u = 0; u < NS; ++u) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cur[u][i] = nxt[u][i];
-      wcur[u] = wnxt[u];
-    }
+    float *y = a.seg[seg].y + r;
+    *y = a.seg[seg].accumulate ? *y + sum : sum;
   }
 }
 
-template <int NS>
+template <int R, int NS>
 hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
-  // waves in flight: 16 a CU for short rows, 8 for long ones (their registers), never more than rows
-  const int target = 256 * (NS <= 8 ? 16 : 8);
-  const int waves = a.total_rows < target ? a.total_rows : target;
+  const int waves = (a.total_rows + R - 1) / R;
   const int blocks = (waves + WAVES - 1) / WAVES;
-  const size_t lds = sizeof(float) * WAVES * (size_t)row_layout(a.k, true).stride;
-  hipLaunchKernelGGL((gemv1_kernel<NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+  const size_t lds = sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
+  hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_decode(const MatArgs &a, hipStream_t s) {
-  const int steps = (a.k / GS + 31) / 32;
-  if (steps <= 1) return launch_gemv1<1>(a, s);
-  if (steps <= 2) return launch_gemv1<2>(a, s);
-  if (steps <= 4) return launch_gemv1<4>(a, s);
-  if (steps <= 8) return launch_gemv1<8>(a, s);
-  if (steps <= 14) return launch_gemv1<14>(a, s);
-  if (steps <= 20) return launch_gemv1<20>(a, s);
+  const int steps = (a.k / GS + 31) / 32;  // 1 KiB steps of a row
+  if (steps <= 1) return launch_gemv1<4, 1>(a, s);
+  if (steps <= 2) return launch_gemv1<4, 2>(a, s);
+  if (steps <= 4) return launch_gemv1<4, 4>(a, s);
+  if (steps <= 8) return launch_gemv1<2, 8>(a, s);
+  if (steps <= 16) return launch_gemv1<1, 16>(a, s);
+  if (steps <= 20) return launch_gemv1<1, 20>(a, s);
   return hipErrorInvalidValue;
 }
 
