@@ -57,8 +57,8 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   float4 kr4[NL];
 #pragma unroll
   for (int u = 0; u < NL; ++u) {
-    const int i = threadIdx.x + u * 256, p = i / C4, c = i % C4;
-    if (p < np) kr4[u] = cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
+    const int i = threadIdx.x + u * 256, p = min(i / C4, np - 1), c = i % C4;  // clamped, unconditional
+    kr4[u] = cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
   }
 #pragma unroll
   for (int u = 0; u < NL; ++u) {
@@ -108,10 +108,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
   float sv[16];  // up to 16 scores a thread, requested with the tile maxima
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int i = tid + 256 * u;
-    if (i < count) sv[u] = scores[i];
-  }
+  for (int u = 0; u < 16; ++u) sv[u] = scores[min(tid + 256 * u, count - 1)];  // clamped, unconditional
   if (tid < 64) {
     float mx = -3.4028234663852886e38f;
     for (int i = tid; i < tiles; i += 64) mx = wmax(mx, tm[i]);
@@ -124,10 +121,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   for (int base = 0; base < count; base += 256 * 16) {
     if (base > 0) {
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int i = base + tid + 256 * u;
-        if (i < count) sv[u] = scores[i];
-      }
+      for (int u = 0; u < 16; ++u) sv[u] = scores[min(base + tid + 256 * u, count - 1)];
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
@@ -174,19 +168,18 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
   static_assert(CH * PVJ / 4 == 4 * 256 && MAXMUL * CH / 4 <= 4 * 256, "the chunk's loads are four a thread");
   float4 vreg[4], preg[4];
   auto fetch = [&](int c0) {
+    // clamped addresses, unconditional loads (the values past count4 are never used)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = tid + u * 256;  // float4 i: position i / 2, columns 4 (i % 2)..
-      const int p = c0 + (i >> 1);
-      vreg[u] = p < count4 ? cache4<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + 4 * (i & 1))
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int p = min(c0 + (i >> 1), count4 - 1);
+      vreg[u] = cache4<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + 4 * (i & 1));
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = tid + u * 256;  // float4 i of [head][position / 4]
-      const int hl = i / (CH / 4), p = c0 + 4 * (i % (CH / 4));
-      preg[u] = (hl < mul && p < count4) ? *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int hl = min(i / (CH / 4), mul - 1), p = min(c0 + 4 * (i % (CH / 4)), count4 - 4);
+      preg[u] = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
     }
   };
   if (count4 > 0) fetch(0);

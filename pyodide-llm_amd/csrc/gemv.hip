@@ -67,8 +67,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
     // every load of the chunk first: the row's weights and scales, the tokens' activations and scales
 #pragma unroll
     for (int u = 0; u < CHUNK; ++u) {
-      const int g = (c0 + u) * GPI + mylocal;
-      if (c0 + u < steps && g < G) {
+      const int g = min((c0 + u) * GPI + mylocal, G - 1);  // clamped: every load unconditional
+      {
         if constexpr (SIX) {
           const uint2 *p = reinterpret_cast<const uint2 *>(wrow + (int64_t)g * 24);
           const uint2 l0 = p[0], l1 = p[1], tops = p[2];
@@ -78,9 +78,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
           wv[u][0] = v.x; wv[u][1] = v.y; wv[u][2] = v.z; wv[u][3] = v.w;
         }
         if constexpr (!SUMS) {
-          wsv[u] = holder ? srow[g] : 0.0f;
+          wsv[u] = srow[g];
 #pragma unroll
-          for (int t = 0; t < M; ++t) xsv[u][t] = holder ? a.xs[(int64_t)t * a.xs_stride + g] : 0.0f;
+          for (int t = 0; t < M; ++t) xsv[u][t] = a.xs[(int64_t)t * a.xs_stride + g];
         }
 #pragma unroll
         for (int t = 0; t < M; ++t) {
@@ -205,8 +205,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const MatArgs a) {
   float wsr[R][NS], xsr[NS];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int row = row0 + i;
-    if (row >= a.total_rows) continue;
+    const int row = min(row0 + i, a.total_rows - 1);  // rows past the end read the last row again, unused
     int seg = 0, r = row;
     while (seg + 1 < a.nseg && r >= a.seg[seg].rows) {
       r -= a.seg[seg].rows;
@@ -214,24 +213,21 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const MatArgs a) {
     }
     const uint8_t *w = a.seg[seg].w + (int64_t)r * K;
     const float *ws = a.seg[seg].ws + (int64_t)r * G;
+    // unconditional loads from clamped (always valid) addresses: a load under a branch is waited for before the next
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
-      const int g = u * 32 + (lane >> 1);
-      if (u < steps && g < G) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(w + (int64_t)g * 32 + half);
-        wr[i][u][0] = v.x; wr[i][u][1] = v.y; wr[i][u][2] = v.z; wr[i][u][3] = v.w;
-        wsr[i][u] = holder ? ws[g] : 0.0f;
-      }
+      const int g = min(u * 32 + (lane >> 1), G - 1);
+      const uint4 v = *reinterpret_cast<const uint4 *>(w + (int64_t)g * 32 + half);
+      wr[i][u][0] = v.x; wr[i][u][1] = v.y; wr[i][u][2] = v.z; wr[i][u][3] = v.w;
+      wsr[i][u] = ws[g];
     }
   }
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
-    const int g = u * 32 + (lane >> 1);
-    if (u < steps && g < G) {
-      const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq + g * 32 + half);
-      xr[u][0] = x0.x; xr[u][1] = x0.y; xr[u][2] = x0.z; xr[u][3] = x0.w;
-      xsr[u] = holder ? a.xs[g] : 0.0f;
-    }
+    const int g = min(u * 32 + (lane >> 1), G - 1);
+    const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq + g * 32 + half);
+    xr[u][0] = x0.x; xr[u][1] = x0.y; xr[u][2] = x0.z; xr[u][3] = x0.w;
+    xsr[u] = a.xs[g];
   }
 #pragma unroll
   for (int u = 0; u < NS; ++u) {

@@ -53,11 +53,9 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
     float4 xr[8], wr[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int j4 = tid + u * 256;
-      if (j4 < n / 4) {
-        xr[u] = reinterpret_cast<const float4 *>(xt)[j4];
-        wr[u] = reinterpret_cast<const float4 *>(w)[j4];
-      }
+      const int j4 = min(tid + u * 256, n / 4 - 1);  // clamped: the loads are unconditional, so none waits
+      xr[u] = reinterpret_cast<const float4 *>(xt)[j4];
+      wr[u] = reinterpret_cast<const float4 *>(w)[j4];
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
