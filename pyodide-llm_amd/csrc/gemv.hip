@@ -34,6 +34,22 @@ __host__ __device__ inline RowLayout row_layout(int k, bool relaxed) {
   return {q, 4 * q + 4};
 }
 
+// the segment (matrix) of a launch's row r, with constant indices into the arguments only, so that they stay in
+// scalar registers (a dynamic index makes the compiler read them from memory and wait on every load before it)
+struct RowAt {
+  const uint8_t *w;
+  const float *ws;
+  float *y;
+  int32_t r, y_stride, accumulate;
+};
+__device__ __forceinline__ RowAt row_at(const MatArgs &a, int row) {
+  const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
+  if (a.nseg > 2 && row >= n0 + n1)
+    return {a.seg[2].w, a.seg[2].ws, a.seg[2].y, row - n0 - n1, a.seg[2].y_stride, a.seg[2].accumulate};
+  if (a.nseg > 1 && row >= n0) return {a.seg[1].w, a.seg[1].ws, a.seg[1].y, row - n0, a.seg[1].y_stride, a.seg[1].accumulate};
+  return {a.seg[0].w, a.seg[0].ws, a.seg[0].y, row, a.seg[0].y_stride, a.seg[0].accumulate};
+}
+
 template <int M, bool SIX, bool RELAXED, bool SUMS>
 __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   constexpr int GPI = SIX ? 64 : 32;  // groups a wave step
@@ -51,12 +67,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   const bool holder = SIX ? true : ((lane & 1) == 0);
   const int mylocal = SIX ? lane : (lane >> 1);
 
-  int s = 0, r = row;
-  while (s + 1 < a.nseg && r >= a.seg[s].rows) {
-    r -= a.seg[s].rows;
-    ++s;
-  }
-  const MatSeg sg = a.seg[s];
+  const RowAt sg = row_at(a, row);
+  const int r = sg.r;
   const uint8_t *wrow = sg.w + (int64_t)r * (SIX ? (int64_t)G * 24 : (int64_t)K);
   const float *srow = SUMS ? nullptr : sg.ws + (int64_t)r * G;
 
@@ -187,32 +199,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 }
 
 // The decode path proper (one token, int8, bias 64): a wave takes R consecutive rows (about 16 KiB of weights) and
-// requests all of them, with their scales and the token's activations, before it uses any; the R rows' products go
-// to LDS and 4R lanes add them in the reference's order at once. NS: wave steps (1 KiB of a row), NS * 1024 >= K.
+// requests all of them with their scales before anything else (a scheduling barrier keeps the compiler from sinking
+// the loads next to their uses); meanwhile the block stages the token's activations, centred, and their scales in
+// LDS once. The R rows' products go to LDS and 4R lanes add them in the reference's order at once.
+// NS: wave steps (1 KiB of a row), NS * 1024 >= K.
 template <int R, int NS>
-__global__ __launch_bounds__(256) void gemv1_kernel(const MatArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv1_kernel(const MatArgs a) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int K = a.k, G = K / GS, G4 = G & ~3;
   const int steps = (G + 31) / 32;
   const RowLayout lay = row_layout(K, true);
-  float *P = smem + wave * R * lay.stride;
+  uint32_t *xl = reinterpret_cast<uint32_t *>(smem);                  // K bytes of centred activations
+  float *xsl = smem + K / 4;                                          // G scales
+  float *P = smem + K / 4 + ((G + 3) & ~3) + wave * R * lay.stride;  // this wave's products
   const bool holder = (lane & 1) == 0;
   const int half = (lane & 1) * 16;
-  const int row0 = (blockIdx.x * WAVES + wave) * R;
-  if (row0 >= a.total_rows) return;
-  uint32_t wr[R][NS][4], xr[NS][4];
-  float wsr[R][NS], xsr[NS];
+  const int row0 = min((blockIdx.x * WAVES + wave) * R, a.total_rows - 1);
+  uint32_t wr[R][NS][4];
+  float wsr[R][NS];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int row = min(row0 + i, a.total_rows - 1);  // rows past the end read the last row again, unused
-    int seg = 0, r = row;
-    while (seg + 1 < a.nseg && r >= a.seg[seg].rows) {
-      r -= a.seg[seg].rows;
-      ++seg;
-    }
-    const uint8_t *w = a.seg[seg].w + (int64_t)r * K;
-    const float *ws = a.seg[seg].ws + (int64_t)r * G;
+    const RowAt at = row_at(a, min(row0 + i, a.total_rows - 1));  // rows past the end: the last again, unused
+    const uint8_t *w = at.w + (int64_t)at.r * K;
+    const float *ws = at.ws + (int64_t)at.r * G;
     // unconditional loads from clamped (always valid) addresses: a load under a branch is waited for before the next
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
@@ -222,30 +232,47 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const MatArgs a) {
       wsr[i][u] = ws[g];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // the block's activations: K / 16 uint4, up to NS * 4 a thread
+  {
+    constexpr int XL = (NS * 1024 / 16 + 255) / 256;
+    uint4 xv[XL];
+    float sv[(NS * 32 + 255) / 256];
 #pragma unroll
-  for (int u = 0; u < NS; ++u) {
-    const int g = min(u * 32 + (lane >> 1), G - 1);
-    const uint4 x0 = *reinterpret_cast<const uint4 *>(a.xq + g * 32 + half);
-    xr[u][0] = x0.x; xr[u][1] = x0.y; xr[u][2] = x0.z; xr[u][3] = x0.w;
-    xsr[u] = a.xs[g];
+    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
+#pragma unroll
+    for (int u = 0; u < (NS * 32 + 255) / 256; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < K / 16)
+        reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
+                                                      centre4(xv[u].w));
+    }
+#pragma unroll
+    for (int u = 0; u < (NS * 32 + 255) / 256; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < G) xsl[i] = sv[u];
+    }
   }
+  __syncthreads();
+  if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     if (u >= steps) break;
     const int g = u * 32 + (lane >> 1);
-    uint32_t xc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xc[j] = centre4(xr[u][j]);
+    const int gc = min(g, G - 1);
+    const uint4 x4 = reinterpret_cast<const uint4 *>(xl)[(gc * 32 + half) / 16];
+    const uint32_t xc[4] = {x4.x, x4.y, x4.z, x4.w};
+    const float xs_g = xsl[gc];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       int32_t S = 0;
-      if (g < G) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) S = dot4(wr[i][u][j], xc[j], S);
-      }
+      for (int j = 0; j < 4; ++j) S = dot4(wr[i][u][j], xc[j], S);
       S += __shfl_xor(S, 1, 64);
       if (holder && g < G) {
-        const float p = (float)S * (wsr[i][u] * xsr[u]);
+        const float p = (float)S * (wsr[i][u] * xs_g);
         float *pi = P + i * lay.stride;
         if (g < G4) pi[(g & 3) * lay.q + (g >> 2)] = p;
         else pi[4 * lay.q + (g - G4)] = p;
@@ -262,13 +289,9 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const MatArgs a) {
     float sum = ((c0 + c1) + c2) + c3;
     const float *tl = P + lane * lay.stride + 4 * lay.q;
     for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
-    int seg = 0, r = row0 + lane;
-    while (seg + 1 < a.nseg && r >= a.seg[seg].rows) {
-      r -= a.seg[seg].rows;
-      ++seg;
-    }
-    float *y = a.seg[seg].y + r;
-    *y = a.seg[seg].accumulate ? *y + sum : sum;
+    const RowAt at = row_at(a, row0 + lane);
+    float *y = at.y + at.r;
+    *y = at.accumulate ? *y + sum : sum;
   }
 }
 
@@ -276,7 +299,8 @@ template <int R, int NS>
 hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const int waves = (a.total_rows + R - 1) / R;
   const int blocks = (waves + WAVES - 1) / WAVES;
-  const size_t lds = sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
+  const size_t lds = (size_t)a.k + sizeof(float) * (((a.k / GS) + 3) & ~3) +
+                     sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
   hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }

@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, co
 // rmsnorm of one token a block: the squares in four lanes (j % 4) added in order by four threads, hsum
 // ((l0 + l1) + l2) + l3, the tail in order; s = f32(1 / f32(sqrt(f32(ss / n) + eps))); out = w * (s * x); then
 // quantize_x of out. x and w are staged in LDS first, so that no global load waits inside the ordered parts.
-__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *xs, float *out, const float *x,
+__global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *xs, float *out, const float *x,
                                                             const float *w, int32_t n, int32_t x_stride,
                                                             int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                                             float eps, int32_t bias) {
@@ -49,17 +49,17 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
   const int t = blockIdx.x, tid = threadIdx.x;
   const float *xt = x + (int64_t)t * x_stride;
   if ((n & 3) == 0 && n <= 8 * 1024) {
-    // every load first (up to 8 float4 of x and of w a thread), then the stores
-    float4 xr[8], wr[8];
+    // every load first (up to 2 float4 of x and of w a thread), then the stores
+    float4 xr[2], wr[2];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j4 = min(tid + u * 256, n / 4 - 1);  // clamped: the loads are unconditional, so none waits
+    for (int u = 0; u < 2; ++u) {
+      const int j4 = min(tid + u * 1024, n / 4 - 1);  // clamped: the loads are unconditional, so none waits
       xr[u] = reinterpret_cast<const float4 *>(xt)[j4];
       wr[u] = reinterpret_cast<const float4 *>(w)[j4];
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j4 = tid + u * 256;
+    for (int u = 0; u < 2; ++u) {
+      const int j4 = tid + u * 1024;
       if (j4 < n / 4) {
         const float4 v = xr[u];
         reinterpret_cast<float4 *>(xv)[j4] = v;
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
       }
     }
   } else {
-    for (int j = tid; j < n; j += 256) {
+    for (int j = tid; j < n; j += 1024) {
       const float v = xt[j];
       xv[j] = v;
       wv[j] = w[j];
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(int8_t *xq, float *x
   const float s = sval;
   int8_t *q = xq + (int64_t)t * xq_stride;
   float *sc = xs + (int64_t)t * xs_stride;
-  for (int g = tid >> 5; g < n / GS; g += 8) {
+  for (int g = tid >> 5; g < n / GS; g += 32) {
     const int j = g * GS + (tid & 31);
     const float o = wv[j] * (s * xv[j]);
     if (out) out[(int64_t)t * out_stride + j] = o;
@@ -308,7 +308,7 @@ hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s) {
   const size_t lds = sizeof(float) * (size_t)(3 * n + 16);
-  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m), dim3(256), lds, s, xq, xs, out, x, w, n, x_stride, xq_stride,
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m), dim3(1024), lds, s, xq, xs, out, x, w, n, x_stride, xq_stride,
                      xs_stride, out_stride, eps, bias);
   return hipGetLastError();
 }
