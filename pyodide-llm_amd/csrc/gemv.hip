@@ -205,19 +205,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 // NS: wave steps (1 KiB of a row), NS * 1024 >= K.
 template <int R, int NS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv1_kernel(const MatArgs a) {
+  constexpr int SV = (NS * 32 + 255) / 256;  // float4 of a row's scales a lane
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int K = a.k, G = K / GS, G4 = G & ~3;
+  const int K = a.k, G = K / GS, G4 = G & ~3, G16 = (G + 3) & ~3;
   const int steps = (G + 31) / 32;
   const RowLayout lay = row_layout(K, true);
-  uint32_t *xl = reinterpret_cast<uint32_t *>(smem);                  // K bytes of centred activations
-  float *xsl = smem + K / 4;                                          // G scales
-  float *P = smem + K / 4 + ((G + 3) & ~3) + wave * R * lay.stride;  // this wave's products
+  uint32_t *xl = reinterpret_cast<uint32_t *>(smem);   // K bytes of centred activations
+  float *xsl = smem + K / 4;                           // G scales of the activations
+  float *wsl = xsl + G16 + wave * R * G16;             // this wave's rows' weight scales
+  float *P = xsl + G16 + WAVES * R * G16 + wave * R * lay.stride;  // this wave's products
   const bool holder = (lane & 1) == 0;
   const int half = (lane & 1) * 16;
   const int row0 = min((blockIdx.x * WAVES + wave) * R, a.total_rows - 1);
   uint32_t wr[R][NS][4];
-  float wsr[R][NS];
+  float4 sr[R][SV];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const RowAt at = row_at(a, min(row0 + i, a.total_rows - 1));  // rows past the end: the last again, unused
@@ -229,7 +231,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       const int g = min(u * 32 + (lane >> 1), G - 1);
       const uint4 v = *reinterpret_cast<const uint4 *>(w + (int64_t)g * 32 + half);
       wr[i][u][0] = v.x; wr[i][u][1] = v.y; wr[i][u][2] = v.z; wr[i][u][3] = v.w;
-      wsr[i][u] = ws[g];
+    }
+    // the row's scales as float4 (a row's scales start 4-byte aligned only: read them one float at a time where
+    // the row does not start on 16 bytes)
+#pragma unroll
+    for (int u = 0; u < SV; ++u) {
+      const int f = min(4 * (lane + 64 * u), G16 - 4);
+      if ((reinterpret_cast<uintptr_t>(ws) & 15) == 0 && f + 4 <= G) {
+        sr[i][u] = *reinterpret_cast<const float4 *>(ws + f);
+      } else {
+        sr[i][u] = make_float4(ws[min(f, G - 1)], ws[min(f + 1, G - 1)], ws[min(f + 2, G - 1)], ws[min(f + 3, G - 1)]);
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -255,6 +267,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       if (i < G) xsl[i] = sv[u];
     }
   }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int u = 0; u < SV; ++u) {
+      const int f = 4 * (lane + 64 * u);
+      if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
+    }
   __syncthreads();
   if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
 #pragma unroll
@@ -272,7 +291,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       for (int j = 0; j < 4; ++j) S = dot4(wr[i][u][j], xc[j], S);
       S += __shfl_xor(S, 1, 64);
       if (holder && g < G) {
-        const float p = (float)S * (wsr[i][u] * xs_g);
+        const float p = (float)S * (wsl[i * G16 + g] * xs_g);
         float *pi = P + i * lay.stride;
         if (g < G4) pi[(g & 3) * lay.q + (g >> 2)] = p;
         else pi[4 * lay.q + (g - G4)] = p;
@@ -299,7 +318,8 @@ template <int R, int NS>
 hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const int waves = (a.total_rows + R - 1) / R;
   const int blocks = (waves + WAVES - 1) / WAVES;
-  const size_t lds = (size_t)a.k + sizeof(float) * (((a.k / GS) + 3) & ~3) +
+  const size_t g16 = ((a.k / GS) + 3) & ~3;
+  const size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
                      sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
   hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
