@@ -166,34 +166,41 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
   float acc = 0.0f;
   // per chunk: CH * PVJ / 4 float4 of values (4 a thread) and mul * CH / 4 float4 of weights (<= 4 a thread)
   static_assert(CH * PVJ / 4 == 4 * 256 && MAXMUL * CH / 4 <= 4 * 256, "the chunk's loads are four a thread");
-  float4 vreg[4], preg[4];
-  auto fetch = [&](int c0) {
-    // clamped addresses, unconditional loads (the values past count4 are never used)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = tid + u * 256;  // float4 i: position i / 2, columns 4 (i % 2)..
-      const int p = min(c0 + (i >> 1), count4 - 1);
-      vreg[u] = cache4<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + 4 * (i & 1));
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = tid + u * 256;  // float4 i of [head][position / 4]
-      const int hl = min(i / (CH / 4), mul - 1), p = min(c0 + 4 * (i % (CH / 4)), count4 - 4);
-      preg[u] = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
-    }
+  // a chunk's loads from clamped addresses, unconditional (the values past count4 are never used), written out four
+  // times over so that every register stays a register (an indexed array went to scratch memory)
+  auto vload = [&](int c0, int u) {
+    const int i = tid + u * 256;
+    const int p = min(c0 + (i >> 1), count4 - 1);
+    return cache4<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + 4 * (i & 1));
   };
-  if (count4 > 0) fetch(0);
+  auto pload = [&](int c0, int u) {
+    const int i = tid + u * 256;
+    const int hl = min(i / (CH / 4), mul - 1), p = min(c0 + 4 * (i % (CH / 4)), count4 - 4);
+    return *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
+  };
+  float4 v0, v1, v2, v3, q0, q1, q2, q3;
+#define PV_FETCH(c0_)                                                                           \
+  do {                                                                                          \
+    v0 = vload((c0_), 0); v1 = vload((c0_), 1); v2 = vload((c0_), 2); v3 = vload((c0_), 3);     \
+    q0 = pload((c0_), 0); q1 = pload((c0_), 1); q2 = pload((c0_), 2); q3 = pload((c0_), 3);     \
+  } while (0)
+  if (count4 > 0) PV_FETCH(0);
   for (int c0 = 0; c0 < count4; c0 += CH) {
     const int nb = min(CH, count4 - c0) >> 2;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) reinterpret_cast<float4 *>(vs)[tid + u * 256] = vreg[u];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    reinterpret_cast<float4 *>(vs)[tid] = v0;
+    reinterpret_cast<float4 *>(vs)[tid + 256] = v1;
+    reinterpret_cast<float4 *>(vs)[tid + 512] = v2;
+    reinterpret_cast<float4 *>(vs)[tid + 768] = v3;
+    auto pstore = [&](int u, float4 v) {
       const int i = tid + u * 256;
-      if (i < mul * CH / 4) reinterpret_cast<float4 *>(ps + (i / (CH / 4)) * PS)[i % (CH / 4)] = preg[u];
-    }
+      if (i < mul * CH / 4) reinterpret_cast<float4 *>(ps + (i / (CH / 4)) * PS)[i % (CH / 4)] = v;
+    };
+    pstore(0, q0);
+    pstore(1, q1);
+    pstore(2, q2);
+    pstore(3, q3);
     __syncthreads();
-    if (c0 + CH < count4) fetch(c0 + CH);  // the next chunk's loads fly while this one is used
+    if (c0 + CH < count4) PV_FETCH(c0 + CH);  // the next chunk's loads fly while this one is used
     for (int i = tid; i < mul * PVJ * nb; i += 256) {
       // the column fastest, then the head, then the block: a wave reads few value rows and broadcasts the weights
       const int j = i % PVJ, hl = (i / PVJ) % mul, b = i / (PVJ * mul);
@@ -206,6 +213,7 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
     if (tid < chains) acc = lds_chain(bs + (hl_me * PVJ + j_me) * BS, nb, acc);
     __syncthreads();
   }
+#undef PV_FETCH
   if (tid < chains) {
     const int h = kh * mul + hl_me, j = j0 + j_me;
     for (int p = count4; p < count; ++p)

@@ -276,9 +276,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     }
   __syncthreads();
   if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
+  // fully unrolled (no early exit), so that wr stays in registers
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
-    if (u >= steps) break;
+    if (u < steps) {
     const int g = u * 32 + (lane >> 1);
     const int gc = min(g, G - 1);
     const uint4 x4 = reinterpret_cast<const uint4 *>(xl)[(gc * 32 + half) / 16];
@@ -296,6 +297,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
         if (g < G4) pi[(g & 3) * lay.q + (g >> 2)] = p;
         else pi[4 * lay.q + (g - G4)] = p;
       }
+    }
     }
   }
   wave_sync_lds();
