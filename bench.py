@@ -27,6 +27,15 @@ from paths import package  # noqa: E402
 
 METRIC = "decode tok/s + GEMV HBM GB/s (8B-shape int8, batch 1); prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+PROFILED_STEPS = 8
+# HBM bytes of one pass of the decode matmuls (every layer's, and the classifier's), from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE runs of this script, each counter scaled by what it reads on HIP's device-to-device copy of 1 GiB
+# (FETCH_SIZE read half the bytes copied: x2; WRITE_SIZE all of them: x1). The profile summary names the commands.
+TRAFFIC = {
+    "llama3-8b": {"bytes_per_pass": (2 * (32 * (13900 + 9308 + 64588 + 32447) + 288653)
+                                     + (32 * (24 + 16 + 112 + 32) + 501)) * 1024,
+                  "source": "profiles/decode_gemv_llama3-8b.md"},
+}
 
 MODELS = {
     # Llama-3-8B shape (hidden 4096, 32 layers, 32 q / 8 kv heads of 128, SwiGLU 14336, vocab 128256, theta 5e5):
@@ -52,6 +61,25 @@ def hip_sync():
     code = lib.hipDeviceSynchronize()
     if code != 0:
         raise RuntimeError(f"hipDeviceSynchronize failed ({code})")
+
+
+def copy_calibration(nbytes=1 << 30, reps=4):
+    """a plain device-to-device copy of known size (HIP's own copy kernel), for scaling the FETCH_SIZE / WRITE_SIZE
+    counters of a profiled run to bytes: each copy reads and writes nbytes"""
+    lib = ctypes.CDLL("libamdhip64.so")
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    for buf in (src, dst):
+        if lib.hipMalloc(ctypes.byref(buf), ctypes.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    if lib.hipMemset(src, 1, ctypes.c_size_t(nbytes)) != 0:
+        raise RuntimeError("hipMemset failed")
+    for _ in range(reps):
+        if lib.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), 3) != 0:  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+    hip_sync()
+    for buf in (src, dst):
+        lib.hipFree(buf)
+    print(json.dumps({"copy_bytes": nbytes, "copies": reps}))
 
 
 def cpu_baseline(pk, spec, seconds=20.0):
@@ -100,7 +128,12 @@ def main():
     ap.add_argument("--model", default="llama3-8b", choices=sorted(MODELS))
     ap.add_argument("--prompt", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true", help="skip the oracle's CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 4 device copies of 1 GiB (the reference kernel for scaling HBM counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: every box here has one, and this engine has no multi-GPU path "
               f"(asked for --gpus {args.gpus})", file=sys.stderr)
@@ -110,7 +143,7 @@ def main():
     prompt_len = args.prompt if args.prompt is not None else spec["prompt"]
     pk = package()
     cfg = pk.config(**spec["cfg"])
-    if prompt_len + args.warmup + steps > cfg.seq_len:
+    if prompt_len + args.warmup + steps + PROFILED_STEPS > cfg.seq_len:
         raise SystemExit("the prompt and the steps do not fit the context")
     tensors, size = pk.places(cfg)
     cos, sin = pk.rope_tables(cfg.seq_len, cfg.head_size, spec["theta"])
@@ -146,11 +179,26 @@ def main():
     decode_s = time.perf_counter() - t0
     tok_s = steps / decode_s
 
-    # one decode step timed kernel by kind (HIP events on the engine's stream), at the position the run reached
-    prof = eng.profile(token, pos, True)
-    gemv_ms, gemv_bytes, gemv_launches = prof["gemv"]
-    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    # decode steps timed kernel by kind (a HIP event pair around every launch on the engine's stream), at the
+    # positions the run reached: the GEMV's achieved GB/s is the algorithmic bytes of its launches over their time
+    prof = {}
+    for i in range(PROFILED_STEPS):
+        for kind, (ms, nbytes, launches) in eng.profile(token, pos + i, True).items():
+            acc = prof.setdefault(kind, [0.0, 0.0, 0])
+            acc[0] += ms / PROFILED_STEPS
+            acc[1] += nbytes / PROFILED_STEPS
+            acc[2] += launches / PROFILED_STEPS
     step_ms = sum(v[0] for v in prof.values())
+    # the roofline's kernel: every decode matmul of a step (m = 1, the engine's weights, every layer, the classifier)
+    # back to back between one HIP event pair on the engine's stream, 4 passes; then each kind of matrix alone
+    gemv_ms, gemv_bytes, gemv_launches = eng.profile_matmul("all", rounds=4)
+    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    by_matrix = {}
+    for which in ("qkv", "wo", "w13", "w2", "classifier"):
+        ms, nbytes, launches = eng.profile_matmul(which, rounds=2)
+        by_matrix[which] = {"us_per_launch": round(1e3 * ms / launches, 2), "bytes_per_launch": round(nbytes / launches),
+                            "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    traffic = TRAFFIC.get(args.model)
     eng.release()
 
     cpu = None if args.no_cpu else cpu_baseline(pk, spec)
@@ -174,9 +222,14 @@ def main():
         "prefill_tok_s": round(prompt_len / prefill_s, 2),
         "gemv_hbm_gb_s": round(gemv_gbs, 1),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel (decode matmuls, one profiled step)",
-                     "launches": gemv_launches, "bytes_per_step": gemv_bytes, "ms_per_step": round(gemv_ms, 4)},
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": round(traffic["bytes_per_pass"] / gemv_launches) if traffic else None,
+                     "kernel": "decode GEMV (gemv1_kernel: every matmul of a decode step, m = 1, back to back)",
+                     "launches_per_pass": int(gemv_launches),
+                     "algorithmic_bytes_per_launch": round(gemv_bytes / gemv_launches),
+                     "us_per_launch": round(1e3 * gemv_ms / gemv_launches, 3),
+                     "traffic_source": traffic["source"] if traffic else None},
+        "gemv_by_matrix": by_matrix,
         "profile_ms": {k: round(v[0], 4) for k, v in prof.items()},
         "profiled_step_ms": round(step_ms, 4),
         "setup_s": round(setup_s, 2),

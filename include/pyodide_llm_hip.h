@@ -151,6 +151,15 @@ enum {
 int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, double *ms, double *bytes,
                            int32_t *launches);
 
+/* The decode matmuls (one token, m = 1) of the engine's own weights timed on their own, the counterpart of the
+ * reference's matmul timing over its weights (tests/q8r-bench.mjs:115-135): `which` -1 runs every matmul of a decode
+ * step in the step's order (q/k/v, wo, w1/w3, w2 of each layer, then the classifier), 0..4 only q/k/v, wo, w1/w3, w2
+ * or the classifier of every layer. The sequence runs `rounds` times back to back on the engine's stream between one
+ * HIP event pair, on the engine's current activations, its outputs into scratch rows (the cache, activations and
+ * logits are not touched). *ms: the mean duration of one pass; *bytes: the algorithmic bytes of one pass (weights,
+ * scales, activations, outputs); *launches: the launches of one pass. */
+int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *ms, double *bytes, int32_t *launches);
+
 /* ---- kernel level: device pointers, for the standalone matmul and the parity tests ---- */
 
 /* quantize_x (kernels/kernel.ts:129-156) of m rows of n float32 (row stride n): int8 rows (stride n) and float32

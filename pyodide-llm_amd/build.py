@@ -57,7 +57,7 @@ def build_addon():
         return None
     tmp = ADDON + ".tmp"
     run(["gcc", "-O2", "-std=c11", "-fPIC", "-shared", "-Wall", "-I", NODE_INCLUDE, "-I", os.path.join(HERE, ".."),
-         "-DNAPI_VERSION=8", "-o", tmp, src, "-L", HERE, "-lpyodide_llm_hip", "-Wl,-rpath,$ORIGIN",
+         "-DNAPI_VERSION=8", "-DNODE_GYP_MODULE_NAME=hip_engine", "-o", tmp, src, "-L", HERE, "-lpyodide_llm_hip", "-Wl,-rpath,$ORIGIN",
          "-Wl,--unresolved-symbols=ignore-in-object-files"])
     os.replace(tmp, ADDON)
     return ADDON

@@ -601,6 +601,65 @@ int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t nee
   return HE_OK;
 }
 
+int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *ms, double *bytes, int32_t *launches) {
+  if (!e || !ms || !bytes || !launches) return fail(HE_E_ARG, "a required pointer is null");
+  if (which < -1 || which > 4 || rounds < 1) return fail(HE_E_ARG, "he_profile_matmul: which in -1..4, rounds >= 1");
+  const he_config &c = e->c;
+  const int32_t dim = c.dim, hidden = c.hidden_dim, qdim = e->qdim, kvdim = e->kvdim;
+  // the outputs go to scratch rows (the engine's activations, cache and logits are not touched)
+  const int64_t out_floats = std::max<int64_t>({(int64_t)c.vocab_size, 2LL * hidden, (int64_t)qdim + 2LL * kvdim,
+                                                (int64_t)dim});
+  float *out = nullptr;
+  if (dev_alloc(&out, sizeof(float) * out_floats)) return HE_E_HIP;
+  struct Launch {
+    MatSeg seg[3];
+    int nseg;
+    int32_t k;
+  };
+  std::vector<Launch> seq;
+  for (int32_t l = 0; l < c.n_layers; ++l) {
+    if (which == -1 || which == 0)
+      seq.push_back({{{e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), out, qdim, qdim, 0},
+                      {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), out + qdim, kvdim, kvdim, 0},
+                      {e->mat(HE_T_WV, l), e->mat_scales(HE_T_WV, l), out + qdim + kvdim, kvdim, kvdim, 0}},
+                     3, dim});
+    if (which == -1 || which == 1)
+      seq.push_back({{{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), out, dim, dim, 1}}, 1, qdim});
+    if (which == -1 || which == 2)
+      seq.push_back({{{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), out, hidden, hidden, 0},
+                      {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), out + hidden, hidden, hidden, 0}},
+                     2, dim});
+    if (which == -1 || which == 3)
+      seq.push_back({{{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), out, dim, dim, 1}}, 1, hidden});
+  }
+  if (which == -1 || which == 4)
+    seq.push_back({{{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), out, c.vocab_size, 0, 0}}, 1, dim});
+  double pass_bytes = 0;
+  for (const Launch &l : seq) pass_bytes += matmul_bytes(e, l.seg, l.nseg, l.k, 1);
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t err = hipEventCreate(&a);
+  if (err == hipSuccess) err = hipEventCreate(&b);
+  if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+  if (err == hipSuccess) err = hipEventRecord(a, e->stream);
+  for (int32_t r = 0; r < rounds && err == hipSuccess; ++r)
+    for (const Launch &l : seq) {
+      err = matmul_launch(e, l.seg, l.nseg, l.k, 1, e->xq, e->xs);
+      if (err != hipSuccess) break;
+    }
+  if (err == hipSuccess) err = hipEventRecord(b, e->stream);
+  if (err == hipSuccess) err = hipEventSynchronize(b);
+  float t = 0;
+  if (err == hipSuccess) err = hipEventElapsedTime(&t, a, b);
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  (void)hipFree(out);
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("he_profile_matmul: ") + hipGetErrorString(err));
+  *ms = (double)t / rounds;
+  *bytes = pass_bytes;
+  *launches = (int32_t)seq.size();
+  return HE_OK;
+}
+
 int32_t he_logits(he_engine *e, float *out) {
   if (!e || !out) return fail(HE_E_ARG, "a required pointer is null");
   if (!e->have_logits) return fail(HE_E_STATE, "no step with logits has run");

@@ -82,6 +82,7 @@ def library():
             "he_device_bytes": (U64, [P]),
             "he_close": (I32, [P]),
             "he_profile_forward": (I32, [P, I32, I32, I32, P, P, P]),
+            "he_profile_matmul": (I32, [P, I32, I32, P, P, P]),
             "hk_quantize_x": (I32, [P, P, P, I32, I32, I32, P]),
             "hk_matmul": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, P]),
             "hk_group_sums": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, P]),
@@ -107,9 +108,10 @@ def _ptr(a):
     return ctypes.c_void_p(a.ctypes.data) if a is not None else None
 
 
-def plan_to_config(plan):
+def plan_to_config(plan, half_keys=None):
     """he_config and he_tensor[] from a plan dict (public/llama2_numpy.py:1261-1270); forms the engine does not take
-    are refused by name, as public/forward.js refuses what its kernels cannot run"""
+    are refused by name, as public/forward.js refuses what its kernels cannot run. Keys and values are float16 where
+    the plan allows it and every head has its own (or half_keys says so): public/forward.js:762"""
     if plan.get("arch", "llama") != "llama":
         raise HipError(f"the engine runs the Llama/Qwen2 form, not {plan['arch']}")
     if plan.get("parallel_residual"):
@@ -132,7 +134,9 @@ def plan_to_config(plan):
                n_kv_heads=plan["n_kv_heads"], head_size=plan["head_size"], vocab_size=plan["vocab_size"],
                seq_len=plan["seq_len"], shared_classifier=int(bool(plan["shared_classifier"])), six=int(six),
                qkv_bias=int("bq" in tensors), relaxed=int(bool(plan.get("relaxed", True))),
-               half_kv=int(bool(plan.get("half_kv", False))), rms_norm_eps=float(plan.get("rms_norm_eps", 1e-5)))
+               half_kv=int(bool(plan.get("half_kv", False)) and (
+                   bool(half_keys) if half_keys is not None else plan["n_kv_heads"] >= plan["n_heads"])),
+               rms_norm_eps=float(plan.get("rms_norm_eps", 1e-5)))
     t = TensorArray()
     for name, i in T.items():
         if name == "wcls" and c.shared_classifier:
@@ -223,6 +227,16 @@ class Engine:
         check(library().he_profile_forward(self._h, int(token), int(pos), int(bool(need_logits)), _ptr(ms),
                                            _ptr(nbytes), _ptr(launches)))
         return {k: (float(ms[i]), float(nbytes[i]), int(launches[i])) for i, k in enumerate(KINDS)}
+
+    MATMULS = {"all": -1, "qkv": 0, "wo": 1, "w13": 2, "w2": 3, "classifier": 4}
+
+    def profile_matmul(self, which="all", rounds=4):
+        """the decode matmuls of `which` (every layer) timed back to back: (ms a pass, algorithmic bytes a pass,
+        launches a pass)"""
+        ms, nbytes, launches = ctypes.c_double(), ctypes.c_double(), ctypes.c_int32()
+        check(library().he_profile_matmul(self._h, self.MATMULS[which], int(rounds), ctypes.byref(ms),
+                                          ctypes.byref(nbytes), ctypes.byref(launches)))
+        return ms.value, nbytes.value, launches.value
 
     def memoryBytes(self):
         return int(library().he_device_bytes(self._h))

@@ -42,7 +42,10 @@ def test_plan_conversion_takes_the_reference_plan_and_refuses_other_forms():
             "kv_start": 256, "rms_norm_eps": 1e-5, "shared_classifier": True, "int8": True, "relaxed": True,
             "tensors": tensors, "derived": {}, "outliers": [], "half_kv": True, "form": {}}
     cfg, t = pk.plan_to_config(plan)
-    assert (cfg.dim, cfg.n_kv_heads, cfg.relaxed, cfg.half_kv, cfg.six, cfg.qkv_bias) == (64, 2, 1, 1, 0, 0)
+    # a grouped-query model keeps float32 keys and values unless told otherwise (public/forward.js:762)
+    assert (cfg.dim, cfg.n_kv_heads, cfg.relaxed, cfg.half_kv, cfg.six, cfg.qkv_bias) == (64, 2, 1, 0, 0, 0)
+    assert pk.plan_to_config(plan, half_keys=True)[0].half_kv == 1
+    assert pk.plan_to_config({**plan, "n_kv_heads": 4})[0].half_kv == 1
     assert t[pk.T["wcls"]].offset == tensors["token_embedding_table"]["offset"]
     for change in ({"arch": "gpt2"}, {"outliers": [3]}, {"int8": False}, {"parallel_residual": True}):
         with pytest.raises(pk.HipError):
