@@ -74,7 +74,10 @@ function floats(bytes, count, name) {
   const u8 = b instanceof Uint8Array ? b : ArrayBuffer.isView(b) ? new Uint8Array(b.buffer, b.byteOffset, b.byteLength)
     : new Uint8Array(b);
   if (u8.byteLength < count * 4) throw new Error(`plan.derived.${name} holds ${u8.byteLength} bytes, not ${count * 4}`);
-  return new Float32Array(u8.slice(0, count * 4).buffer);
+  // a copy of its own (a Node Buffer's slice() shares a larger pooled ArrayBuffer at some offset)
+  const copy = new Uint8Array(count * 4);
+  copy.set(u8.subarray(0, count * 4));
+  return new Float32Array(copy.buffer);
 }
 
 /** The engine's config and tensor places from a plan (public/llama2_numpy.py:1261-1270). The forms the engine does not
