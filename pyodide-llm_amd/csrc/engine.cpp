@@ -109,7 +109,7 @@ struct he_engine {
   float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *hb2 = nullptr;
   int8_t *xq = nullptr;
   float *xs = nullptr;
-  float *scores = nullptr, *partial = nullptr, *tilemax = nullptr;
+  float *scores = nullptr, *tilemax = nullptr;
   float *logits = nullptr;
   int32_t *tokens = nullptr;
   float *amax_v = nullptr;
@@ -144,7 +144,7 @@ namespace {
 void destroy(he_engine *e) {
   if (!e) return;
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
-                  e->xq, e->xs, e->scores, e->partial, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
+                  e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
                   e->best_v, e->best_i};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
@@ -260,7 +260,6 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->xq, (size_t)T * e->widest);
   ALLOC(e->xs, sizeof(float) * T * (e->widest / 32));
   ALLOC(e->scores, sizeof(float) * T * c.n_heads * (size_t)c.seq_len);
-  ALLOC(e->partial, sizeof(float) * T * c.n_heads * (size_t)(c.seq_len / 4 + 4) * c.head_size);
   ALLOC(e->tilemax, sizeof(float) * T * c.n_heads * (size_t)(c.seq_len / 64 + 1));
   ALLOC(e->logits, sizeof(float) * c.vocab_size);
   ALLOC(e->tokens, sizeof(int32_t) * T);
@@ -284,7 +283,8 @@ int32_t open_common(const he_config *cfg, const he_tensor *tensors, uint64_t siz
   std::memcpy(e->t, tensors, sizeof(e->t));
   e->size = size;
   e->max_block = max_block;
-  e->chunk = std::min(max_block, 16);
+  // the tokens of one pass through the layers: a whole prompt block up to 512 (the prefill GEMM's token tiles are 128)
+  e->chunk = std::min(max_block, e->c.relaxed ? 512 : 16);
   HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
   if ((rc = plan_regions(e))) return rc;
   if ((rc = dev_alloc(&e->blob, e->blob_bytes))) return rc;
@@ -348,7 +348,32 @@ hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, 
   return hipSuccess;
 }
 
+// more tokens than one GEMV launch takes go to the MFMA GEMM (the same bits per token and row)
+bool use_gemm(const he_engine *e, int32_t k, int32_t m) {
+  return m > GEMV_MOST && gemm_supported(k, e->c.relaxed != 0);
+}
+
+hipError_t gemm_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
+                       const float *xs) {
+  MatArgs a{};
+  a.nseg = nseg;
+  for (int i = 0; i < nseg; ++i) {
+    a.seg[i] = segs[i];
+    a.total_rows += segs[i].rows;
+  }
+  a.xq = xq;
+  a.xs = xs;
+  a.xq_stride = e->widest;
+  a.xs_stride = e->widest / 32;
+  a.k = k;
+  a.m = m;
+  return launch_gemm(a, e->c.six, e->c.relaxed, e->stream);
+}
+
 hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs) {
+  if (use_gemm(e, k, m))
+    return timed(e, HE_K_GEMM, matmul_bytes(e, segs, nseg, k, m),
+                 [&] { return gemm_launch(e, segs, nseg, k, m, xq, xs); });
   return timed(e, HE_K_GEMV, matmul_bytes(e, segs, nseg, k, m),
                [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs); });
 }
@@ -403,7 +428,6 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.out = e->xb;
     at.out_stride = e->xw;
     at.scores = e->scores;
-    at.partial = e->partial;
     at.tilemax = e->tilemax;
     at.nh = c.n_heads;
     at.nkv = c.n_kv_heads;
@@ -763,6 +787,11 @@ int32_t hk_matmul(void *y, const void *xq, const void *xs, const void *w, const 
   if (rc) return rc;
   if (!y || !xs || !ws) return fail(HE_E_ARG, "matmul: a required pointer is null");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (m > GEMV_MOST && gemm_supported(k, bias == 64)) {
+    base.m = m;
+    HIP_TRY(launch_gemm(base, six != 0, bias == 64, s));
+    return HE_OK;
+  }
   const int32_t step = gemv_tokens(k, bias == 64);
   if (step < 1) return fail(HE_E_ARG, "matmul: rows too long for the GEMV");
   for (int32_t t0 = 0; t0 < m; t0 += step) {
@@ -783,6 +812,13 @@ int32_t hk_group_sums(void *s, const void *xq, const void *w, int32_t m, int32_t
   if (rc) return rc;
   if (!s) return fail(HE_E_ARG, "sums is null");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (gemm) {
+    if (!gemm_supported(k, bias == 64)) return fail(HE_E_ARG, "the MFMA GEMM takes bias 64 only");
+    base.m = m;
+    base.sums = reinterpret_cast<int32_t *>(s);
+    HIP_TRY(launch_gemm(base, six != 0, true, st));
+    return HE_OK;
+  }
   const int64_t per_token = (int64_t)rows * (k / 32) * (bias ? 1 : 4);
   for (int32_t t0 = 0; t0 < m; t0 += 8) {
     MatArgs a = base;
@@ -791,7 +827,6 @@ int32_t hk_group_sums(void *s, const void *xq, const void *w, int32_t m, int32_t
     a.sums = reinterpret_cast<int32_t *>(s) + t0 * per_token;
     HIP_TRY(launch_gemv(a, six != 0, bias == 64, st));
   }
-  (void)gemm;
   return HE_OK;
 }
 

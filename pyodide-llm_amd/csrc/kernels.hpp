@@ -32,13 +32,17 @@ struct MatArgs {
   int32_t *sums;  // group-sum output (hk_group_sums) or null
 };
 
+// the most tokens the engine gives one GEMV pass: more go to the MFMA GEMM where it takes them
+constexpr int32_t GEMV_MOST = 8;
+
 // decode GEMV, m <= 8 tokens: exact int32 group sums, the reference's float32 order
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
 // the most tokens one launch_gemv takes for rows of k (its products of a row fit the block's LDS)
 int32_t gemv_tokens(int32_t k, bool relaxed);
-// prefill GEMM on i8 MFMA, any m: the same bits as launch_gemv per (token, row)
+// prefill GEMM on i8 MFMA, any m (bias 64, int8 or int6): the same bits as launch_gemv per (token, row); with
+// a.sums (one segment) the exact int32 group sums [m][rows][K/32] instead
 hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
-bool gemm_supported(int32_t k, bool six);
+bool gemm_supported(int32_t k, bool relaxed);
 
 // quantize_x over m rows of n (x_stride apart) into xq (xq_stride) / xs (xs_stride)
 hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n, int32_t x_stride,
@@ -75,7 +79,6 @@ struct AttnArgs {
   float *out;
   int32_t out_stride;
   float *scores;  // [m][nh][seq_len]
-  float *partial; // [m][nh][seq_len / 4 + 4][hs] weighted-value blocks
   float *tilemax; // [m][nh][seq_len / 64 + 1]
   int32_t nh, nkv, hs, pos0, m, seq_len, half;
 };

@@ -56,6 +56,32 @@ def test_gemv_bits(k, rows, m, bias, six):
     assert np.array_equal(sums, ol.group_sums(xq, w, rows, k, bias, six))
 
 
+GEMM_CASES = [(k, rows, m) for k in (32, 96, 288, 1056, 4096) for rows, m in ((37, 9), (64, 130), (130, 200))]
+
+
+@pytest.mark.parametrize("six", [0, 1])
+@pytest.mark.parametrize("k,rows,m", GEMM_CASES)
+def test_gemm_bits(k, rows, m, six):
+    """more than 8 tokens: the MFMA GEMM, every output to the bit and every int32 group sum exact, ragged rows and
+    tokens, K with and without tail groups (G % 4 != 0)"""
+    w, ws = weights(rows, k, six)
+    xq, xs = activations(m, k, 64)
+    want = ol.matmul(xq, xs, w, ws, rows, k, 64, six)
+    got = gl.matmul(xq, xs, w, ws, rows, k, 64, six)
+    assert same_bits(got, want)
+    sums = gl.group_sums(xq, w, rows, k, 64, six, gemm=1)
+    assert np.array_equal(sums, ol.group_sums(xq, w, rows, k, 64, six))
+
+
+@pytest.mark.parametrize("six", [0, 1])
+def test_plain_order_with_many_tokens(six):
+    """bias 0 (matmul_q8's lanes) with more than 8 tokens stays on the GEMV, in passes of 8"""
+    k, rows, m = 288, 40, 20
+    w, ws = weights(rows, k, six)
+    xq, xs = activations(m, k, 0)
+    assert same_bits(gl.matmul(xq, xs, w, ws, rows, k, 0, six), ol.matmul(xq, xs, w, ws, rows, k, 0, six))
+
+
 @pytest.mark.parametrize("n", [4096, 14336])
 @pytest.mark.parametrize("m", [1, 4, 16, 512])
 def test_standalone_matmul_full_size(n, m):
@@ -69,11 +95,14 @@ def test_standalone_matmul_full_size(n, m):
     assert same_bits(got, want)
     if m <= 16:
         assert np.array_equal(gl.group_sums(xq, w, n, k, 64, 0), ol.group_sums(xq, w, n, k, 64, 0))
+    if m > 8 and n == 4096:
+        assert np.array_equal(gl.group_sums(xq, w, n, k, 64, 0, gemm=1), ol.group_sums(xq, w, n, k, 64, 0))
 
 
-def test_extremes_of_int8_equal_float64():
+@pytest.mark.parametrize("reps", [1, 3])
+def test_extremes_of_int8_equal_float64(reps):
     """tests/forward-check.mjs:244-276 on the device: rows of -128 and 127 against activations 127 and 1, scales
-    powers of two: the float32 result is the exact float64 sum"""
+    powers of two: the float32 result is the exact float64 sum (4 tokens on the GEMV, 12 on the GEMM)"""
     rows, groups = 8, 5
     n = groups * 32
     rng = np.random.default_rng(3)
@@ -82,7 +111,8 @@ def test_extremes_of_int8_equal_float64():
     w[2, ::2], w[2, 1::2] = -128, 127
     xq = np.stack([np.full(n, 127), np.ones(n), np.where(np.arange(n) & 1, 1, 127), rng.integers(1, 128, n)]).astype(np.int8)
     xs = np.stack([np.full(groups, 2.0 ** -(2 + t)) for t in range(4)]).astype(np.float32)
+    xq, xs = np.tile(xq, (reps, 1)), np.tile(xs, (reps, 1))
     ws = np.full((rows, groups), 2.0 ** -7, dtype=np.float32)
     got = gl.matmul(xq, xs, w, ws, rows, n, 64, 0)
-    want = (w.astype(np.float64)[None] * (xq.astype(np.float64)[:, None] - 64)).sum(-1) * 2.0 ** -7 * xs[:, :1]
+    want = (w.astype(np.float64)[None] * (xq.astype(np.float64)[:, None] - 64)).sum(-1) * 2.0 ** -7 * xs[:, :1].astype(np.float64)
     assert np.array_equal(got.astype(np.float64), want)
