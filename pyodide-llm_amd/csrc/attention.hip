@@ -24,6 +24,7 @@ constexpr int TILE = 64;   // positions a block of (A)
 constexpr int MAXMUL = 8;  // query heads a kv head at most
 constexpr int PVJ = 8;     // columns a block of (C)
 constexpr int CH = 512;    // positions a chunk of (C)
+constexpr int FUSED_TOKENS = 8;  // up to this many tokens the softmax and the values run fused (below)
 
 template <bool HALF>
 __device__ __forceinline__ float4 cache4(const void *c, int64_t i) {  // four values from element i (i % 4 == 0)
@@ -222,10 +223,133 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
   }
 }
 
+// (B+C) for a few tokens (decode): one block of 512 threads a (token, kv head, 8 of the head's columns), the softmax
+// of the nh / nkv query heads and their weighted values in one launch. Wave 0 runs the ordered sums; waves 1-7
+// produce what they add, one 480-position chunk ahead, in double-buffered LDS:
+//   phase 1: the exponentials of a chunk (every head, laid out by lane k = position % 4), then the four ordered sums
+//            of every head advance over it; the tail and 1 / sum at the end;
+//   phase 2: the exponentials again (the same bits), the weights p = e * inv, the four-position products
+//            ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) of a chunk of values, then the ordered sum of every (head, column)
+//            advances over it; the positions past the fours at the end.
+// Each block of a (token, kv head) computes the same sums: redundant arithmetic, but no launch and no global round
+// trip between the softmax and the values.
+constexpr int FCH = 480;           // positions a chunk (the double buffer within 64 KB of LDS)
+constexpr int FNB = FCH / 4;       // four-position blocks a chunk
+constexpr int FRS = FNB + 4;       // LDS row of a chain (padded)
+constexpr int FPROD = 448;         // producer threads (waves 1-7)
+
+template <int HS, bool HALF>
+__global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
+  __shared__ float buf[2][MAXMUL * PVJ * FRS];  // phase 1: [head][lane][q]; phase 2: [head][column][block]
+  __shared__ float mxs[MAXMUL], invs[MAXMUL];
+  const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const int count = a.pos0 + t + 1, count4 = count & ~3;
+  const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
+  const int tiles = (count + TILE - 1) / TILE;
+  const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
+  const int chunks = (count4 + FCH - 1) / FCH;
+  const bool producer = tid >= 64;
+  const int ptid = tid - 64;
+
+  // the largest score of each head, from the tile maxima of the scores kernel (wave 0, a head at a time)
+  if (tid < 64) {
+    for (int hl = 0; hl < mul; ++hl) {
+      const float *tm = a.tilemax + ((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1);
+      float mx = -3.4028234663852886e38f;
+      for (int i = tid; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+      for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+      if (tid == 0) mxs[hl] = mx;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 1: the sums ----
+  // producer item i of a chunk: head i / FNB, four positions 4 * (i % FNB) (clamped loads; what lies past count4 is
+  // computed but never added)
+  auto exps = [&](int c, float *dst) {
+    for (int i = ptid; i < mul * FNB; i += FPROD) {
+      const int hl = i / FNB, q = i % FNB;
+      const int p = min(c * FCH + 4 * q, count4 - 4);
+      const float4 sv = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
+      const float mx = mxs[hl];
+      float *row = dst + hl * 4 * FRS + q;
+      row[0] = vexp(sv.x - mx);
+      row[FRS] = vexp(sv.y - mx);
+      row[2 * FRS] = vexp(sv.z - mx);
+      row[3 * FRS] = vexp(sv.w - mx);
+    }
+  };
+  float acc = 0.0f;  // wave 0, lane hl * 4 + k: the sum of lane k of head hl; then (phase 2) lane hl * 8 + j
+  for (int c = 0; c <= chunks; ++c) {
+    if (producer && c < chunks) exps(c, buf[c & 1]);
+    if (!producer && c > 0 && tid < mul * 4) {
+      const int nq = min(FCH, count4 - (c - 1) * FCH) >> 2;
+      acc = lds_chain(buf[(c - 1) & 1] + (tid >> 2) * 4 * FRS + (tid & 3) * FRS, nq, acc);
+    }
+    __syncthreads();
+  }
+  // ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
+  if (tid < 64) {
+    const float l1 = __shfl_down(acc, 1, 64), l2 = __shfl_down(acc, 2, 64), l3 = __shfl_down(acc, 3, 64);
+    if (tid < mul * 4 && (tid & 3) == 0) {
+      const int hl = tid >> 2;
+      float sum = ((acc + l1) + l2) + l3;
+      for (int i = count4; i < count; ++i) sum = sum + fexp(scores[(int64_t)hl * a.seq_len + i] - mxs[hl]);
+      invs[hl] = 1.0f / sum;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: the weighted values ----
+  // producer item i of a chunk: block b = i / 2 (positions 4b..4b+3), columns j0 + 4 * (i % 2) .. +3, every head
+  auto products = [&](int c, float *dst) {
+    for (int i = ptid; i < FNB * 2; i += FPROD) {
+      const int b = i >> 1, jq = i & 1;
+      const int p = min(c * FCH + 4 * b, count4 - 4);
+      const int64_t at = (int64_t)p * kvdim + kh * HS + j0 + 4 * jq;
+      const float4 v0 = cache4<HALF>(a.vcache, at), v1 = cache4<HALF>(a.vcache, at + kvdim);
+      const float4 v2 = cache4<HALF>(a.vcache, at + 2 * kvdim), v3 = cache4<HALF>(a.vcache, at + 3 * kvdim);
+      for (int hl = 0; hl < mul; ++hl) {
+        const float4 sv = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
+        const float mx = mxs[hl], inv = invs[hl];
+        const float p0 = vexp(sv.x - mx) * inv, p1 = vexp(sv.y - mx) * inv;
+        const float p2 = vexp(sv.z - mx) * inv, p3 = vexp(sv.w - mx) * inv;
+        float *row = dst + (hl * PVJ + 4 * jq) * FRS + b;
+        row[0] = (p0 * v0.x + p1 * v1.x) + (p2 * v2.x + p3 * v3.x);
+        row[FRS] = (p0 * v0.y + p1 * v1.y) + (p2 * v2.y + p3 * v3.y);
+        row[2 * FRS] = (p0 * v0.z + p1 * v1.z) + (p2 * v2.z + p3 * v3.z);
+        row[3 * FRS] = (p0 * v0.w + p1 * v1.w) + (p2 * v2.w + p3 * v3.w);
+      }
+    }
+  };
+  acc = 0.0f;
+  for (int c = 0; c <= chunks; ++c) {
+    if (producer && c < chunks) products(c, buf[c & 1]);
+    if (!producer && c > 0 && tid < mul * PVJ) {
+      const int nb = min(FCH, count4 - (c - 1) * FCH) >> 2;
+      acc = lds_chain(buf[(c - 1) & 1] + tid * FRS, nb, acc);
+    }
+    __syncthreads();
+  }
+  if (tid < mul * PVJ) {
+    const int hl = tid / PVJ, j = tid % PVJ;
+    const float mx = mxs[hl], inv = invs[hl];
+    for (int p = count4; p < count; ++p) {
+      const float pw = fexp(scores[(int64_t)hl * a.seq_len + p] - mx) * inv;
+      acc = acc + pw * cache1<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + j);
+    }
+    a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
+  }
+}
+
 template <int HS, bool HALF>
 hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
   hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
+  if (a.m <= FUSED_TOKENS) {
+    hipLaunchKernelGGL((softmax_pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
   const int most4 = (a.pos0 + a.m) & ~3;
   const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
