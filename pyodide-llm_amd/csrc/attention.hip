@@ -224,190 +224,152 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
 }
 
 // (B+C) for a few tokens (decode): one block of 512 threads a (token, kv head, 8 of the head's columns), the softmax
-// of the nh / nkv query heads and their weighted values in one launch. Wave 0 runs the ordered sums; waves 1-7
-// produce what they add one chunk of positions ahead, in double-buffered LDS, with the global loads of the chunk
-// after that in flight meanwhile:
-//   phase 1: the exponentials of a chunk (every head, laid out by lane k = position % 4), then the four ordered sums
-//            of every head advance over it; the tail and 1 / sum at the end;
-//   phase 2: the chunk's values and scores staged in LDS; the exponentials again (the same bits), the weights
-//            p = e * inv and the four-position products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)); then the ordered sum of
-//            every (head, column) advances over them; the positions past the fours at the end.
-// Each block of a (token, kv head) computes the same sums: redundant arithmetic, but no launch and no global round
-// trip between the softmax and the values.
-constexpr int FCH = 240;           // positions a chunk
-constexpr int FNB = FCH / 4;       // four-position blocks a chunk
-constexpr int FRS = FNB + 4;       // LDS row of a chain (padded, 16-byte aligned)
-constexpr int FPROD = 448;         // producer threads (waves 1-7)
-static_assert(MAXMUL * FNB <= 2 * FPROD && FCH * PVJ / 4 <= 2 * FPROD, "two items a producer thread");
+// of the nh / nkv query heads and their weighted values in one launch. Wave 0 runs the ordered sums; waves 1-7 each
+// produce every 7th chunk of what those sums add into a ring of LDS slots, as far ahead as the ring allows, with an
+// LDS flag a slot to say it is filled and a counter of the chunks wave 0 has used (no block-wide barrier a chunk, so
+// the producers' global loads overlap each other and the sums):
+//   phase 1 (chunks of 256 positions): the exponentials of every head, laid out by lane k = position % 4; wave 0's
+//            four ordered sums of every head advance over them; the tail and 1 / sum at the end;
+//   phase 2 (chunks of 128 positions): the exponentials again (the same bits), p = e * inv, and the four-position
+//            products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) of the block's 8 columns; wave 0's ordered sum of every
+//            (head, column) advances over them; the positions past the fours at the end.
+// Each of the hs / 8 blocks of a (token, kv head) computes the same softmax: redundant arithmetic, no launch and no
+// global round trip between the softmax and the values. Every wait is on another wave of the same block, for a chunk
+// of a lower index, so every wait ends.
+constexpr int P1 = 256, Q1 = P1 / 4, R1 = Q1 + 4;  // phase 1: positions, quads, LDS row (floats) of a chunk
+constexpr int P2 = 128, Q2 = P2 / 4, R2 = Q2 + 4;  // phase 2: positions, four-position blocks, LDS row of a chunk
+constexpr int NSLOT = 6;                           // ring slots
+constexpr int SLOT = MAXMUL * PVJ * R2;            // floats a slot (phase 1 takes MAXMUL * 4 * R1 <= SLOT)
+static_assert(MAXMUL * 4 * R1 <= SLOT, "a phase-1 chunk fits a slot");
+constexpr int NPROD = 7;                           // producer waves
 
-struct FusedLds {
-  float chain[2][MAXMUL * PVJ * FRS];  // phase 1: [head][lane][q]; phase 2: [head][column][block]
-  float v[2][FCH * PVJ];               // phase 2: the chunk's values [position][column]
-  float s[2][MAXMUL * FCH];            // phase 2: the chunk's scores [head][position]
-  float mx[MAXMUL], inv[MAXMUL];
-};
-
-// phase 1, producer item u of chunk c: head i / FNB, positions 4 * (i % FNB) .. +3 (clamped: what lies past count4 is
-// computed but never added)
-__device__ __forceinline__ float4 score4(const float *scores, int seq_len, int mul, int count4, int c, int i) {
-  const int hl = min(i / FNB, mul - 1), q = i % FNB;
-  const int p = min(c * FCH + 4 * q, count4 - 4);
-  return *reinterpret_cast<const float4 *>(scores + (int64_t)hl * seq_len + p);
-}
-
-template <bool HALF>
-__device__ __forceinline__ float4 value4(const void *vcache, int64_t base, int kvdim, int count4, int c, int i) {
-  const int p = min(c * FCH + (i >> 1), count4 - 1);  // i: position i / 2 of the chunk, columns 4 * (i % 2) .. +3
-  return cache4<HALF>(vcache, base + (int64_t)p * kvdim + 4 * (i & 1));
+__device__ __forceinline__ int lds_load(const int *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void lds_store(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+__device__ __forceinline__ void wait_at_least(const int *p, int v) {
+  while (lds_load(p) < v) __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 template <int HS, bool HALF>
 __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
-  __shared__ FusedLds L;
+  __shared__ float ring[NSLOT * SLOT];
+  __shared__ int filled[NSLOT], used[2];
+  __shared__ float mxs[MAXMUL], invs[MAXMUL];
   const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int count = a.pos0 + t + 1, count4 = count & ~3;
   const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
   const int tiles = (count + TILE - 1) / TILE;
   const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
   const int64_t vbase = (int64_t)kh * HS + j0;
-  const int chunks = (count4 + FCH - 1) / FCH;
-  const bool producer = tid >= 64;
-  const int i0 = tid - 64, i1 = tid - 64 + FPROD;  // a producer's two items
-  const bool has0 = producer && i0 < mul * FNB, has1 = producer && i1 < mul * FNB;
+  const int n1 = (count4 + P1 - 1) / P1, n2 = (count4 + P2 - 1) / P2;
 
-  // phase 1's first scores fly while the maxima are found
-  float4 s0 = make_float4(0, 0, 0, 0), s1 = s0;
-  if (chunks > 0 && producer) {
-    s0 = score4(scores, a.seq_len, mul, count4, 0, i0);
-    s1 = score4(scores, a.seq_len, mul, count4, 0, i1);
-  }
+  if (tid < NSLOT) filled[tid] = 0;
+  if (tid < 2) used[tid] = 0;
   // the largest score of each head, from the tile maxima of the scores kernel (wave 0, a head at a time)
-  if (tid < 64) {
+  if (wave == 0) {
     for (int hl = 0; hl < mul; ++hl) {
       const float *tm = a.tilemax + ((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1);
       float mx = -3.4028234663852886e38f;
-      for (int i = tid; i < tiles; i += 64) mx = wmax(mx, tm[i]);
+      for (int i = lane; i < tiles; i += 64) mx = wmax(mx, tm[i]);
       for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-      if (tid == 0) L.mx[hl] = mx;
+      if (lane == 0) mxs[hl] = mx;
     }
   }
   __syncthreads();
 
   // ---- phase 1: the sums ----
   float acc = 0.0f;  // wave 0, lane hl * 4 + k: the sum of lane k of head hl; then (phase 2) lane hl * 8 + j
-  for (int c = 0; c <= chunks; ++c) {
-    if (producer && c < chunks) {
-      float4 n0 = s0, n1 = s1;
-      if (c + 1 < chunks) {  // the next chunk's scores fly while this one is used
-        n0 = score4(scores, a.seq_len, mul, count4, c + 1, i0);
-        n1 = score4(scores, a.seq_len, mul, count4, c + 1, i1);
+  if (wave > 0) {
+    for (int c = wave - 1; c < n1; c += NPROD) {
+      wait_at_least(&used[0], c - NSLOT + 1);  // the slot's last chunk has been added
+      float *slot = ring + (c % NSLOT) * SLOT;
+      const int p = min(c * P1 + 4 * lane, count4 - 4);  // lane = the quad (clamped: never added past count4)
+      for (int hl = 0; hl < mul; ++hl) {
+        const float4 sv = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
+        const float mx = mxs[hl];
+        float *row = slot + hl * 4 * R1 + lane;
+        row[0] = vexp(sv.x - mx);
+        row[R1] = vexp(sv.y - mx);
+        row[2 * R1] = vexp(sv.z - mx);
+        row[3 * R1] = vexp(sv.w - mx);
       }
-      float *dst = L.chain[c & 1];
-      if (has0) {
-        const int hl = i0 / FNB, q = i0 % FNB;
-        const float mx = L.mx[hl];
-        float *row = dst + hl * 4 * FRS + q;
-        row[0] = vexp(s0.x - mx);
-        row[FRS] = vexp(s0.y - mx);
-        row[2 * FRS] = vexp(s0.z - mx);
-        row[3 * FRS] = vexp(s0.w - mx);
-      }
-      if (has1) {
-        const int hl = i1 / FNB, q = i1 % FNB;
-        const float mx = L.mx[hl];
-        float *row = dst + hl * 4 * FRS + q;
-        row[0] = vexp(s1.x - mx);
-        row[FRS] = vexp(s1.y - mx);
-        row[2 * FRS] = vexp(s1.z - mx);
-        row[3 * FRS] = vexp(s1.w - mx);
-      }
-      s0 = n0;
-      s1 = n1;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) lds_store(&filled[c % NSLOT], c + 1);
     }
-    if (!producer && c > 0 && tid < mul * 4) {
-      const int nq = min(FCH, count4 - (c - 1) * FCH) >> 2;
-      acc = lds_chain(L.chain[(c - 1) & 1] + (tid >> 2) * 4 * FRS + (tid & 3) * FRS, nq, acc);
+  } else {
+    for (int c = 0; c < n1; ++c) {
+      wait_at_least(&filled[c % NSLOT], c + 1);
+      if (lane < mul * 4) {
+        const int nq = min(P1, count4 - c * P1) >> 2;
+        acc = lds_chain(ring + (c % NSLOT) * SLOT + (lane >> 2) * 4 * R1 + (lane & 3) * R1, nq, acc);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) lds_store(&used[0], c + 1);
     }
-    __syncthreads();
-  }
-
-  // phase 2's first chunk: values and scores into LDS (producers) while wave 0 finishes the sums
-  const int vi0 = tid - 64, vi1 = tid - 64 + FPROD;  // value float4 items: FCH * PVJ / 4 of a chunk
-  const bool hv0 = producer && vi0 < FCH * PVJ / 4, hv1 = producer && vi1 < FCH * PVJ / 4;
-  float4 v0 = make_float4(0, 0, 0, 0), v1 = v0, q0 = v0, q1 = v0;
-  auto load2 = [&](int c) {
-    v0 = value4<HALF>(a.vcache, vbase, kvdim, count4, c, vi0);
-    v1 = value4<HALF>(a.vcache, vbase, kvdim, count4, c, vi1);
-    q0 = score4(scores, a.seq_len, mul, count4, c, i0);
-    q1 = score4(scores, a.seq_len, mul, count4, c, i1);
-  };
-  auto stage2 = [&](int buf) {
-    float4 *vd = reinterpret_cast<float4 *>(L.v[buf]);
-    if (hv0) vd[vi0] = v0;
-    if (hv1) vd[vi1] = v1;
-    if (has0) reinterpret_cast<float4 *>(L.s[buf] + (i0 / FNB) * FCH)[i0 % FNB] = q0;
-    if (has1) reinterpret_cast<float4 *>(L.s[buf] + (i1 / FNB) * FCH)[i1 % FNB] = q1;
-  };
-  if (chunks > 0 && producer) {
-    load2(0);
-    stage2(0);
-  }
-  // ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
-  if (tid < 64) {
+    // ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
     const float l1 = __shfl_down(acc, 1, 64), l2 = __shfl_down(acc, 2, 64), l3 = __shfl_down(acc, 3, 64);
-    if (tid < mul * 4 && (tid & 3) == 0) {
-      const int hl = tid >> 2;
+    if (lane < mul * 4 && (lane & 3) == 0) {
+      const int hl = lane >> 2;
       float sum = ((acc + l1) + l2) + l3;
-      for (int i = count4; i < count; ++i) sum = sum + fexp(scores[(int64_t)hl * a.seq_len + i] - L.mx[hl]);
-      L.inv[hl] = 1.0f / sum;
+      for (int i = count4; i < count; ++i) sum = sum + fexp(scores[(int64_t)hl * a.seq_len + i] - mxs[hl]);
+      invs[hl] = 1.0f / sum;
     }
   }
+  __syncthreads();
+  if (tid < NSLOT) filled[tid] = 0;
   __syncthreads();
 
   // ---- phase 2: the weighted values ----
   acc = 0.0f;
-  for (int c = 0; c <= chunks; ++c) {
-    if (producer && c < chunks) {
-      if (c + 1 < chunks) load2(c + 1);  // the next chunk's values and scores fly while this one is used
-      // item (block b, head hl): the products of its four positions for the block's 8 columns
-      const float *vs = L.v[c & 1], *ss = L.s[c & 1];
-      float *dst = L.chain[c & 1];
-      for (int i = i0; i < mul * FNB; i += FPROD) {
-        const int hl = i / FNB, b = i % FNB;
-        const float4 sv = *reinterpret_cast<const float4 *>(ss + hl * FCH + 4 * b);
-        const float mx = L.mx[hl], inv = L.inv[hl];
+  if (wave > 0) {
+    const int b = lane >> 1;  // the lane's four-position block; its heads lane % 2, lane % 2 + 2, ...
+    for (int c = wave - 1; c < n2; c += NPROD) {
+      wait_at_least(&used[1], c - NSLOT + 1);
+      float *slot = ring + (c % NSLOT) * SLOT;
+      const int p = min(c * P2 + 4 * b, count4 - 4);
+      const int64_t at = (int64_t)p * kvdim + vbase;
+      const float4 v0a = cache4<HALF>(a.vcache, at), v0b = cache4<HALF>(a.vcache, at + 4);
+      const float4 v1a = cache4<HALF>(a.vcache, at + kvdim), v1b = cache4<HALF>(a.vcache, at + kvdim + 4);
+      const float4 v2a = cache4<HALF>(a.vcache, at + 2 * kvdim), v2b = cache4<HALF>(a.vcache, at + 2 * kvdim + 4);
+      const float4 v3a = cache4<HALF>(a.vcache, at + 3 * kvdim), v3b = cache4<HALF>(a.vcache, at + 3 * kvdim + 4);
+      for (int hl = lane & 1; hl < mul; hl += 2) {
+        const float4 sv = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
+        const float mx = mxs[hl], inv = invs[hl];
         const float p0 = vexp(sv.x - mx) * inv, p1 = vexp(sv.y - mx) * inv;
         const float p2 = vexp(sv.z - mx) * inv, p3 = vexp(sv.w - mx) * inv;
-        const float *vr = vs + 4 * b * PVJ;
-        float *row = dst + hl * PVJ * FRS + b;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float4 a0 = *reinterpret_cast<const float4 *>(vr + 4 * h);
-          const float4 a1 = *reinterpret_cast<const float4 *>(vr + PVJ + 4 * h);
-          const float4 a2 = *reinterpret_cast<const float4 *>(vr + 2 * PVJ + 4 * h);
-          const float4 a3 = *reinterpret_cast<const float4 *>(vr + 3 * PVJ + 4 * h);
-          row[(4 * h + 0) * FRS] = (p0 * a0.x + p1 * a1.x) + (p2 * a2.x + p3 * a3.x);
-          row[(4 * h + 1) * FRS] = (p0 * a0.y + p1 * a1.y) + (p2 * a2.y + p3 * a3.y);
-          row[(4 * h + 2) * FRS] = (p0 * a0.z + p1 * a1.z) + (p2 * a2.z + p3 * a3.z);
-          row[(4 * h + 3) * FRS] = (p0 * a0.w + p1 * a1.w) + (p2 * a2.w + p3 * a3.w);
-        }
+        float *row = slot + hl * PVJ * R2 + b;
+        row[0 * R2] = (p0 * v0a.x + p1 * v1a.x) + (p2 * v2a.x + p3 * v3a.x);
+        row[1 * R2] = (p0 * v0a.y + p1 * v1a.y) + (p2 * v2a.y + p3 * v3a.y);
+        row[2 * R2] = (p0 * v0a.z + p1 * v1a.z) + (p2 * v2a.z + p3 * v3a.z);
+        row[3 * R2] = (p0 * v0a.w + p1 * v1a.w) + (p2 * v2a.w + p3 * v3a.w);
+        row[4 * R2] = (p0 * v0b.x + p1 * v1b.x) + (p2 * v2b.x + p3 * v3b.x);
+        row[5 * R2] = (p0 * v0b.y + p1 * v1b.y) + (p2 * v2b.y + p3 * v3b.y);
+        row[6 * R2] = (p0 * v0b.z + p1 * v1b.z) + (p2 * v2b.z + p3 * v3b.z);
+        row[7 * R2] = (p0 * v0b.w + p1 * v1b.w) + (p2 * v2b.w + p3 * v3b.w);
       }
-      if (c + 1 < chunks) stage2((c + 1) & 1);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) lds_store(&filled[c % NSLOT], c + 1);
     }
-    if (!producer && c > 0 && tid < mul * PVJ) {
-      const int nb = min(FCH, count4 - (c - 1) * FCH) >> 2;
-      acc = lds_chain(L.chain[(c - 1) & 1] + tid * FRS, nb, acc);
+  } else {
+    for (int c = 0; c < n2; ++c) {
+      wait_at_least(&filled[c % NSLOT], c + 1);
+      if (lane < mul * PVJ) {
+        const int nb = min(P2, count4 - c * P2) >> 2;
+        acc = lds_chain(ring + (c % NSLOT) * SLOT + lane * R2, nb, acc);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) lds_store(&used[1], c + 1);
     }
-    __syncthreads();
-  }
-  if (tid < mul * PVJ) {
-    const int hl = tid / PVJ, j = tid % PVJ;
-    const float mx = L.mx[hl], inv = L.inv[hl];
-    for (int p = count4; p < count; ++p) {
-      const float pw = fexp(scores[(int64_t)hl * a.seq_len + p] - mx) * inv;
-      acc = acc + pw * cache1<HALF>(a.vcache, (int64_t)p * kvdim + vbase + j);
+    if (lane < mul * PVJ) {
+      const int hl = lane / PVJ, j = lane % PVJ;
+      const float mx = mxs[hl], inv = invs[hl];
+      for (int p = count4; p < count; ++p) {
+        const float pw = fexp(scores[(int64_t)hl * a.seq_len + p] - mx) * inv;
+        acc = acc + pw * cache1<HALF>(a.vcache, (int64_t)p * kvdim + vbase + j);
+      }
+      a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
     }
-    a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
   }
 }
 
