@@ -255,6 +255,7 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
   __shared__ float ring[NSLOT * SLOT];
   __shared__ int filled[NSLOT], used[2];
   __shared__ float mxs[MAXMUL], invs[MAXMUL];
+  __shared__ float tail_s[MAXMUL][4], tail_v[4][PVJ];  // the positions past the fours (at most 3)
   const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int count = a.pos0 + t + 1, count4 = count & ~3;
@@ -263,17 +264,27 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
   const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
   const int64_t vbase = (int64_t)kh * HS + j0;
   const int n1 = (count4 + P1 - 1) / P1, n2 = (count4 + P2 - 1) / P2;
+  // a global load here takes about a microsecond: every wave requests what it needs next before it waits for any
 
   if (tid < NSLOT) filled[tid] = 0;
   if (tid < 2) used[tid] = 0;
-  // the largest score of each head, from the tile maxima of the scores kernel (wave 0, a head at a time)
-  if (wave == 0) {
-    for (int hl = 0; hl < mul; ++hl) {
-      const float *tm = a.tilemax + ((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1);
-      float mx = -3.4028234663852886e38f;
-      for (int i = lane; i < tiles; i += 64) mx = wmax(mx, tm[i]);
-      for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-      if (lane == 0) mxs[hl] = mx;
+  // wave w < mul: the largest score of head w from the tile maxima of the scores kernel (two loads a lane, together);
+  // wave 7: the positions past the fours, scores and values, into LDS
+  if (wave < mul) {
+    const float *tm = a.tilemax + ((int64_t)t * a.nh + kh * mul + wave) * (a.seq_len / TILE + 1);
+    const float m0 = tm[min(lane, tiles - 1)], m1 = tm[min(lane + 64, tiles - 1)];  // clamped: repeats are harmless
+    float mx = wmax(m0, m1);
+    for (int i = lane + 128; i < tiles; i += 64) mx = wmax(mx, tm[i]);  // contexts past 8192 positions
+    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) mxs[wave] = mx;
+  }
+  if (wave == 7) {
+    if (lane < MAXMUL * 4) {
+      const int hl = min(lane >> 2, mul - 1), r = lane & 3;
+      tail_s[lane >> 2][r] = scores[(int64_t)hl * a.seq_len + min(count4 + r, count - 1)];
+    } else if (lane < MAXMUL * 4 + 4 * PVJ) {
+      const int i = lane - MAXMUL * 4, r = i / PVJ, j = i % PVJ;
+      tail_v[r][j] = cache1<HALF>(a.vcache, (int64_t)min(count4 + r, count - 1) * kvdim + vbase + j);
     }
   }
   __syncthreads();
@@ -281,21 +292,35 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
   // ---- phase 1: the sums ----
   float acc = 0.0f;  // wave 0, lane hl * 4 + k: the sum of lane k of head hl; then (phase 2) lane hl * 8 + j
   if (wave > 0) {
-    for (int c = wave - 1; c < n1; c += NPROD) {
+    // lane = the quad of the chunk; the scores of every head requested at once, the wave's next chunk (7 on) too
+    float4 cur[MAXMUL], nxt[MAXMUL];
+    auto fetch1 = [&](int c, float4 *dst) {
+      const int p = min(c * P1 + 4 * lane, count4 - 4);  // clamped: never added past count4
+#pragma unroll
+      for (int hl = 0; hl < MAXMUL; ++hl)
+        dst[hl] = *reinterpret_cast<const float4 *>(scores + (int64_t)min(hl, mul - 1) * a.seq_len + p);
+    };
+    int c = wave - 1;
+    if (c < n1) fetch1(c, cur);
+    for (; c < n1; c += NPROD) {
+      if (c + NPROD < n1) fetch1(c + NPROD, nxt);
       wait_at_least(&used[0], c - NSLOT + 1);  // the slot's last chunk has been added
       float *slot = ring + (c % NSLOT) * SLOT;
-      const int p = min(c * P1 + 4 * lane, count4 - 4);  // lane = the quad (clamped: never added past count4)
-      for (int hl = 0; hl < mul; ++hl) {
-        const float4 sv = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
-        const float mx = mxs[hl];
-        float *row = slot + hl * 4 * R1 + lane;
-        row[0] = vexp(sv.x - mx);
-        row[R1] = vexp(sv.y - mx);
-        row[2 * R1] = vexp(sv.z - mx);
-        row[3 * R1] = vexp(sv.w - mx);
+#pragma unroll
+      for (int hl = 0; hl < MAXMUL; ++hl) {
+        if (hl < mul) {
+          const float mx = mxs[hl];
+          float *row = slot + hl * 4 * R1 + lane;
+          row[0] = vexp(cur[hl].x - mx);
+          row[R1] = vexp(cur[hl].y - mx);
+          row[2 * R1] = vexp(cur[hl].z - mx);
+          row[3 * R1] = vexp(cur[hl].w - mx);
+        }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) lds_store(&filled[c % NSLOT], c + 1);
+#pragma unroll
+      for (int hl = 0; hl < MAXMUL; ++hl) cur[hl] = nxt[hl];
     }
   } else {
     for (int c = 0; c < n1; ++c) {
@@ -312,7 +337,7 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
     if (lane < mul * 4 && (lane & 3) == 0) {
       const int hl = lane >> 2;
       float sum = ((acc + l1) + l2) + l3;
-      for (int i = count4; i < count; ++i) sum = sum + fexp(scores[(int64_t)hl * a.seq_len + i] - mxs[hl]);
+      for (int i = 0; i < count - count4; ++i) sum = sum + fexp(tail_s[hl][i] - mxs[hl]);
       invs[hl] = 1.0f / sum;
     }
   }
@@ -323,33 +348,52 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
   // ---- phase 2: the weighted values ----
   acc = 0.0f;
   if (wave > 0) {
-    const int b = lane >> 1;  // the lane's four-position block; its heads lane % 2, lane % 2 + 2, ...
-    for (int c = wave - 1; c < n2; c += NPROD) {
-      wait_at_least(&used[1], c - NSLOT + 1);
-      float *slot = ring + (c % NSLOT) * SLOT;
+    // lane: four-position block b = lane / 2 of the chunk, heads lane % 2, lane % 2 + 2, ...; its values (4 rows of 8
+    // columns) and scores requested at once, and the wave's next chunk's
+    const int b = lane >> 1, h0 = lane & 1;
+    float4 va[8], vn[8], sa[MAXMUL / 2], sn[MAXMUL / 2];
+    auto fetch2 = [&](int c, float4 *v, float4 *sc) {
       const int p = min(c * P2 + 4 * b, count4 - 4);
       const int64_t at = (int64_t)p * kvdim + vbase;
-      const float4 v0a = cache4<HALF>(a.vcache, at), v0b = cache4<HALF>(a.vcache, at + 4);
-      const float4 v1a = cache4<HALF>(a.vcache, at + kvdim), v1b = cache4<HALF>(a.vcache, at + kvdim + 4);
-      const float4 v2a = cache4<HALF>(a.vcache, at + 2 * kvdim), v2b = cache4<HALF>(a.vcache, at + 2 * kvdim + 4);
-      const float4 v3a = cache4<HALF>(a.vcache, at + 3 * kvdim), v3b = cache4<HALF>(a.vcache, at + 3 * kvdim + 4);
-      for (int hl = lane & 1; hl < mul; hl += 2) {
-        const float4 sv = *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
-        const float mx = mxs[hl], inv = invs[hl];
-        const float p0 = vexp(sv.x - mx) * inv, p1 = vexp(sv.y - mx) * inv;
-        const float p2 = vexp(sv.z - mx) * inv, p3 = vexp(sv.w - mx) * inv;
-        float *row = slot + hl * PVJ * R2 + b;
-        row[0 * R2] = (p0 * v0a.x + p1 * v1a.x) + (p2 * v2a.x + p3 * v3a.x);
-        row[1 * R2] = (p0 * v0a.y + p1 * v1a.y) + (p2 * v2a.y + p3 * v3a.y);
-        row[2 * R2] = (p0 * v0a.z + p1 * v1a.z) + (p2 * v2a.z + p3 * v3a.z);
-        row[3 * R2] = (p0 * v0a.w + p1 * v1a.w) + (p2 * v2a.w + p3 * v3a.w);
-        row[4 * R2] = (p0 * v0b.x + p1 * v1b.x) + (p2 * v2b.x + p3 * v3b.x);
-        row[5 * R2] = (p0 * v0b.y + p1 * v1b.y) + (p2 * v2b.y + p3 * v3b.y);
-        row[6 * R2] = (p0 * v0b.z + p1 * v1b.z) + (p2 * v2b.z + p3 * v3b.z);
-        row[7 * R2] = (p0 * v0b.w + p1 * v1b.w) + (p2 * v2b.w + p3 * v3b.w);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        v[2 * r] = cache4<HALF>(a.vcache, at + r * kvdim);
+        v[2 * r + 1] = cache4<HALF>(a.vcache, at + r * kvdim + 4);
+      }
+#pragma unroll
+      for (int i = 0; i < MAXMUL / 2; ++i)
+        sc[i] = *reinterpret_cast<const float4 *>(scores + (int64_t)min(h0 + 2 * i, mul - 1) * a.seq_len + p);
+    };
+    int c = wave - 1;
+    if (c < n2) fetch2(c, va, sa);
+    for (; c < n2; c += NPROD) {
+      if (c + NPROD < n2) fetch2(c + NPROD, vn, sn);
+      wait_at_least(&used[1], c - NSLOT + 1);
+      float *slot = ring + (c % NSLOT) * SLOT;
+#pragma unroll
+      for (int i = 0; i < MAXMUL / 2; ++i) {
+        const int hl = h0 + 2 * i;
+        if (hl < mul) {
+          const float mx = mxs[hl], inv = invs[hl];
+          const float p0 = vexp(sa[i].x - mx) * inv, p1 = vexp(sa[i].y - mx) * inv;
+          const float p2 = vexp(sa[i].z - mx) * inv, p3 = vexp(sa[i].w - mx) * inv;
+          float *row = slot + hl * PVJ * R2 + b;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float4 x0 = va[h], x1 = va[2 + h], x2 = va[4 + h], x3 = va[6 + h];
+            row[(4 * h + 0) * R2] = (p0 * x0.x + p1 * x1.x) + (p2 * x2.x + p3 * x3.x);
+            row[(4 * h + 1) * R2] = (p0 * x0.y + p1 * x1.y) + (p2 * x2.y + p3 * x3.y);
+            row[(4 * h + 2) * R2] = (p0 * x0.z + p1 * x1.z) + (p2 * x2.z + p3 * x3.z);
+            row[(4 * h + 3) * R2] = (p0 * x0.w + p1 * x1.w) + (p2 * x2.w + p3 * x3.w);
+          }
+        }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) lds_store(&filled[c % NSLOT], c + 1);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) va[i] = vn[i];
+#pragma unroll
+      for (int i = 0; i < MAXMUL / 2; ++i) sa[i] = sn[i];
     }
   } else {
     for (int c = 0; c < n2; ++c) {
@@ -364,10 +408,7 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
     if (lane < mul * PVJ) {
       const int hl = lane / PVJ, j = lane % PVJ;
       const float mx = mxs[hl], inv = invs[hl];
-      for (int p = count4; p < count; ++p) {
-        const float pw = fexp(scores[(int64_t)hl * a.seq_len + p] - mx) * inv;
-        acc = acc + pw * cache1<HALF>(a.vcache, (int64_t)p * kvdim + vbase + j);
-      }
+      for (int i = 0; i < count - count4; ++i) acc = acc + (fexp(tail_s[hl][i] - mx) * inv) * tail_v[i][j];
       a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
     }
   }
