@@ -24,7 +24,7 @@ constexpr int TILE = 64;   // positions a block of (A)
 constexpr int MAXMUL = 8;  // query heads a kv head at most
 constexpr int PVJ = 8;     // columns a block of (C)
 constexpr int CH = 512;    // positions a chunk of (C)
-constexpr int FUSED_TOKENS = 8;  // up to this many tokens the softmax and the values run fused (below)
+constexpr int RING_TOKENS = 8;  // up to this many tokens the weighted values run on the ring kernel (below)
 
 template <bool HALF>
 __device__ __forceinline__ float4 cache4(const void *c, int64_t i) {  // four values from element i (i % 4 == 0)
@@ -223,25 +223,17 @@ __global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
   }
 }
 
-// (B+C) for a few tokens (decode): one block of 512 threads a (token, kv head, 8 of the head's columns), the softmax
-// of the nh / nkv query heads and their weighted values in one launch. Wave 0 runs the ordered sums; waves 1-7 each
-// produce every 7th chunk of what those sums add into a ring of LDS slots, as far ahead as the ring allows, with an
-// LDS flag a slot to say it is filled and a counter of the chunks wave 0 has used (no block-wide barrier a chunk, so
-// the producers' global loads overlap each other and the sums):
-//   phase 1 (chunks of 256 positions): the exponentials of every head, laid out by lane k = position % 4; wave 0's
-//            four ordered sums of every head advance over them; the tail and 1 / sum at the end;
-//   phase 2 (chunks of 128 positions): the exponentials again (the same bits), p = e * inv, and the four-position
-//            products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) of the block's 8 columns; wave 0's ordered sum of every
-//            (head, column) advances over them; the positions past the fours at the end.
-// Each of the hs / 8 blocks of a (token, kv head) computes the same softmax: redundant arithmetic, no launch and no
-// global round trip between the softmax and the values. Every wait is on another wave of the same block, for a chunk
-// of a lower index, so every wait ends.
-constexpr int P1 = 256, Q1 = P1 / 4, R1 = Q1 + 4;  // phase 1: positions, quads, LDS row (floats) of a chunk
-constexpr int P2 = 128, Q2 = P2 / 4, R2 = Q2 + 4;  // phase 2: positions, four-position blocks, LDS row of a chunk
-constexpr int NSLOT = 6;                           // ring slots
-constexpr int SLOT = MAXMUL * PVJ * R2;            // floats a slot (phase 1 takes MAXMUL * 4 * R1 <= SLOT)
-static_assert(MAXMUL * 4 * R1 <= SLOT, "a phase-1 chunk fits a slot");
-constexpr int NPROD = 7;                           // producer waves
+// (C) for a few tokens (decode): one block of 256 threads a (token, kv head, 8 of the head's columns), after (B) has
+// turned the scores into the weights p. Wave 0 runs the ordered sums of every (head, column); waves 1-3 each produce
+// every 3rd chunk of 256 positions of what those sums add, the four-position products
+// ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), into a ring of LDS slots, as far ahead as the ring allows, with the loads of
+// their next chunk in flight meanwhile. An LDS flag a slot says it is filled and a counter says how many chunks wave 0
+// has added: no block-wide barrier a chunk. Every wait is on another wave of the same block, for a chunk of a lower
+// index, so every wait ends.
+constexpr int RP = 256, RB = RP / 4, RR = RB + 4;  // positions, four-position blocks, LDS row (floats) of a chunk
+constexpr int NSLOT = 3;                           // ring slots
+constexpr int SLOT = MAXMUL * PVJ * RR;            // floats a slot
+constexpr int NPROD = 3;                           // producer waves
 
 __device__ __forceinline__ int lds_load(const int *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void lds_store(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
@@ -251,37 +243,24 @@ __device__ __forceinline__ void wait_at_least(const int *p, int v) {
 }
 
 template <int HS, bool HALF>
-__global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) void pv_ring_kernel(const AttnArgs a) {
   __shared__ float ring[NSLOT * SLOT];
-  __shared__ int filled[NSLOT], used[2];
-  __shared__ float mxs[MAXMUL], invs[MAXMUL];
-  __shared__ float tail_s[MAXMUL][4], tail_v[4][PVJ];  // the positions past the fours (at most 3)
+  __shared__ int filled[NSLOT], used;
+  __shared__ float tail_p[MAXMUL][4], tail_v[4][PVJ];  // the positions past the fours (at most 3)
   const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int count = a.pos0 + t + 1, count4 = count & ~3;
   const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
-  const int tiles = (count + TILE - 1) / TILE;
-  const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
+  const float *weights = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
   const int64_t vbase = (int64_t)kh * HS + j0;
-  const int n1 = (count4 + P1 - 1) / P1, n2 = (count4 + P2 - 1) / P2;
-  // a global load here takes about a microsecond: every wave requests what it needs next before it waits for any
+  const int chunks = (count4 + RP - 1) / RP;
 
   if (tid < NSLOT) filled[tid] = 0;
-  if (tid < 2) used[tid] = 0;
-  // wave w < mul: the largest score of head w from the tile maxima of the scores kernel (two loads a lane, together);
-  // wave 7: the positions past the fours, scores and values, into LDS
-  if (wave < mul) {
-    const float *tm = a.tilemax + ((int64_t)t * a.nh + kh * mul + wave) * (a.seq_len / TILE + 1);
-    const float m0 = tm[min(lane, tiles - 1)], m1 = tm[min(lane + 64, tiles - 1)];  // clamped: repeats are harmless
-    float mx = wmax(m0, m1);
-    for (int i = lane + 128; i < tiles; i += 64) mx = wmax(mx, tm[i]);  // contexts past 8192 positions
-    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-    if (lane == 0) mxs[wave] = mx;
-  }
-  if (wave == 7) {
+  if (tid == NSLOT) used = 0;
+  if (wave == 1) {  // the positions past the fours, weights and values, into LDS
     if (lane < MAXMUL * 4) {
       const int hl = min(lane >> 2, mul - 1), r = lane & 3;
-      tail_s[lane >> 2][r] = scores[(int64_t)hl * a.seq_len + min(count4 + r, count - 1)];
+      tail_p[lane >> 2][r] = weights[(int64_t)hl * a.seq_len + min(count4 + r, count - 1)];
     } else if (lane < MAXMUL * 4 + 4 * PVJ) {
       const int i = lane - MAXMUL * 4, r = i / PVJ, j = i % PVJ;
       tail_v[r][j] = cache1<HALF>(a.vcache, (int64_t)min(count4 + r, count - 1) * kvdim + vbase + j);
@@ -289,71 +268,12 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
   }
   __syncthreads();
 
-  // ---- phase 1: the sums ----
-  float acc = 0.0f;  // wave 0, lane hl * 4 + k: the sum of lane k of head hl; then (phase 2) lane hl * 8 + j
+  float acc = 0.0f;  // wave 0, lane hl * 8 + j
   if (wave > 0) {
-    // lane = the quad of the chunk; the scores of every head requested at once, the wave's next chunk (7 on) too
-    float4 cur[MAXMUL], nxt[MAXMUL];
-    auto fetch1 = [&](int c, float4 *dst) {
-      const int p = min(c * P1 + 4 * lane, count4 - 4);  // clamped: never added past count4
-#pragma unroll
-      for (int hl = 0; hl < MAXMUL; ++hl)
-        dst[hl] = *reinterpret_cast<const float4 *>(scores + (int64_t)min(hl, mul - 1) * a.seq_len + p);
-    };
-    int c = wave - 1;
-    if (c < n1) fetch1(c, cur);
-    for (; c < n1; c += NPROD) {
-      if (c + NPROD < n1) fetch1(c + NPROD, nxt);
-      wait_at_least(&used[0], c - NSLOT + 1);  // the slot's last chunk has been added
-      float *slot = ring + (c % NSLOT) * SLOT;
-#pragma unroll
-      for (int hl = 0; hl < MAXMUL; ++hl) {
-        if (hl < mul) {
-          const float mx = mxs[hl];
-          float *row = slot + hl * 4 * R1 + lane;
-          row[0] = vexp(cur[hl].x - mx);
-          row[R1] = vexp(cur[hl].y - mx);
-          row[2 * R1] = vexp(cur[hl].z - mx);
-          row[3 * R1] = vexp(cur[hl].w - mx);
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) lds_store(&filled[c % NSLOT], c + 1);
-#pragma unroll
-      for (int hl = 0; hl < MAXMUL; ++hl) cur[hl] = nxt[hl];
-    }
-  } else {
-    for (int c = 0; c < n1; ++c) {
-      wait_at_least(&filled[c % NSLOT], c + 1);
-      if (lane < mul * 4) {
-        const int nq = min(P1, count4 - c * P1) >> 2;
-        acc = lds_chain(ring + (c % NSLOT) * SLOT + (lane >> 2) * 4 * R1 + (lane & 3) * R1, nq, acc);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) lds_store(&used[0], c + 1);
-    }
-    // ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
-    const float l1 = __shfl_down(acc, 1, 64), l2 = __shfl_down(acc, 2, 64), l3 = __shfl_down(acc, 3, 64);
-    if (lane < mul * 4 && (lane & 3) == 0) {
-      const int hl = lane >> 2;
-      float sum = ((acc + l1) + l2) + l3;
-      for (int i = 0; i < count - count4; ++i) sum = sum + fexp(tail_s[hl][i] - mxs[hl]);
-      invs[hl] = 1.0f / sum;
-    }
-  }
-  __syncthreads();
-  if (tid < NSLOT) filled[tid] = 0;
-  __syncthreads();
-
-  // ---- phase 2: the weighted values ----
-  acc = 0.0f;
-  if (wave > 0) {
-    // lane: four-position block b = lane / 2 of the chunk, heads lane % 2, lane % 2 + 2, ...; its values (4 rows of 8
-    // columns) and scores requested at once, and the wave's next chunk's
-    const int b = lane >> 1, h0 = lane & 1;
-    float4 va[8], vn[8], sa[MAXMUL / 2], sn[MAXMUL / 2];
-    auto fetch2 = [&](int c, float4 *v, float4 *sc) {
-      const int p = min(c * P2 + 4 * b, count4 - 4);
+    // lane = the four-position block b of the chunk: its 4 value rows (8 columns) and every head's 4 weights
+    float4 va[8], vn[8], pa[MAXMUL], pn[MAXMUL];
+    auto fetch = [&](int c, float4 *v, float4 *pw) {
+      const int p = min(c * RP + 4 * lane, count4 - 4);  // clamped: never added past count4
       const int64_t at = (int64_t)p * kvdim + vbase;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -361,30 +281,27 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
         v[2 * r + 1] = cache4<HALF>(a.vcache, at + r * kvdim + 4);
       }
 #pragma unroll
-      for (int i = 0; i < MAXMUL / 2; ++i)
-        sc[i] = *reinterpret_cast<const float4 *>(scores + (int64_t)min(h0 + 2 * i, mul - 1) * a.seq_len + p);
+      for (int hl = 0; hl < MAXMUL; ++hl)
+        pw[hl] = *reinterpret_cast<const float4 *>(weights + (int64_t)min(hl, mul - 1) * a.seq_len + p);
     };
     int c = wave - 1;
-    if (c < n2) fetch2(c, va, sa);
-    for (; c < n2; c += NPROD) {
-      if (c + NPROD < n2) fetch2(c + NPROD, vn, sn);
-      wait_at_least(&used[1], c - NSLOT + 1);
+    if (c < chunks) fetch(c, va, pa);
+    for (; c < chunks; c += NPROD) {
+      if (c + NPROD < chunks) fetch(c + NPROD, vn, pn);  // the wave's next chunk flies meanwhile
+      wait_at_least(&used, c - NSLOT + 1);                // the slot's last chunk has been added
       float *slot = ring + (c % NSLOT) * SLOT;
 #pragma unroll
-      for (int i = 0; i < MAXMUL / 2; ++i) {
-        const int hl = h0 + 2 * i;
+      for (int hl = 0; hl < MAXMUL; ++hl) {
         if (hl < mul) {
-          const float mx = mxs[hl], inv = invs[hl];
-          const float p0 = vexp(sa[i].x - mx) * inv, p1 = vexp(sa[i].y - mx) * inv;
-          const float p2 = vexp(sa[i].z - mx) * inv, p3 = vexp(sa[i].w - mx) * inv;
-          float *row = slot + hl * PVJ * R2 + b;
+          const float p0 = pa[hl].x, p1 = pa[hl].y, p2 = pa[hl].z, p3 = pa[hl].w;
+          float *row = slot + hl * PVJ * RR + lane;
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const float4 x0 = va[h], x1 = va[2 + h], x2 = va[4 + h], x3 = va[6 + h];
-            row[(4 * h + 0) * R2] = (p0 * x0.x + p1 * x1.x) + (p2 * x2.x + p3 * x3.x);
-            row[(4 * h + 1) * R2] = (p0 * x0.y + p1 * x1.y) + (p2 * x2.y + p3 * x3.y);
-            row[(4 * h + 2) * R2] = (p0 * x0.z + p1 * x1.z) + (p2 * x2.z + p3 * x3.z);
-            row[(4 * h + 3) * R2] = (p0 * x0.w + p1 * x1.w) + (p2 * x2.w + p3 * x3.w);
+            row[(4 * h + 0) * RR] = (p0 * x0.x + p1 * x1.x) + (p2 * x2.x + p3 * x3.x);
+            row[(4 * h + 1) * RR] = (p0 * x0.y + p1 * x1.y) + (p2 * x2.y + p3 * x3.y);
+            row[(4 * h + 2) * RR] = (p0 * x0.z + p1 * x1.z) + (p2 * x2.z + p3 * x3.z);
+            row[(4 * h + 3) * RR] = (p0 * x0.w + p1 * x1.w) + (p2 * x2.w + p3 * x3.w);
           }
         }
       }
@@ -393,22 +310,21 @@ __global__ __launch_bounds__(512) void softmax_pv_kernel(const AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) va[i] = vn[i];
 #pragma unroll
-      for (int i = 0; i < MAXMUL / 2; ++i) sa[i] = sn[i];
+      for (int hl = 0; hl < MAXMUL; ++hl) pa[hl] = pn[hl];
     }
   } else {
-    for (int c = 0; c < n2; ++c) {
+    for (int c = 0; c < chunks; ++c) {
       wait_at_least(&filled[c % NSLOT], c + 1);
       if (lane < mul * PVJ) {
-        const int nb = min(P2, count4 - c * P2) >> 2;
-        acc = lds_chain(ring + (c % NSLOT) * SLOT + lane * R2, nb, acc);
+        const int nb = min(RP, count4 - c * RP) >> 2;
+        acc = lds_chain(ring + (c % NSLOT) * SLOT + lane * RR, nb, acc);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) lds_store(&used[1], c + 1);
+      if (lane == 0) lds_store(&used, c + 1);
     }
     if (lane < mul * PVJ) {
       const int hl = lane / PVJ, j = lane % PVJ;
-      const float mx = mxs[hl], inv = invs[hl];
-      for (int i = 0; i < count - count4; ++i) acc = acc + (fexp(tail_s[hl][i] - mx) * inv) * tail_v[i][j];
+      for (int i = 0; i < count - count4; ++i) acc = acc + tail_p[hl][i] * tail_v[i][j];
       a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
     }
   }
@@ -418,14 +334,13 @@ template <int HS, bool HALF>
 hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
   hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
-  if (a.m <= FUSED_TOKENS) {
-    hipLaunchKernelGGL((softmax_pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(512), 0, s, a);
-    return hipGetLastError();
-  }
   const int most4 = (a.pos0 + a.m) & ~3;
   const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
-  hipLaunchKernelGGL((pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
+  if (a.m <= RING_TOKENS)
+    hipLaunchKernelGGL((pv_ring_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
