@@ -12,6 +12,8 @@
 // the whole row go to LDS, laid out so that the lane holding accumulator k of token t reads its groups in order.
 #pragma clang fp contract(off)
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -198,6 +200,53 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   }
 }
 
+// a.norm, by the launch's last block to finish: every block's outputs are released device-wide before it counts
+// itself, and the last one acquires them before it reads the residual. rmsnorm's squares in four lanes (j % 4) added
+// in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail in order; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
+// out = w * (s * x); quantize_x of out a half-wave a group. sq: 4 * ((n / 4 + 3) & ~3) floats of LDS.
+__device__ void norm_next(const NormNext &nn, float *sq) {
+  __shared__ int last;
+  __shared__ float part[4], sval;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last = atomicAdd(nn.counter, 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const int tid = threadIdx.x, n = nn.n, n4 = n & ~3, q4 = n4 >> 2, qs = (q4 + 3) & ~3;
+  const float4 *x4 = reinterpret_cast<const float4 *>(nn.x);
+  for (int base = 0; base < q4; base += 256 * 8) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = x4[min(base + tid + 256 * u, q4 - 1)];  // clamped: all requested at once
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j4 = base + tid + 256 * u;
+      if (j4 < q4) {
+        sq[j4] = v[u].x * v[u].x;
+        sq[qs + j4] = v[u].y * v[u].y;
+        sq[2 * qs + j4] = v[u].z * v[u].z;
+        sq[3 * qs + j4] = v[u].w * v[u].w;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
+  __syncthreads();
+  if (tid == 0) {
+    float ss = ((part[0] + part[1]) + part[2]) + part[3];
+    for (int j = n4; j < n; ++j) ss = ss + nn.x[j] * nn.x[j];
+    sval = 1.0f / __builtin_sqrtf(ss / (float)n + nn.eps);
+  }
+  __syncthreads();
+  const float sc = sval;
+  for (int g = tid >> 5; g < n / GS; g += blockDim.x / 32) {
+    const int j = g * GS + (tid & 31);
+    quantize_group(nn.w[j] * (sc * nn.x[j]), nn.xq, nn.xs, j, g, nn.bias);
+  }
+  if (tid == 0) *nn.counter = 0;  // for the next launch that uses it (stream order)
+}
+
 // The decode path proper (one token, int8, bias 64): a wave takes R consecutive rows (about 16 KiB of weights) and
 // requests all of them with their scales before anything else (a scheduling barrier keeps the compiler from sinking
 // the loads next to their uses); meanwhile the block stages the token's activations, centred, and their scales in
@@ -275,7 +324,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
     }
   __syncthreads();
-  if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
+  const bool active = (blockIdx.x * WAVES + wave) * R < a.total_rows;
+  if (active) {
   // fully unrolled (no early exit), so that wr stays in registers
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
@@ -314,6 +364,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     float *y = at.y + at.r;
     *y = at.accumulate ? *y + sum : sum;
   }
+  }
+  if (a.norm.counter) norm_next(a.norm, smem);
 }
 
 template <int R, int NS>
@@ -321,8 +373,9 @@ hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const int waves = (a.total_rows + R - 1) / R;
   const int blocks = (waves + WAVES - 1) / WAVES;
   const size_t g16 = ((a.k / GS) + 3) & ~3;
-  const size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
-                     sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
+  size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
+               sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
+  if (a.norm.counter) lds = std::max(lds, sizeof(float) * 4 * (size_t)(((a.norm.n / 4) + 3) & ~3));
   hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }
@@ -370,9 +423,14 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
   return m < 1 ? 0 : (m > 8 ? 8 : m);
 }
 
+bool decode_path(const MatArgs &a, bool six, bool relaxed) {
+  return a.sums == nullptr && !six && relaxed && a.m == 1 && a.k <= 20 * 1024;
+}
+
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
-  if (!sums && !six && relaxed && a.m == 1 && a.k <= 20 * 1024) return launch_decode(a, s);
+  if (decode_path(a, six, relaxed)) return launch_decode(a, s);
+  if (a.norm.counter) return hipErrorInvalidValue;
   if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;
   if (six) {
     if (relaxed) return sums ? launch_sel<true, true, true>(a, s) : launch_sel<true, true, false>(a, s);
