@@ -200,33 +200,44 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   }
 }
 
-// a.norm, by the launch's last block to finish: every block's outputs are released device-wide before it counts
-// itself, and the last one acquires them before it reads the residual. rmsnorm's squares in four lanes (j % 4) added
+// a.norm, by the launch's last block to finish. The blocks write their outputs with atomic exchanges and wait for them
+// before they count themselves (an atomic counter); the last block reads the residual with atomic read-modify-writes
+// that change no bit. Device-scope atomics are performed at one point of coherence for every XCD, so the last
+// block sees every output. (Device-scope fences instead would write back and invalidate whole L2s in every block:
+// far slower.) rmsnorm's squares in four lanes (j % 4) added
 // in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail in order; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
-// out = w * (s * x); quantize_x of out a half-wave a group. sq: 4 * ((n / 4 + 3) & ~3) floats of LDS.
+// out = w * (s * x); quantize_x of out a half-wave a group. sq: 4 * ((n / 4 + 3) & ~3) + n floats of LDS.
+// the value at p, by a compare-and-swap that writes back what it finds (an atomic read-modify-write that changes no
+// bit; the compiler keeps it, where it turns an idempotent or / add into a plain load)
+__device__ __forceinline__ float coherent_read(float *p) {
+  uint32_t seen = 0x7fc0dead;
+  __hip_atomic_compare_exchange_strong(reinterpret_cast<uint32_t *>(p), &seen, 0x7fc0deadu, __ATOMIC_RELAXED,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __uint_as_float(seen);
+}
+
 __device__ void norm_next(const NormNext &nn, float *sq) {
   __shared__ int last;
   __shared__ float part[4], sval;
-  __threadfence();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this thread's stores have completed
   __syncthreads();
-  if (threadIdx.x == 0) last = atomicAdd(nn.counter, 1) == (int)gridDim.x - 1;
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(nn.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
   __syncthreads();
   if (!last) return;
-  __threadfence();
   const int tid = threadIdx.x, n = nn.n, n4 = n & ~3, q4 = n4 >> 2, qs = (q4 + 3) & ~3;
-  const float4 *x4 = reinterpret_cast<const float4 *>(nn.x);
-  for (int base = 0; base < q4; base += 256 * 8) {
-    float4 v[8];
+  float *xl = sq + 4 * qs;  // the residual, n floats
+  for (int base = 0; base < n; base += 256 * 16) {
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = x4[min(base + tid + 256 * u, q4 - 1)];  // clamped: all requested at once
+    for (int u = 0; u < 16; ++u)  // clamped: all requested at once
+      v[u] = coherent_read(nn.x + min(base + tid + 256 * u, n - 1));
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j4 = base + tid + 256 * u;
-      if (j4 < q4) {
-        sq[j4] = v[u].x * v[u].x;
-        sq[qs + j4] = v[u].y * v[u].y;
-        sq[2 * qs + j4] = v[u].z * v[u].z;
-        sq[3 * qs + j4] = v[u].w * v[u].w;
+    for (int u = 0; u < 16; ++u) {
+      const int j = base + tid + 256 * u;
+      if (j < n) {
+        xl[j] = v[u];
+        if (j < n4) sq[(j & 3) * qs + (j >> 2)] = v[u] * v[u];
       }
     }
   }
@@ -235,14 +246,14 @@ __device__ void norm_next(const NormNext &nn, float *sq) {
   __syncthreads();
   if (tid == 0) {
     float ss = ((part[0] + part[1]) + part[2]) + part[3];
-    for (int j = n4; j < n; ++j) ss = ss + nn.x[j] * nn.x[j];
+    for (int j = n4; j < n; ++j) ss = ss + xl[j] * xl[j];
     sval = 1.0f / __builtin_sqrtf(ss / (float)n + nn.eps);
   }
   __syncthreads();
   const float sc = sval;
   for (int g = tid >> 5; g < n / GS; g += blockDim.x / 32) {
     const int j = g * GS + (tid & 31);
-    quantize_group(nn.w[j] * (sc * nn.x[j]), nn.xq, nn.xs, j, g, nn.bias);
+    quantize_group(nn.w[j] * (sc * xl[j]), nn.xq, nn.xs, j, g, nn.bias);
   }
   if (tid == 0) *nn.counter = 0;  // for the next launch that uses it (stream order)
 }
@@ -362,7 +373,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
     const RowAt at = row_at(a, row0 + lane);
     float *y = at.y + at.r;
-    *y = at.accumulate ? *y + sum : sum;
+    const float v = at.accumulate ? *y + sum : sum;
+    if (a.norm.counter) (void)__hip_atomic_exchange(y, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *y = v;
   }
   }
   if (a.norm.counter) norm_next(a.norm, smem);
@@ -375,7 +388,7 @@ hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const size_t g16 = ((a.k / GS) + 3) & ~3;
   size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
                sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
-  if (a.norm.counter) lds = std::max(lds, sizeof(float) * 4 * (size_t)(((a.norm.n / 4) + 3) & ~3));
+  if (a.norm.counter) lds = std::max(lds, sizeof(float) * (4 * (size_t)(((a.norm.n / 4) + 3) & ~3) + a.norm.n));
   hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }

@@ -24,7 +24,7 @@ struct MatSeg {
 // counter: zero before the launch (the last block sets it back to zero); null: none.
 struct NormNext {
   int32_t *counter;
-  const float *x;  // the residual (n floats), the output of this matmul
+  float *x;        // the residual (n floats), the output of this matmul (read with atomics that change no bit)
   const float *w;  // the norm's weights
   int8_t *xq;
   float *xs;
