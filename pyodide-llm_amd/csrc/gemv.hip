@@ -216,7 +216,7 @@ __device__ __forceinline__ float coherent_read(float *p) {
   return __uint_as_float(seen);
 }
 
-__device__ void norm_next(const NormNext &nn, float *sq) {
+__device__ void norm_next(const NormNext &nn, float *sq) {  // blocks of 256 threads
   __shared__ int last;
   __shared__ float part[4], sval;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this thread's stores have completed
@@ -251,9 +251,17 @@ __device__ void norm_next(const NormNext &nn, float *sq) {
   }
   __syncthreads();
   const float sc = sval;
-  for (int g = tid >> 5; g < n / GS; g += blockDim.x / 32) {
-    const int j = g * GS + (tid & 31);
-    quantize_group(nn.w[j] * (sc * xl[j]), nn.xq, nn.xs, j, g, nn.bias);
+  // quantize_x a half-wave a group: thread tid takes positions tid + 256 i, i.e. group (tid / 32) + 8 i; the weights
+  // of 16 groups requested at once
+  for (int base = 0; base < n; base += 256 * 16) {
+    float wv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) wv[u] = nn.w[min(base + tid + 256 * u, n - 1)];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int j = base + tid + 256 * u;
+      if (j - (tid & 31) < n) quantize_group(wv[u] * (sc * xl[min(j, n - 1)]), nn.xq, nn.xs, j, j / GS, nn.bias);
+    }
   }
   if (tid == 0) *nn.counter = 0;  // for the next launch that uses it (stream order)
 }
