@@ -116,7 +116,6 @@ struct he_engine {
   int32_t *amax_i = nullptr;
   float *best_v = nullptr;
   int32_t *best_i = nullptr;
-  int32_t *norm_counter = nullptr;  // the decode matmuls' last-block rmsnorm (NormNext.counter)
   uint64_t device_bytes = 0;
   bool have_logits = false;
   // he_profile_forward: event pairs around every launch while `profiling` is set
@@ -146,7 +145,7 @@ void destroy(he_engine *e) {
   if (!e) return;
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
-                  e->best_v, e->best_i, e->norm_counter};
+                  e->best_v, e->best_i};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -268,8 +267,6 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->amax_i, sizeof(int32_t) * 256);
   ALLOC(e->best_v, sizeof(float) * 4);
   ALLOC(e->best_i, sizeof(int32_t) * 4);
-  ALLOC(e->norm_counter, sizeof(int32_t) * 4);
-  HIP_TRY(hipMemset(e->norm_counter, 0, sizeof(int32_t) * 4));
 #undef ALLOC
   return HE_OK;
 }
@@ -325,7 +322,7 @@ double matmul_bytes(const he_engine *e, const MatSeg *segs, int nseg, int32_t k,
 }
 
 hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
-                         const float *xs, const NormNext *norm = nullptr) {
+                         const float *xs) {
   const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
   const int32_t step = gemv_tokens(k, e->c.relaxed);
   if (step < 1) return hipErrorInvalidValue;
@@ -345,7 +342,6 @@ hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, 
     a.k = k;
     a.m = std::min(step, m - t0);
     a.sums = nullptr;
-    if (norm) a.norm = *norm;
     hipError_t err = launch_gemv(a, e->c.six, e->c.relaxed, e->stream);
     if (err != hipSuccess) return err;
   }
@@ -374,26 +370,12 @@ hipError_t gemm_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, in
   return launch_gemm(a, e->c.six, e->c.relaxed, e->stream);
 }
 
-hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs,
-                  const NormNext *norm = nullptr) {
+hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs) {
   if (use_gemm(e, k, m))
     return timed(e, HE_K_GEMM, matmul_bytes(e, segs, nseg, k, m),
                  [&] { return gemm_launch(e, segs, nseg, k, m, xq, xs); });
   return timed(e, HE_K_GEMV, matmul_bytes(e, segs, nseg, k, m),
-               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, norm); });
-}
-
-// whether a one-token matmul of rows of k runs on the decode path, whose last block can run the next rmsnorm
-bool norm_fuses(const he_engine *e, int32_t k, int32_t m) {
-  MatArgs a{};
-  a.m = m;
-  a.k = k;
-  return decode_path(a, e->c.six != 0, e->c.relaxed != 0);
-}
-
-// rmsnorm + quantize_x of the (one) token's residual into the activations, by the matmul's last block
-NormNext norm_after(he_engine *e, const float *w) {
-  return NormNext{e->norm_counter, e->x, w, e->xq, e->xs, e->c.dim, e->c.rms_norm_eps, e->bias};
+               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs); });
 }
 
 int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, bool need_logits) {
@@ -407,14 +389,11 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     return launch_embed(e->x, e->tokens, e->values[HE_T_EMBEDDING], e->scales[HE_T_EMBEDDING], m, dim, dim,
                         c.six ? 32 : group_size(dim), c.six, s);
   }));
-  bool normed = false;  // xq / xs hold the rmsnorm of x already (run by the last matmul's last block)
   for (int32_t l = 0; l < c.n_layers; ++l) {
-    if (!normed)
-      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
-                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s);
-      }));
-    normed = false;
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim, W,
+                                  W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
     const MatSeg qkv[3] = {
         {e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), e->q, qdim, qdim, 0},
         {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), e->k, kvdim, kvdim, 0},
@@ -464,16 +443,11 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     HIP_TRY(timed(e, HE_K_NORM, (double)m * qdim * (4 + 1 + 0.125),
                   [&] { return launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s); }));
     const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
-    if (norm_fuses(e, qdim, m)) {
-      const NormNext nn = norm_after(e, e->vec(HE_T_RMS_FFN, (int64_t)l * dim));
-      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs, &nn));
-    } else {
-      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
-      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim,
-                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s);
-      }));
-    }
+    HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
+                                  W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
     const MatSeg w13[2] = {{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), e->hb, hidden, hidden, 0},
                            {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), e->hb2, hidden, hidden, 0}};
     HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs));
@@ -481,23 +455,13 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
       return launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s);
     }));
     const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
-    // the next rmsnorm: the next layer's, or the final one where logits are wanted
-    const float *next = l + 1 < c.n_layers ? e->vec(HE_T_RMS_ATT, (int64_t)(l + 1) * dim)
-                                           : (need_logits ? e->vec(HE_T_RMS_FINAL, 0) : nullptr);
-    if (next && norm_fuses(e, hidden, m)) {
-      const NormNext nn = norm_after(e, next);
-      HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs, &nn));
-      normed = true;
-    } else {
-      HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs));
-    }
+    HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs));
   }
   if (need_logits) {
-    if (!normed)
-      HIP_TRY(timed(e, HE_K_NORM, (double)dim * (8 + 1 + 0.125), [&] {
-        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x + (int64_t)(m - 1) * dim, e->vec(HE_T_RMS_FINAL, 0),
-                                    1, dim, dim, W, W / 32, 0, c.rms_norm_eps, e->bias, s);
-      }));
+    HIP_TRY(timed(e, HE_K_NORM, (double)dim * (8 + 1 + 0.125), [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x + (int64_t)(m - 1) * dim, e->vec(HE_T_RMS_FINAL, 0), 1,
+                                  dim, dim, W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
     const MatSeg cls[1] = {{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), e->logits, c.vocab_size, 0, 0}};
     HIP_TRY(matmul(e, cls, 1, dim, 1, e->xq, e->xs));
     e->have_logits = true;

@@ -12,8 +12,6 @@
 // the whole row go to LDS, laid out so that the lane holding accumulator k of token t reads its groups in order.
 #pragma clang fp contract(off)
 
-#include <algorithm>
-
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -200,72 +198,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   }
 }
 
-// a.norm, by the launch's last block to finish. The blocks write their outputs with atomic exchanges and wait for them
-// before they count themselves (an atomic counter); the last block reads the residual with atomic read-modify-writes
-// that change no bit. Device-scope atomics are performed at one point of coherence for every XCD, so the last
-// block sees every output. (Device-scope fences instead would write back and invalidate whole L2s in every block:
-// far slower.) rmsnorm's squares in four lanes (j % 4) added
-// in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail in order; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
-// out = w * (s * x); quantize_x of out a half-wave a group. sq: 4 * ((n / 4 + 3) & ~3) + n floats of LDS.
-// the value at p, by a compare-and-swap that writes back what it finds (an atomic read-modify-write that changes no
-// bit; the compiler keeps it, where it turns an idempotent or / add into a plain load)
-__device__ __forceinline__ float coherent_read(float *p) {
-  uint32_t seen = 0x7fc0dead;
-  __hip_atomic_compare_exchange_strong(reinterpret_cast<uint32_t *>(p), &seen, 0x7fc0deadu, __ATOMIC_RELAXED,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __uint_as_float(seen);
-}
-
-__device__ void norm_next(const NormNext &nn, float *sq) {  // blocks of 256 threads
-  __shared__ int last;
-  __shared__ float part[4], sval;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // this thread's stores have completed
-  __syncthreads();
-  if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(nn.counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
-  __syncthreads();
-  if (!last) return;
-  const int tid = threadIdx.x, n = nn.n, n4 = n & ~3, q4 = n4 >> 2, qs = (q4 + 3) & ~3;
-  float *xl = sq + 4 * qs;  // the residual, n floats
-  for (int base = 0; base < n; base += 256 * 16) {
-    float v[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u)  // clamped: all requested at once
-      v[u] = coherent_read(nn.x + min(base + tid + 256 * u, n - 1));
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int j = base + tid + 256 * u;
-      if (j < n) {
-        xl[j] = v[u];
-        if (j < n4) sq[(j & 3) * qs + (j >> 2)] = v[u] * v[u];
-      }
-    }
-  }
-  __syncthreads();
-  if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
-  __syncthreads();
-  if (tid == 0) {
-    float ss = ((part[0] + part[1]) + part[2]) + part[3];
-    for (int j = n4; j < n; ++j) ss = ss + xl[j] * xl[j];
-    sval = 1.0f / __builtin_sqrtf(ss / (float)n + nn.eps);
-  }
-  __syncthreads();
-  const float sc = sval;
-  // quantize_x a half-wave a group: thread tid takes positions tid + 256 i, i.e. group (tid / 32) + 8 i; the weights
-  // of 16 groups requested at once
-  for (int base = 0; base < n; base += 256 * 16) {
-    float wv[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) wv[u] = nn.w[min(base + tid + 256 * u, n - 1)];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int j = base + tid + 256 * u;
-      if (j - (tid & 31) < n) quantize_group(wv[u] * (sc * xl[min(j, n - 1)]), nn.xq, nn.xs, j, j / GS, nn.bias);
-    }
-  }
-  if (tid == 0) *nn.counter = 0;  // for the next launch that uses it (stream order)
-}
-
 // The decode path proper (one token, int8, bias 64): a wave takes R consecutive rows (about 16 KiB of weights) and
 // requests all of them with their scales before anything else (a scheduling barrier keeps the compiler from sinking
 // the loads next to their uses); meanwhile the block stages the token's activations, centred, and their scales in
@@ -343,8 +275,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
     }
   __syncthreads();
-  const bool active = (blockIdx.x * WAVES + wave) * R < a.total_rows;
-  if (active) {
+  if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
   // fully unrolled (no early exit), so that wr stays in registers
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
@@ -381,12 +312,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
     const RowAt at = row_at(a, row0 + lane);
     float *y = at.y + at.r;
-    const float v = at.accumulate ? *y + sum : sum;
-    if (a.norm.counter) (void)__hip_atomic_exchange(y, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *y = v;
+    *y = at.accumulate ? *y + sum : sum;
   }
-  }
-  if (a.norm.counter) norm_next(a.norm, smem);
 }
 
 template <int R, int NS>
@@ -394,9 +321,8 @@ hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const int waves = (a.total_rows + R - 1) / R;
   const int blocks = (waves + WAVES - 1) / WAVES;
   const size_t g16 = ((a.k / GS) + 3) & ~3;
-  size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
-               sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
-  if (a.norm.counter) lds = std::max(lds, sizeof(float) * (4 * (size_t)(((a.norm.n / 4) + 3) & ~3) + a.norm.n));
+  const size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
+                     sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
   hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }
@@ -444,14 +370,9 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
   return m < 1 ? 0 : (m > 8 ? 8 : m);
 }
 
-bool decode_path(const MatArgs &a, bool six, bool relaxed) {
-  return a.sums == nullptr && !six && relaxed && a.m == 1 && a.k <= 20 * 1024;
-}
-
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
-  if (decode_path(a, six, relaxed)) return launch_decode(a, s);
-  if (a.norm.counter) return hipErrorInvalidValue;
+  if (!sums && !six && relaxed && a.m == 1 && a.k <= 20 * 1024) return launch_decode(a, s);
   if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;
   if (six) {
     if (relaxed) return sums ? launch_sel<true, true, true>(a, s) : launch_sel<true, true, false>(a, s);

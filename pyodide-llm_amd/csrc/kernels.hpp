@@ -19,20 +19,6 @@ struct MatSeg {
   int32_t accumulate;
 };
 
-// rmsnorm then quantize_x of the residual a decode matmul has just accumulated, run by the launch's last block to
-// finish (kernels/kernel.ts:330-342 then :129-156): the next matmul's activations without a launch of their own.
-// counter: zero before the launch (the last block sets it back to zero); null: none.
-struct NormNext {
-  int32_t *counter;
-  float *x;        // the residual (n floats), the output of this matmul (read with atomics that change no bit)
-  const float *w;  // the norm's weights
-  int8_t *xq;
-  float *xs;
-  int32_t n;
-  float eps;
-  int32_t bias;
-};
-
 struct MatArgs {
   MatSeg seg[3];
   int32_t nseg;
@@ -44,7 +30,6 @@ struct MatArgs {
   int32_t k;
   int32_t m;
   int32_t *sums;  // group-sum output (hk_group_sums) or null
-  NormNext norm;  // the decode path only (decode_path); counter null elsewhere
 };
 
 // the most tokens the engine gives one GEMV pass: more go to the MFMA GEMM where it takes them
@@ -52,8 +37,6 @@ constexpr int32_t GEMV_MOST = 8;
 
 // decode GEMV, m <= 8 tokens: exact int32 group sums, the reference's float32 order
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
-// whether launch_gemv takes a on its one-token decode path (the only one that runs a.norm)
-bool decode_path(const MatArgs &a, bool six, bool relaxed);
 // the most tokens one launch_gemv takes for rows of k (its products of a row fit the block's LDS)
 int32_t gemv_tokens(int32_t k, bool relaxed);
 // prefill GEMM on i8 MFMA, any m (bias 64, int8 or int6): the same bits as launch_gemv per (token, row); with

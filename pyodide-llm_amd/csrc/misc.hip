@@ -12,6 +12,16 @@ namespace ple {
 
 namespace {
 
+// one group of 32 a half-wave: amax (order-free), scale = f32(amax / qmax), inv = scale > 0 ? f32(1 / scale) : 0
+__device__ __forceinline__ void quantize_group(float v, int8_t *xq, float *xs, int j, int g, int32_t bias) {
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  const float amax = wave_max32(__builtin_fabsf(v));
+  const float scale = amax / qmax;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  xq[j] = quant_value(v, inv, bias);
+  if ((threadIdx.x & 31) == 0) xs[g] = scale;
+}
+
 __global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n,
                                                        int32_t x_stride, int32_t xq_stride, int32_t xs_stride,
                                                        int32_t bias) {
