@@ -316,6 +316,151 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   }
 }
 
+// The int6 decode path (one token, six.ts groups, bias 64: kernels/kernel_relaxed.ts:189-218 matmul_q6r): as
+// gemv1_kernel, with a lane taking two consecutive groups of 24 bytes (48 bytes, three 16-byte loads) of each of its
+// wave's R rows, 128 groups a wave step, widened to int8 in registers (kernels/six.ts) next to their use.
+// NS: wave steps, NS * 128 groups >= K / 32.
+template <int R, int NS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv6_kernel(const MatArgs a) {
+  constexpr int SV = (NS * 128 + 255) / 256;  // float4 of a row's scales a lane
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int K = a.k, G = K / GS, G4 = G & ~3, G16 = (G + 3) & ~3;
+  const int steps = (G + 127) / 128;
+  const RowLayout lay = row_layout(K, true);
+  uint32_t *xl = reinterpret_cast<uint32_t *>(smem);   // K bytes of centred activations
+  float *xsl = smem + K / 4;                           // G scales of the activations
+  float *wsl = xsl + G16 + wave * R * G16;             // this wave's rows' weight scales
+  float *P = xsl + G16 + WAVES * R * G16 + wave * R * lay.stride;  // this wave's products
+  const int row0 = min((blockIdx.x * WAVES + wave) * R, a.total_rows - 1);
+  uint4 wr[R][NS][3];
+  float4 sr[R][SV];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const RowAt at = row_at(a, min(row0 + i, a.total_rows - 1));  // rows past the end: the last again, unused
+    const uint8_t *w = at.w + (int64_t)at.r * G * 24;
+    const float *ws = at.ws + (int64_t)at.r * G;
+    // unconditional loads from clamped (always valid) addresses: groups 2 * pair and 2 * pair + 1 of the step
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int pair = min(u * 64 + lane, (G - 2) >> 1);  // G is even where it matters; an odd G's last pair clamps
+      const uint4 *p = reinterpret_cast<const uint4 *>(w + (int64_t)pair * 48);
+      wr[i][u][0] = p[0];
+      wr[i][u][1] = p[1];
+      wr[i][u][2] = p[2];
+    }
+#pragma unroll
+    for (int u = 0; u < SV; ++u) {
+      const int f = min(4 * (lane + 64 * u), G16 - 4);
+      if ((reinterpret_cast<uintptr_t>(ws) & 15) == 0 && f + 4 <= G) {
+        sr[i][u] = *reinterpret_cast<const float4 *>(ws + f);
+      } else {
+        sr[i][u] = make_float4(ws[min(f, G - 1)], ws[min(f + 1, G - 1)], ws[min(f + 2, G - 1)], ws[min(f + 3, G - 1)]);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    constexpr int XL = (NS * 4096 / 16 + 255) / 256;
+    uint4 xv[XL];
+    float sv[SV * 4 / 4 + 1];
+#pragma unroll
+    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
+#pragma unroll
+    for (int u = 0; u < SV * 4 / 4 + 1; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < K / 16)
+        reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
+                                                      centre4(xv[u].w));
+    }
+#pragma unroll
+    for (int u = 0; u < SV * 4 / 4 + 1; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      if (i < G) xsl[i] = sv[u];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int u = 0; u < SV; ++u) {
+      const int f = 4 * (lane + 64 * u);
+      if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
+    }
+  __syncthreads();
+  if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    if (u < steps) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int g = u * 128 + 2 * lane + h;
+        const int gc = min(g, G - 1);
+        const uint4 x0 = reinterpret_cast<const uint4 *>(xl)[gc * 2], x1 = reinterpret_cast<const uint4 *>(xl)[gc * 2 + 1];
+        const uint32_t xc[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float xs_g = xsl[gc];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          // group h of the lane's 48 bytes: its 16 low-nibble bytes and 8 bytes of top bits
+          const uint4 q0 = wr[i][u][0], q1 = wr[i][u][1], q2 = wr[i][u][2];
+          uint32_t L[4], T0, T1;
+          if (h == 0) {
+            L[0] = q0.x; L[1] = q0.y; L[2] = q0.z; L[3] = q0.w; T0 = q1.x; T1 = q1.y;
+          } else {
+            L[0] = q1.z; L[1] = q1.w; L[2] = q2.x; L[3] = q2.y; T0 = q2.z; T1 = q2.w;
+          }
+          uint32_t wv[8];
+          six_widen(L, T0, T1, wv);
+          int32_t S = 0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) S = dot4(wv[j], xc[j], S);
+          if (g < G) {
+            const float p = (float)S * (wsl[i * G16 + g] * xs_g);
+            float *pi = P + i * lay.stride;
+            if (g < G4) pi[(g & 3) * lay.q + (g >> 2)] = p;
+            else pi[4 * lay.q + (g - G4)] = p;
+          }
+        }
+      }
+    }
+  }
+  wave_sync_lds();
+  float chain = 0.0f;  // lane 4i + k: accumulator k of row row0 + i
+  if (lane < 4 * R) chain = lds_chain(P + (lane >> 2) * lay.stride + (lane & 3) * lay.q, G4 / 4, 0.0f);
+  const int src = (lane < R ? lane : 0) * 4;
+  const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
+  const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
+  if (lane < R && row0 + lane < a.total_rows) {
+    float sum = ((c0 + c1) + c2) + c3;
+    const float *tl = P + lane * lay.stride + 4 * lay.q;
+    for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
+    const RowAt at = row_at(a, row0 + lane);
+    float *y = at.y + at.r;
+    *y = at.accumulate ? *y + sum : sum;
+  }
+}
+
+template <int R, int NS>
+hipError_t launch_gemv6(const MatArgs &a, hipStream_t s) {
+  const int waves = (a.total_rows + R - 1) / R;
+  const int blocks = (waves + WAVES - 1) / WAVES;
+  const size_t g16 = ((a.k / GS) + 3) & ~3;
+  const size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
+                     sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
+  hipLaunchKernelGGL((gemv6_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode6(const MatArgs &a, hipStream_t s) {
+  const int steps = (a.k / GS + 127) / 128;  // 3 KiB steps of a row
+  if (steps <= 1) return launch_gemv6<4, 1>(a, s);
+  if (steps <= 2) return launch_gemv6<2, 2>(a, s);
+  if (steps <= 4) return launch_gemv6<1, 4>(a, s);
+  if (steps <= 6) return launch_gemv6<1, 6>(a, s);
+  return hipErrorInvalidValue;
+}
+
 template <int R, int NS>
 hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const int waves = (a.total_rows + R - 1) / R;
@@ -373,6 +518,7 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
   if (!sums && !six && relaxed && a.m == 1 && a.k <= 20 * 1024) return launch_decode(a, s);
+  if (!sums && six && relaxed && a.m == 1 && a.k <= 24 * 1024 && (a.k / GS) % 2 == 0) return launch_decode6(a, s);
   if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;
   if (six) {
     if (relaxed) return sums ? launch_sel<true, true, true>(a, s) : launch_sel<true, true, false>(a, s);

@@ -56,6 +56,16 @@ def test_gemv_bits(k, rows, m, bias, six):
     assert np.array_equal(sums, ol.group_sums(xq, w, rows, k, bias, six))
 
 
+@pytest.mark.parametrize("k", [64, 192, 640, 3584, 18944])
+@pytest.mark.parametrize("rows", [37, 130])
+def test_int6_decode_bits(k, rows):
+    """one token against int6 rows of an even number of groups: the int6 decode path (two groups a lane), tails of
+    0 and 2 groups, the Qwen2.5-7B widths"""
+    w, ws = weights(rows, k, 1)
+    xq, xs = activations(1, k, 64)
+    assert same_bits(gl.matmul(xq, xs, w, ws, rows, k, 64, 1), ol.matmul(xq, xs, w, ws, rows, k, 64, 1))
+
+
 GEMM_CASES = [(k, rows, m) for k in (32, 96, 288, 1056, 4096) for rows, m in ((37, 9), (64, 130), (130, 200))]
 
 
