@@ -321,8 +321,15 @@ double matmul_bytes(const he_engine *e, const MatSeg *segs, int nseg, int32_t k,
   return b;
 }
 
+// the float32 source of a one-token matmul's activations, quantized in the launch (after rmsnorm with weights norm
+// where norm is not null): MatArgs.xf
+struct F32Source {
+  const float *x;
+  const float *norm;
+};
+
 hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
-                         const float *xs) {
+                         const float *xs, const F32Source *f32 = nullptr) {
   const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
   const int32_t step = gemv_tokens(k, e->c.relaxed);
   if (step < 1) return hipErrorInvalidValue;
@@ -342,6 +349,11 @@ hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, 
     a.k = k;
     a.m = std::min(step, m - t0);
     a.sums = nullptr;
+    if (f32) {
+      a.xf = f32->x;
+      a.xnorm = f32->norm;
+      a.eps = e->c.rms_norm_eps;
+    }
     hipError_t err = launch_gemv(a, e->c.six, e->c.relaxed, e->stream);
     if (err != hipSuccess) return err;
   }
@@ -370,12 +382,19 @@ hipError_t gemm_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, in
   return launch_gemm(a, e->c.six, e->c.relaxed, e->stream);
 }
 
-hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs) {
+hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs,
+                  const F32Source *f32 = nullptr) {
   if (use_gemm(e, k, m))
     return timed(e, HE_K_GEMM, matmul_bytes(e, segs, nseg, k, m),
                  [&] { return gemm_launch(e, segs, nseg, k, m, xq, xs); });
   return timed(e, HE_K_GEMV, matmul_bytes(e, segs, nseg, k, m),
-               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs); });
+               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, f32); });
+}
+
+// one token whose rows of k the decode GEMV quantizes (and normalizes) itself: it saves a launch where the GEMV is
+// about one block a CU (q/k/v, wo), and would cost more than it saves on the larger ones (each block repeats it)
+bool quantizes_itself(const he_engine *e, int32_t k, int32_t m, int32_t rows) {
+  return m == 1 && rows <= 8192 && decode_takes_f32(k, e->c.six != 0, e->c.relaxed != 0);
 }
 
 int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, bool need_logits) {
@@ -390,15 +409,20 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
                         c.six ? 32 : group_size(dim), c.six, s);
   }));
   for (int32_t l = 0; l < c.n_layers; ++l) {
-    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim, W,
-                                  W / 32, 0, c.rms_norm_eps, e->bias, s);
-    }));
     const MatSeg qkv[3] = {
         {e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), e->q, qdim, qdim, 0},
         {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), e->k, kvdim, kvdim, 0},
         {e->mat(HE_T_WV, l), e->mat_scales(HE_T_WV, l), e->v, kvdim, kvdim, 0}};
-    HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
+    if (quantizes_itself(e, dim, m, qdim + 2 * kvdim)) {
+      const F32Source src{e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim)};
+      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, &src));
+    } else {
+      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
+                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+      }));
+      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
+    }
     QkvPost qp{};
     qp.q = e->q;
     qp.k = e->k;
@@ -440,10 +464,15 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     for (int32_t t = 0; t < m; ++t) kv_rows += pos0 + t + 1;
     HIP_TRY(timed(e, HE_K_ATTENTION, kv_rows * 2 * kvdim * esz + (double)m * qdim * 8,
                   [&] { return launch_attention(at, s); }));
-    HIP_TRY(timed(e, HE_K_NORM, (double)m * qdim * (4 + 1 + 0.125),
-                  [&] { return launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s); }));
     const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
-    HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
+    if (quantizes_itself(e, qdim, m, dim)) {
+      const F32Source src{e->xb, nullptr};
+      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs, &src));
+    } else {
+      HIP_TRY(timed(e, HE_K_NORM, (double)m * qdim * (4 + 1 + 0.125),
+                    [&] { return launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s); }));
+      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
+    }
     HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
       return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
                                   W / 32, 0, c.rms_norm_eps, e->bias, s);

@@ -12,6 +12,8 @@
 // the whole row go to LDS, laid out so that the lane holding accumulator k of token t reads its groups in order.
 #pragma clang fp contract(off)
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -198,12 +200,57 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   }
 }
 
+// The activations of a decode launch from the float32 token instead of quantize_x's output, in the block itself (no
+// launch of their own): with a.xnorm, rmsnorm first (kernels/kernel.ts:330-342: the squares in four lanes j % 4 added
+// in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
+// out = w * (s * x)), then quantize_x with bias 64 (kernels/kernel.ts:129-156) a half-wave a group, stored centred
+// (q - 64) into xl with the group scales into xsl. Every block computes the same bits. Thread tid takes positions
+// tid + 256 u (group tid / 32 + 8 u), all requested at once. MAXU * 256 >= K; sq: 4 * (K / 4 + 3 & ~3) floats of LDS.
+template <int MAXU>
+__device__ __forceinline__ void stage_from_f32(const MatArgs &a, uint8_t *xl, float *xsl, float *sq) {
+  __shared__ float part[4], sval;
+  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = (q4 + 3) & ~3;
+  float xv[MAXU], wv[MAXU];
+#pragma unroll
+  for (int u = 0; u < MAXU; ++u) {
+    const int j = min(tid + 256 * u, K - 1);  // clamped: every load unconditional
+    xv[u] = a.xf[j];
+    wv[u] = a.xnorm ? a.xnorm[j] : 1.0f;
+  }
+  float sc = 1.0f;
+  if (a.xnorm) {
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+      const int j = tid + 256 * u;
+      if (j < K) sq[(j & 3) * qs + (j >> 2)] = xv[u] * xv[u];
+    }
+    __syncthreads();
+    if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
+    __syncthreads();
+    if (tid == 0) sval = 1.0f / __builtin_sqrtf((((part[0] + part[1]) + part[2]) + part[3]) / (float)K + a.eps);
+    __syncthreads();
+    sc = sval;
+  }
+#pragma unroll
+  for (int u = 0; u < MAXU; ++u) {
+    const int j = tid + 256 * u;
+    if (j - (tid & 31) < K) {  // whole half-waves (K is a multiple of 32)
+      const float o = a.xnorm ? wv[u] * (sc * xv[u]) : xv[u];
+      const float amax = wave_max32(__builtin_fabsf(o));
+      const float scale = amax / 63.0f;
+      const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+      xl[j] = (uint8_t)(quant_value(o, inv, 64) - 64);
+      if ((tid & 31) == 0) xsl[j >> 5] = scale;
+    }
+  }
+}
+
 // The decode path proper (one token, int8, bias 64): a wave takes R consecutive rows (about 16 KiB of weights) and
 // requests all of them with their scales before anything else (a scheduling barrier keeps the compiler from sinking
 // the loads next to their uses); meanwhile the block stages the token's activations, centred, and their scales in
 // LDS once. The R rows' products go to LDS and 4R lanes add them in the reference's order at once.
 // NS: wave steps (1 KiB of a row), NS * 1024 >= K.
-template <int R, int NS>
+template <int R, int NS, bool F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv1_kernel(const MatArgs a) {
   constexpr int SV = (NS * 32 + 255) / 256;  // float4 of a row's scales a lane
   extern __shared__ float smem[];
@@ -245,8 +292,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  // the block's activations: K / 16 uint4, up to NS * 4 a thread
-  {
+  // the block's activations: K / 16 uint4, up to NS * 4 a thread (or made here from the float32 token)
+  if constexpr (F32) {
+    static_assert(NS <= 4, "the float32 token is held a thread at a time");
+    stage_from_f32<NS * 4>(a, reinterpret_cast<uint8_t *>(xl), xsl, P - wave * R * lay.stride);
+  } else {
     constexpr int XL = (NS * 1024 / 16 + 255) / 256;
     uint4 xv[XL];
     float sv[(NS * 32 + 255) / 256];
@@ -463,12 +513,21 @@ hipError_t launch_decode6(const MatArgs &a, hipStream_t s) {
 
 template <int R, int NS>
 hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
+  if (a.xf && (NS > 4 || a.k % 32)) return hipErrorInvalidValue;
   const int waves = (a.total_rows + R - 1) / R;
   const int blocks = (waves + WAVES - 1) / WAVES;
   const size_t g16 = ((a.k / GS) + 3) & ~3;
-  const size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
-                     sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
-  hipLaunchKernelGGL((gemv1_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+  const size_t head = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R);
+  size_t products = sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
+  if (a.xf) products = std::max(products, sizeof(float) * 4 * (size_t)(((a.k / 4) + 3) & ~3));  // the squares
+  const size_t lds = head + products;
+  if constexpr (NS <= 4) {
+    if (a.xf) {
+      hipLaunchKernelGGL((gemv1_kernel<R, NS, true>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((gemv1_kernel<R, NS, false>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
 }
 
@@ -515,8 +574,11 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
   return m < 1 ? 0 : (m > 8 ? 8 : m);
 }
 
+bool decode_takes_f32(int32_t k, bool six, bool relaxed) { return !six && relaxed && k <= 4 * 1024 && k % 32 == 0; }
+
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
+  if (a.xf && (sums || a.m != 1 || !decode_takes_f32(a.k, six, relaxed))) return hipErrorInvalidValue;
   if (!sums && !six && relaxed && a.m == 1 && a.k <= 20 * 1024) return launch_decode(a, s);
   if (!sums && six && relaxed && a.m == 1 && a.k <= 24 * 1024 && (a.k / GS) % 2 == 0) return launch_decode6(a, s);
   if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;

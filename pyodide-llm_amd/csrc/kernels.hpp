@@ -30,6 +30,11 @@ struct MatArgs {
   int32_t k;
   int32_t m;
   int32_t *sums;  // group-sum output (hk_group_sums) or null
+  // one token (the decode path, decode_takes_f32): the float32 token instead of xq / xs, quantized in the launch,
+  // after rmsnorm with weights xnorm (and eps) where xnorm is not null
+  const float *xf;
+  const float *xnorm;
+  float eps;
 };
 
 // the most tokens the engine gives one GEMV pass: more go to the MFMA GEMM where it takes them
@@ -37,6 +42,8 @@ constexpr int32_t GEMV_MOST = 8;
 
 // decode GEMV, m <= 8 tokens: exact int32 group sums, the reference's float32 order
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
+// whether a one-token launch_gemv of rows of k takes its activations as float32 (MatArgs.xf)
+bool decode_takes_f32(int32_t k, bool six, bool relaxed);
 // the most tokens one launch_gemv takes for rows of k (its products of a row fit the block's LDS)
 int32_t gemv_tokens(int32_t k, bool relaxed);
 // prefill GEMM on i8 MFMA, any m (bias 64, int8 or int6): the same bits as launch_gemv per (token, row); with
