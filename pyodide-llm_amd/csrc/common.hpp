@@ -126,9 +126,20 @@ __device__ __forceinline__ float from_f16(uint16_t h) {
 
 // ---- wave helpers (wave64) ----
 
-__device__ __forceinline__ float wave_max32(float v) {  // over each half of the wave (32 lanes)
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m, 64));
+// lane i ^ 1 (DPP quad_perm [1, 0, 3, 2]): a VALU operand, not a trip through the LDS unit as __shfl_xor is
+__device__ __forceinline__ float dpp_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ int32_t dpp_xor1(int32_t v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true); }
+
+// the largest over each half of the wave (32 lanes), order-free: xor 1 and xor 2 within quads, the mirrors within
+// 8 and 16 lanes (DPP), then xor 16 (ds_swizzle); fmax ignores a NaN beside a number, as before
+__device__ __forceinline__ float wave_max32(float v) {
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
   return v;
 }
 

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
         }
         if constexpr (!SIX) {
 #pragma unroll
-          for (int k = 0; k < (RELAXED ? 1 : 4); ++k) S[t][k] += __shfl_xor(S[t][k], 1, 64);
+          for (int k = 0; k < (RELAXED ? 1 : 4); ++k) S[t][k] += dpp_xor1(S[t][k]);
         }
       }
       if (!(holder && active)) continue;
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       int32_t S = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) S = dot4(wr[i][u][j], xc[j], S);
-      S += __shfl_xor(S, 1, 64);
+      S += dpp_xor1(S);
       if (holder && g < G) {
         const float p = (float)S * (wsl[i * G16 + g] * xs_g);
         float *pi = P + i * lay.stride;
