@@ -143,35 +143,48 @@ __device__ __forceinline__ float wave_max32(float v) {
   return v;
 }
 
-// acc + c[0] + c[1] + ... + c[n-1] in order (every add rounded), the values read from LDS 32 at a time with the
-// next 32 already requested: c 16-byte aligned. The dependent adds run back to back instead of waiting on each load.
+__device__ __forceinline__ float add32(float acc, const float4 v[8]) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    acc = acc + v[u].x;
+    acc = acc + v[u].y;
+    acc = acc + v[u].z;
+    acc = acc + v[u].w;
+  }
+  return acc;
+}
+
+// acc + c[0] + c[1] + ... + c[n-1] in order (every add rounded), the values read from LDS 32 at a time into two sets
+// of registers in turn: the next 32 are requested before this 32's adds (the scheduling barriers keep the compiler
+// from sinking the loads among the adds), so the dependent adds run back to back instead of waiting on the LDS.
+// c 16-byte aligned.
 __device__ __forceinline__ float lds_chain(const float *c, int n, float acc) {
   const float4 *c4 = reinterpret_cast<const float4 *>(c);
   const int n4 = n >> 2;
   int i = 0;
   if (n4 >= 8) {
-    float4 cur[8];
+    float4 a[8], b[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) cur[u] = c4[u];
-    for (i = 8; i + 8 <= n4; i += 8) {
-      float4 nxt[8];
+    for (int u = 0; u < 8; ++u) a[u] = c4[u];
+    for (i = 8; i + 16 <= n4; i += 16) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) nxt[u] = c4[i + u];
+      for (int u = 0; u < 8; ++u) b[u] = c4[i + u];
+      __builtin_amdgcn_sched_barrier(0);
+      acc = add32(acc, a);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        acc = acc + cur[u].x;
-        acc = acc + cur[u].y;
-        acc = acc + cur[u].z;
-        acc = acc + cur[u].w;
-        cur[u] = nxt[u];
-      }
+      for (int u = 0; u < 8; ++u) a[u] = c4[i + 8 + u];
+      __builtin_amdgcn_sched_barrier(0);
+      acc = add32(acc, b);
     }
+    if (i + 8 <= n4) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      acc = acc + cur[u].x;
-      acc = acc + cur[u].y;
-      acc = acc + cur[u].z;
-      acc = acc + cur[u].w;
+      for (int u = 0; u < 8; ++u) b[u] = c4[i + u];
+      __builtin_amdgcn_sched_barrier(0);
+      acc = add32(acc, a);
+      acc = add32(acc, b);
+      i += 8;
+    } else {
+      acc = add32(acc, a);
     }
   }
   for (; i < n4; ++i) {

@@ -391,8 +391,9 @@ hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t
                [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, f32); });
 }
 
-// one token whose rows of k the decode GEMV quantizes (and normalizes) itself: it saves a launch where the GEMV is
-// about one block a CU (q/k/v, wo), and would cost more than it saves on the larger ones (each block repeats it)
+// one token whose rows of k the decode GEMV quantizes itself: it saves a launch where the GEMV is about one block a
+// CU (wo), and would cost more than it saves on the larger ones (each block repeats it). (Measured: rmsnorm in the
+// q/k/v GEMV's blocks costs as much as its own launch, which is latency inside the norm, not the launch.)
 bool quantizes_itself(const he_engine *e, int32_t k, int32_t m, int32_t rows) {
   return m == 1 && rows <= 8192 && decode_takes_f32(k, e->c.six != 0, e->c.relaxed != 0);
 }
@@ -413,16 +414,11 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
         {e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), e->q, qdim, qdim, 0},
         {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), e->k, kvdim, kvdim, 0},
         {e->mat(HE_T_WV, l), e->mat_scales(HE_T_WV, l), e->v, kvdim, kvdim, 0}};
-    if (quantizes_itself(e, dim, m, qdim + 2 * kvdim)) {
-      const F32Source src{e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim)};
-      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, &src));
-    } else {
-      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
-                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s);
-      }));
-      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
-    }
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
+                                  W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
+    HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
     QkvPost qp{};
     qp.q = e->q;
     qp.k = e->k;
