@@ -90,7 +90,9 @@ __global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *
   const float s = sval;
   int8_t *q = xq + (int64_t)t * xq_stride;
   float *sc = xs + (int64_t)t * xs_stride;
-  for (int g = tid >> 5; g < n / GS; g += 32) {
+  // this block's share of the groups: gridDim.y blocks of a token each run the (short) sums themselves and quantize
+  // every gridDim.y-th group, so that no one CU does all the divisions
+  for (int g = (tid >> 5) * gridDim.y + blockIdx.y; g < n / GS; g += 32 * gridDim.y) {
     const int j = g * GS + (tid & 31);
     const float o = wv[j] * (s * xv[j]);
     if (out) out[(int64_t)t * out_stride + j] = o;
@@ -308,8 +310,10 @@ hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s) {
   const size_t lds = sizeof(float) * (size_t)(3 * n + 16);
-  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m), dim3(1024), lds, s, xq, xs, out, x, w, n, x_stride, xq_stride,
-                     xs_stride, out_stride, eps, bias);
+  // one token: 4 blocks share its groups (more tokens fill the chip by themselves)
+  const int split = m < 64 ? 4 : 1;
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m, split), dim3(1024), lds, s, xq, xs, out, x, w, n, x_stride,
+                     xq_stride, xs_stride, out_stride, eps, bias);
   return hipGetLastError();
 }
 
