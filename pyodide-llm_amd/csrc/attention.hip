@@ -246,7 +246,6 @@ template <int HS, bool HALF>
 __global__ __launch_bounds__(256) void pv_ring_kernel(const AttnArgs a) {
   __shared__ float ring[NSLOT * SLOT];
   __shared__ int filled[NSLOT], used;
-  __shared__ float tail_p[MAXMUL][4], tail_v[4][PVJ];  // the positions past the fours (at most 3)
   const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int count = a.pos0 + t + 1, count4 = count & ~3;
@@ -257,36 +256,39 @@ __global__ __launch_bounds__(256) void pv_ring_kernel(const AttnArgs a) {
 
   if (tid < NSLOT) filled[tid] = 0;
   if (tid == NSLOT) used = 0;
-  if (wave == 1) {  // the positions past the fours, weights and values, into LDS
-    if (lane < MAXMUL * 4) {
-      const int hl = min(lane >> 2, mul - 1), r = lane & 3;
-      tail_p[lane >> 2][r] = weights[(int64_t)hl * a.seq_len + min(count4 + r, count - 1)];
-    } else if (lane < MAXMUL * 4 + 4 * PVJ) {
-      const int i = lane - MAXMUL * 4, r = i / PVJ, j = i % PVJ;
-      tail_v[r][j] = cache1<HALF>(a.vcache, (int64_t)min(count4 + r, count - 1) * kvdim + vbase + j);
+  // wave 0, lane hl * 8 + j: the weights and values of the positions past the fours (at most 3), requested now and
+  // used at the end
+  float tp[3], tv[3];
+  if (wave == 0) {
+    const int hl = min(lane / PVJ, mul - 1), j = lane % PVJ;
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      const int p = min(count4 + r, count - 1);
+      tp[r] = weights[(int64_t)hl * a.seq_len + p];
+      tv[r] = cache1<HALF>(a.vcache, (int64_t)p * kvdim + vbase + j);
     }
   }
-  __syncthreads();
 
   float acc = 0.0f;  // wave 0, lane hl * 8 + j
+  // lane = the four-position block b of the chunk: its 4 value rows (8 columns) and every head's 4 weights; a
+  // producer's first chunk is requested before the block's barrier
+  float4 va[8], vn[8], pa[MAXMUL], pn[MAXMUL];
+  auto fetch = [&](int c, float4 *v, float4 *pw) {
+    const int p = min(c * RP + 4 * lane, count4 - 4);  // clamped: never added past count4
+    const int64_t at = (int64_t)p * kvdim + vbase;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v[2 * r] = cache4<HALF>(a.vcache, at + r * kvdim);
+      v[2 * r + 1] = cache4<HALF>(a.vcache, at + r * kvdim + 4);
+    }
+#pragma unroll
+    for (int hl = 0; hl < MAXMUL; ++hl)
+      pw[hl] = *reinterpret_cast<const float4 *>(weights + (int64_t)min(hl, mul - 1) * a.seq_len + p);
+  };
+  if (wave > 0 && wave - 1 < chunks) fetch(wave - 1, va, pa);
+  __syncthreads();
   if (wave > 0) {
-    // lane = the four-position block b of the chunk: its 4 value rows (8 columns) and every head's 4 weights
-    float4 va[8], vn[8], pa[MAXMUL], pn[MAXMUL];
-    auto fetch = [&](int c, float4 *v, float4 *pw) {
-      const int p = min(c * RP + 4 * lane, count4 - 4);  // clamped: never added past count4
-      const int64_t at = (int64_t)p * kvdim + vbase;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        v[2 * r] = cache4<HALF>(a.vcache, at + r * kvdim);
-        v[2 * r + 1] = cache4<HALF>(a.vcache, at + r * kvdim + 4);
-      }
-#pragma unroll
-      for (int hl = 0; hl < MAXMUL; ++hl)
-        pw[hl] = *reinterpret_cast<const float4 *>(weights + (int64_t)min(hl, mul - 1) * a.seq_len + p);
-    };
-    int c = wave - 1;
-    if (c < chunks) fetch(c, va, pa);
-    for (; c < chunks; c += NPROD) {
+    for (int c = wave - 1; c < chunks; c += NPROD) {
       if (c + NPROD < chunks) fetch(c + NPROD, vn, pn);  // the wave's next chunk flies meanwhile
       wait_at_least(&used, c - NSLOT + 1);                // the slot's last chunk has been added
       float *slot = ring + (c % NSLOT) * SLOT;
@@ -324,7 +326,9 @@ __global__ __launch_bounds__(256) void pv_ring_kernel(const AttnArgs a) {
     }
     if (lane < mul * PVJ) {
       const int hl = lane / PVJ, j = lane % PVJ;
-      for (int i = 0; i < count - count4; ++i) acc = acc + tail_p[hl][i] * tail_v[i][j];
+#pragma unroll
+      for (int r = 0; r < 3; ++r)
+        if (r < count - count4) acc = acc + tp[r] * tv[r];
       a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
     }
   }
