@@ -8,10 +8,12 @@
 //           the fours one at a time, out = out + p v.
 // Three launches: (A) the scores of 64-position tiles, every CU streaming keys once for the nh / nkv query heads
 // that share them, with each tile's maxima; (B) one block a (token, head): the exponentials, their ordered sum from
-// LDS, the weights; (C) one block a (token, kv head, 8 of the head's columns): 512-position chunks of values and
-// weights staged in LDS (the next chunk's loads in flight while this one is used), the four-position products, and
-// the ordered sums over the blocks, one thread a (head, column).
+// LDS, the weights p written over the scores; (C) the weighted values: for a few tokens (decode) a ring of LDS slots
+// that producer waves fill with the four-position products ahead of the wave that runs the ordered sums; for a prompt
+// block, blocks of tokens that share the values they stage, a thread a (token, head, column) sum.
 #pragma clang fp contract(off)
+
+#include <algorithm>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -23,7 +25,6 @@ namespace {
 constexpr int TILE = 64;   // positions a block of (A)
 constexpr int MAXMUL = 8;  // query heads a kv head at most
 constexpr int PVJ = 8;     // columns a block of (C)
-constexpr int CH = 512;    // positions a chunk of (C)
 constexpr int RING_TOKENS = 8;  // up to this many tokens the weighted values run on the ring kernel (below)
 
 template <bool HALF>
@@ -150,76 +151,89 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   }
 }
 
-// (C) grid (hs / PVJ, nkv, m), block 256: the weighted values of columns j0..j0+7 of the nh / nkv heads of kv head kh
+// (C) for many tokens (a prompt block): one block of 256 threads a (kv head, 32 of its columns (16 where hs is not a
+// multiple of 32), 256 / (columns * mul) tokens), a thread a (token, head, column) whose ordered sum over the
+// four-position blocks it runs itself: out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) from LDS, where 128-position
+// chunks of the values (transposed: a column's positions side by side) and of the weights are staged, the next
+// chunk's loads in flight meanwhile. The block's tokens share every value they read; each stops at its own last four.
+constexpr int TPC = 128;  // positions a chunk
+
 template <int HS, bool HALF>
-__global__ __launch_bounds__(256) void pv_kernel(const AttnArgs a) {
-  constexpr int NB = CH / 4;  // four-position blocks a chunk
-  constexpr int PS = CH + 4, BS = NB + 4;   // padded rows: heads and columns fall on different LDS banks
-  __shared__ float vs[CH * PVJ];            // [position][column]
-  __shared__ float ps[MAXMUL * PS];         // [head][position]
-  __shared__ float bs[MAXMUL * PVJ * BS];   // [head][column][block]
-  const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+__global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
+  constexpr int COLS = HS % 32 == 0 ? 32 : 16;   // columns a block
+  constexpr int ROWS = 256 / COLS;               // (token, head) weight rows a block at most
+  constexpr int TVS = TPC + 4;                   // LDS row of a column's values (16 lanes' float4 on distinct banks)
+  constexpr int VPT = TPC * (COLS / 4) / 256;    // float4 of values a thread a chunk
+  constexpr int WPT = ROWS * (TPC / 4) / 256;    // float4 of weights a thread a chunk
+  __shared__ float vs[2][COLS * TVS];  // [column][position]
+  __shared__ float ps[2][ROWS * TPC];  // [token * mul + head][position]
+  const int tid = threadIdx.x, kh = blockIdx.y;
+  const int mul = a.nh / a.nkv, tt_n = max(1, ROWS / mul);
+  const int j0 = blockIdx.x * COLS, t0 = blockIdx.z * tt_n;
+  const int kvdim = a.nkv * HS;
+  const int j = tid % COLS, hl = (tid / COLS) % mul, tt = tid / (COLS * mul);
+  const bool chain = tt < tt_n && t0 + tt < a.m;
+  const int t = min(t0 + tt, a.m - 1);
   const int count = a.pos0 + t + 1, count4 = count & ~3;
-  const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
-  const float *scores = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
-  const int chains = mul * PVJ;
-  const int hl_me = tid / PVJ, j_me = tid % PVJ;
-  float acc = 0.0f;
-  // per chunk: CH * PVJ / 4 float4 of values (4 a thread) and mul * CH / 4 float4 of weights (<= 4 a thread)
-  static_assert(CH * PVJ / 4 == 4 * 256 && MAXMUL * CH / 4 <= 4 * 256, "the chunk's loads are four a thread");
-  // a chunk's loads from clamped addresses, unconditional (the values past count4 are never used), written out four
-  // times over so that every register stays a register (an indexed array went to scratch memory)
-  auto vload = [&](int c0, int u) {
-    const int i = tid + u * 256;
-    const int p = min(c0 + (i >> 1), count4 - 1);
-    return cache4<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + 4 * (i & 1));
-  };
-  auto pload = [&](int c0, int u) {
-    const int i = tid + u * 256;
-    const int hl = min(i / (CH / 4), mul - 1), p = min(c0 + 4 * (i % (CH / 4)), count4 - 4);
-    return *reinterpret_cast<const float4 *>(scores + (int64_t)hl * a.seq_len + p);
-  };
-  float4 v0, v1, v2, v3, q0, q1, q2, q3;
-#define PV_FETCH(c0_)                                                                           \
-  do {                                                                                          \
-    v0 = vload((c0_), 0); v1 = vload((c0_), 1); v2 = vload((c0_), 2); v3 = vload((c0_), 3);     \
-    q0 = pload((c0_), 0); q1 = pload((c0_), 1); q2 = pload((c0_), 2); q3 = pload((c0_), 3);     \
+  const int last = min(t0 + tt_n, a.m) - 1;  // the block's last token reads the most positions
+  const int most4 = (a.pos0 + last + 1) & ~3;
+  const int chunks = (most4 + TPC - 1) / TPC;
+  const int rows = (last - t0 + 1) * mul;  // weight rows of the block
+  float4 v[VPT], w[WPT];
+  // a chunk's loads, from clamped addresses (unconditional; what lies past a token's count4 is never added), and their
+  // stores into LDS: written out as macros, so that v and w stay in registers
+#define PVT_FETCH(c_)                                                                                             \
+  do {                                                                                                            \
+    _Pragma("unroll") for (int u = 0; u < VPT; ++u) {                                                             \
+      const int i = tid + 256 * u, pos = min((c_) * TPC + i / (COLS / 4), most4 - 1), q = i % (COLS / 4);        \
+      v[u] = cache4<HALF>(a.vcache, (int64_t)pos * kvdim + kh * HS + j0 + 4 * q);                                 \
+    }                                                                                                             \
+    _Pragma("unroll") for (int u = 0; u < WPT; ++u) {                                                             \
+      const int i = tid + 256 * u;                                                                                \
+      const int r = min(i / (TPC / 4), rows - 1), pos = min((c_) * TPC + 4 * (i % (TPC / 4)), most4 - 4);       \
+      w[u] = *reinterpret_cast<const float4 *>(a.scores + ((int64_t)(t0 + r / mul) * a.nh + kh * mul + r % mul) * \
+                                                              a.seq_len + pos);                                   \
+    }                                                                                                             \
   } while (0)
-  if (count4 > 0) PV_FETCH(0);
-  for (int c0 = 0; c0 < count4; c0 += CH) {
-    const int nb = min(CH, count4 - c0) >> 2;
-    reinterpret_cast<float4 *>(vs)[tid] = v0;
-    reinterpret_cast<float4 *>(vs)[tid + 256] = v1;
-    reinterpret_cast<float4 *>(vs)[tid + 512] = v2;
-    reinterpret_cast<float4 *>(vs)[tid + 768] = v3;
-    auto pstore = [&](int u, float4 v) {
-      const int i = tid + u * 256;
-      if (i < mul * CH / 4) reinterpret_cast<float4 *>(ps + (i / (CH / 4)) * PS)[i % (CH / 4)] = v;
-    };
-    pstore(0, q0);
-    pstore(1, q1);
-    pstore(2, q2);
-    pstore(3, q3);
-    __syncthreads();
-    if (c0 + CH < count4) PV_FETCH(c0 + CH);  // the next chunk's loads fly while this one is used
-    for (int i = tid; i < mul * PVJ * nb; i += 256) {
-      // the column fastest, then the head, then the block: a wave reads few value rows and broadcasts the weights
-      const int j = i % PVJ, hl = (i / PVJ) % mul, b = i / (PVJ * mul);
-      const float *pp = ps + hl * PS + 4 * b, *vv = vs + 4 * b * PVJ + j;
-      const float pair0 = pp[0] * vv[0] + pp[1] * vv[PVJ];
-      const float pair1 = pp[2] * vv[2 * PVJ] + pp[3] * vv[3 * PVJ];
-      bs[(hl * PVJ + j) * BS + b] = pair0 + pair1;
+#define PVT_STAGE(buf_)                                                                                           \
+  do {                                                                                                            \
+    _Pragma("unroll") for (int u = 0; u < VPT; ++u) {                                                             \
+      const int i = tid + 256 * u, pl = i / (COLS / 4), q = i % (COLS / 4);                                       \
+      float *col = vs[(buf_)] + (4 * q) * TVS + pl;                                                               \
+      col[0] = v[u].x;                                                                                            \
+      col[TVS] = v[u].y;                                                                                          \
+      col[2 * TVS] = v[u].z;                                                                                      \
+      col[3 * TVS] = v[u].w;                                                                                      \
+    }                                                                                                             \
+    _Pragma("unroll") for (int u = 0; u < WPT; ++u) {                                                             \
+      reinterpret_cast<float4 *>(ps[(buf_)])[tid + 256 * u] = w[u]; /* every row, the block's or clamped copies */ \
+    }                                                                                                             \
+  } while (0)
+  if (chunks > 0) {
+    PVT_FETCH(0);
+    PVT_STAGE(0);
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  for (int c = 0; c < chunks; ++c) {
+    PVT_FETCH(c + 1);  // the next chunk's loads fly while this one is added (after the last: clamped, unused)
+    const float *vc = vs[c & 1] + j * TVS;
+    const float *prow = ps[c & 1] + (tt * mul + hl) * TPC;
+    const int nb = chain ? max(0, min(TPC, count4 - c * TPC)) >> 2 : 0;
+    for (int b = 0; b < nb; ++b) {
+      const float4 pw = *reinterpret_cast<const float4 *>(prow + 4 * b);
+      const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * b);
+      acc = acc + ((pw.x * vv.x + pw.y * vv.y) + (pw.z * vv.z + pw.w * vv.w));
     }
-    __syncthreads();
-    if (tid < chains) acc = lds_chain(bs + (hl_me * PVJ + j_me) * BS, nb, acc);
+    PVT_STAGE((c + 1) & 1);  // the other buffer: its last readers passed the previous barrier
     __syncthreads();
   }
-#undef PV_FETCH
-  if (tid < chains) {
-    const int h = kh * mul + hl_me, j = j0 + j_me;
-    for (int p = count4; p < count; ++p)
-      acc = acc + scores[(int64_t)hl_me * a.seq_len + p] * cache1<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j);
-    a.out[(int64_t)t * a.out_stride + h * HS + j] = acc;
+#undef PVT_FETCH
+#undef PVT_STAGE
+  if (chain) {
+    const float *pt = a.scores + ((int64_t)t * a.nh + kh * mul + hl) * a.seq_len;
+    for (int p = count4; p < count; ++p) acc = acc + pt[p] * cache1<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + j);
+    a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
   }
 }
 
@@ -341,10 +355,13 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const int most4 = (a.pos0 + a.m) & ~3;
   const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
-  if (a.m <= RING_TOKENS)
+  if (a.m <= RING_TOKENS) {
     hipLaunchKernelGGL((pv_ring_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((pv_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
+  } else {
+    constexpr int COLS = HS % 32 == 0 ? 32 : 16;
+    const int tt = std::max(1, 256 / COLS / (a.nh / a.nkv));
+    hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / COLS, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 
