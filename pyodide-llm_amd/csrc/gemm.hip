@@ -10,10 +10,10 @@
 // (product of scales, convert, multiply, add) run on the VALU for every (row, token, group), so the kernel is bound by
 // the VALU, not by the MFMA pipe: one MFMA a group a tile against 64 VALU instructions.
 //
-// Tiling: a block of 256 threads (4 waves) makes 64 rows x 128 tokens. Each K step stages 4 groups (128 bytes of K:
+// Tiling: a block of 512 threads (8 waves) makes 64 rows x 128 tokens. Each K step stages 4 groups (128 bytes of K:
 // one group for each lane chain) of the block's weights, activations (centred: q - 64) and scales in LDS, double
-// buffered: the next step's global loads are in flight while the current one is computed. A wave makes 32 rows x 64
-// tokens: two MFMA tiles sharing the weights operand, 4 chains x 2 tiles x 16 accumulators a lane.
+// buffered: the next step's global loads are in flight while the current one is computed. A wave makes one 32 x 32
+// MFMA tile: 4 chains x 16 accumulators a lane, few enough registers for two waves a SIMD and no AGPR traffic.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -47,44 +47,41 @@ __device__ __forceinline__ SegRow seg_row(const MatArgs &a, int row) {
   return {a.seg[0].w, a.seg[0].ws, row};
 }
 
-// what one thread loads of a K step: one (row, group) of the weights with its scale, two (token, group)s of the
-// activations with their scales. Registers between the global load and the LDS store.
+// what one thread loads of a K step: half of one (row, group) of the weights (int8; int6: a whole group by the first
+// 256 threads) with its scale, one (token, group) of the activations with its scale. Registers between the global
+// load and the LDS store.
 template <bool SIX>
 struct Fetch {
-  uint32_t w[SIX ? 6 : 8];
+  uint32_t w[SIX ? 6 : 4];
   float wsv;
-  uint4 x[2][2];
-  float xsv[2];
+  uint4 x[2];
+  float xsv;
 };
 
 template <bool SIX, bool SUMS>
 __device__ __forceinline__ void fetch(Fetch<SIX> &f, const MatArgs &a, int r0, int t0, int g0, int G, int tid) {
-  // weights: thread tid takes row tid / 4, group tid % 4 of the step (rows and groups past the end clamped: the loads
-  // stay unconditional and valid; what they bring is never added)
-  {
-    const int row = min(r0 + (tid >> 2), a.total_rows - 1), g = min(g0 + (tid & 3), G - 1);
+  // rows, groups and tokens past the end clamped: the loads stay unconditional and valid; what they bring is never
+  // added
+  if constexpr (SIX) {
+    const int q = tid & 255, row = min(r0 + (q >> 2), a.total_rows - 1), g = min(g0 + (q & 3), G - 1);
     const SegRow s = seg_row(a, row);
-    if constexpr (SIX) {
-      const uint2 *p = reinterpret_cast<const uint2 *>(s.w + ((int64_t)s.r * G + g) * 24);
-      const uint2 l0 = p[0], l1 = p[1], tops = p[2];
-      f.w[0] = l0.x; f.w[1] = l0.y; f.w[2] = l1.x; f.w[3] = l1.y; f.w[4] = tops.x; f.w[5] = tops.y;
-    } else {
-      const uint4 *p = reinterpret_cast<const uint4 *>(s.w + ((int64_t)s.r * G + g) * 32);
-      const uint4 v0 = p[0], v1 = p[1];
-      f.w[0] = v0.x; f.w[1] = v0.y; f.w[2] = v0.z; f.w[3] = v0.w;
-      f.w[4] = v1.x; f.w[5] = v1.y; f.w[6] = v1.z; f.w[7] = v1.w;
-    }
+    const uint2 *p = reinterpret_cast<const uint2 *>(s.w + ((int64_t)s.r * G + g) * 24);
+    const uint2 l0 = p[0], l1 = p[1], tops = p[2];
+    f.w[0] = l0.x; f.w[1] = l0.y; f.w[2] = l1.x; f.w[3] = l1.y; f.w[4] = tops.x; f.w[5] = tops.y;
+    f.wsv = SUMS ? 0.0f : s.ws[(int64_t)s.r * G + g];
+  } else {
+    const int row = min(r0 + (tid >> 3), a.total_rows - 1), g = min(g0 + ((tid >> 1) & 3), G - 1);
+    const SegRow s = seg_row(a, row);
+    const uint4 v = *reinterpret_cast<const uint4 *>(s.w + ((int64_t)s.r * G + g) * 32 + (tid & 1) * 16);
+    f.w[0] = v.x; f.w[1] = v.y; f.w[2] = v.z; f.w[3] = v.w;
     f.wsv = SUMS ? 0.0f : s.ws[(int64_t)s.r * G + g];
   }
-  // activations: (token, group) pairs tid and tid + 256 of the step's 128 x 4
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int i = tid + 256 * u;
-    const int t = min(t0 + (i >> 2), a.m - 1), g = min(g0 + (i & 3), G - 1);
+  {
+    const int t = min(t0 + (tid >> 2), a.m - 1), g = min(g0 + (tid & 3), G - 1);
     const uint4 *p = reinterpret_cast<const uint4 *>(a.xq + (int64_t)t * a.xq_stride + (int64_t)g * 32);
-    f.x[u][0] = p[0];
-    f.x[u][1] = p[1];
-    f.xsv[u] = SUMS ? 0.0f : a.xs[(int64_t)t * a.xs_stride + g];
+    f.x[0] = p[0];
+    f.x[1] = p[1];
+    f.xsv = SUMS ? 0.0f : a.xs[(int64_t)t * a.xs_stride + g];
   }
 }
 
@@ -92,28 +89,28 @@ __device__ __forceinline__ uint4 centre16(uint4 v) { return {centre4(v.x), centr
 
 template <bool SIX>
 __device__ __forceinline__ void store(Stage &st, const Fetch<SIX> &f, int tid) {
-  {
-    const int row = tid >> 2, gi = tid & 3;
-    uint32_t w[8];
-    if constexpr (SIX) {
+  if constexpr (SIX) {
+    if (tid < 256) {
+      const int row = tid >> 2, gi = tid & 3;
+      uint32_t w[8];
       const uint32_t L[4] = {f.w[0], f.w[1], f.w[2], f.w[3]};
       six_widen(L, f.w[4], f.w[5], w);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) w[i] = f.w[i];
+      uint4 *d = reinterpret_cast<uint4 *>(st.a + row * ROWB + gi * 32);
+      d[0] = {w[0], w[1], w[2], w[3]};
+      d[1] = {w[4], w[5], w[6], w[7]};
+      st.ws[gi * BR + row] = f.wsv;
     }
-    uint4 *d = reinterpret_cast<uint4 *>(st.a + row * ROWB + gi * 32);
-    d[0] = {w[0], w[1], w[2], w[3]};
-    d[1] = {w[4], w[5], w[6], w[7]};
-    st.ws[gi * BR + row] = f.wsv;
+  } else {
+    const int row = tid >> 3, gi = (tid >> 1) & 3;
+    *reinterpret_cast<uint4 *>(st.a + row * ROWB + gi * 32 + (tid & 1) * 16) = {f.w[0], f.w[1], f.w[2], f.w[3]};
+    if ((tid & 1) == 0) st.ws[gi * BR + row] = f.wsv;
   }
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int i = tid + 256 * u, tok = i >> 2, gi = i & 3;
+  {
+    const int tok = tid >> 2, gi = tid & 3;
     uint4 *d = reinterpret_cast<uint4 *>(st.b + tok * ROWB + gi * 32);
-    d[0] = centre16(f.x[u][0]);
-    d[1] = centre16(f.x[u][1]);
-    st.xs[gi * BT + tok] = f.xsv[u];
+    d[0] = centre16(f.x[0]);
+    d[1] = centre16(f.x[1]);
+    st.xs[gi * BT + tok] = f.xsv;
   }
 }
 
@@ -143,28 +140,26 @@ __device__ __forceinline__ void write_sums(const MatArgs &a, const v16i &S, int 
 
 // with SUMS the kernel writes the exact int32 group sums S_g to a.sums [m][rows][G] instead (one segment)
 template <bool SIX, bool SUMS>
-__global__ __launch_bounds__(256) void gemm_kernel(const MatArgs a) {
+__global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
   __shared__ Stage stage[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave & 1, wt = wave >> 1;  // the wave's 32 rows and 64 tokens of the block
+  const int wr = wave & 1, wt = wave >> 1;  // the wave's 32 rows and 32 tokens of the block
   const int r0 = blockIdx.x * BR, t0 = blockIdx.y * BT;
   const int G = a.k / 32, G4 = G & ~3, steps = G4 / KS, tail = G - G4;
 
-  float acc[KS][2][16];
+  float acc[KS][16];
 #pragma unroll
   for (int c = 0; c < KS; ++c)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[c][j][v] = 0.0f;
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
   const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-  // the operands of this lane in a stage: weights row wr*32 + lane%32, activations tokens wt*64 + j*32 + lane%32,
-  // 16 bytes of each group at (lane / 32) * 16 (A and B take the same k bytes, so the sum is the group's)
+  // the operands of this lane in a stage: weights row wr*32 + lane%32, activations token wt*32 + lane%32, 16 bytes
+  // of each group at (lane / 32) * 16 (A and B take the same k bytes, so the sum is the group's)
   const int a_off = (wr * 32 + (lane & 31)) * ROWB + (lane >> 5) * 16;
-  const int b_off = (wt * 64 + (lane & 31)) * ROWB + (lane >> 5) * 16;
+  const int b_off = (wt * 32 + (lane & 31)) * ROWB + (lane >> 5) * 16;
   const int ws_off = wr * 32 + (lane >> 5) * 4;
-  const int xs_off = wt * 64 + (lane & 31);
+  const int xs_off = wt * 32 + (lane & 31);
 
   Fetch<SIX> f;
   const int total = steps + (tail ? 1 : 0);
@@ -179,18 +174,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(const MatArgs a) {
 #pragma unroll
     for (int gi = 0; gi < KS; ++gi) {
       const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
+      const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
+      const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+      if constexpr (SUMS) {
+        write_sums(a, S, r0 + wr * 32, t0 + wt * 32, s * KS + gi, G, lane);
+      } else {
+        float p[16];
+        products(S, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + j * 32 * ROWB + gi * 32);
-        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-        if constexpr (SUMS) {
-          write_sums(a, S, r0 + wr * 32, t0 + wt * 64 + j * 32, s * KS + gi, G, lane);
-        } else {
-          float p[16];
-          products(S, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off + j * 32], p);
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[gi][j][v] = acc[gi][j][v] + p[v];
-        }
+        for (int v = 0; v < 16; ++v) acc[gi][v] = acc[gi][v] + p[v];
       }
     }
     if (s + 1 < total) store<SIX>(stage[(s + 1) & 1], f, tid);
@@ -198,29 +190,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(const MatArgs a) {
   }
 
   // ((l0 + l1) + l2) + l3, then the tail groups in order
-  float out[2][16];
+  float out[16];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) out[j][v] = ((acc[0][j][v] + acc[1][j][v]) + acc[2][j][v]) + acc[3][j][v];
+  for (int v = 0; v < 16; ++v) out[v] = ((acc[0][v] + acc[1][v]) + acc[2][v]) + acc[3][v];
   if (tail) {
     const Stage &st = stage[steps & 1];
 #pragma unroll
     for (int gi = 0; gi < KS - 1; ++gi) {
       if (gi < tail) {
         const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
+        const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
+        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+        if constexpr (SUMS) {
+          write_sums(a, S, r0 + wr * 32, t0 + wt * 32, G4 + gi, G, lane);
+        } else {
+          float p[16];
+          products(S, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + j * 32 * ROWB + gi * 32);
-          const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-          if constexpr (SUMS) {
-            write_sums(a, S, r0 + wr * 32, t0 + wt * 64 + j * 32, G4 + gi, G, lane);
-          } else {
-            float p[16];
-            products(S, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off + j * 32], p);
-#pragma unroll
-            for (int v = 0; v < 16; ++v) out[j][v] = out[j][v] + p[v];
-          }
+          for (int v = 0; v < 16; ++v) out[v] = out[v] + p[v];
         }
       }
     }
@@ -228,29 +215,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(const MatArgs a) {
 
   if constexpr (SUMS) return;
   // y[t][r] = out (or y + out): the lane's token, its 16 rows in 4 runs of 4
+  const int t = t0 + wt * 32 + (lane & 31);
+  if (t >= a.m) return;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = t0 + wt * 64 + j * 32 + (lane & 31);
-    if (t >= a.m) continue;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int row = r0 + wr * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (row >= a.total_rows) continue;
-      const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
-      int si = 0, r = row;
-      if (a.nseg > 2 && row >= n0 + n1) {
-        si = 2;
-        r = row - n0 - n1;
-      } else if (a.nseg > 1 && row >= n0) {
-        si = 1;
-        r = row - n0;
-      }
-      float *y = (si == 2 ? a.seg[2].y : si == 1 ? a.seg[1].y : a.seg[0].y);
-      const int stride = (si == 2 ? a.seg[2].y_stride : si == 1 ? a.seg[1].y_stride : a.seg[0].y_stride);
-      const int accumulate = (si == 2 ? a.seg[2].accumulate : si == 1 ? a.seg[1].accumulate : a.seg[0].accumulate);
-      float *dst = y + (int64_t)t * stride + r;
-      *dst = accumulate ? *dst + out[j][v] : out[j][v];
+  for (int v = 0; v < 16; ++v) {
+    const int row = r0 + wr * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+    if (row >= a.total_rows) continue;
+    const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
+    int si = 0, r = row;
+    if (a.nseg > 2 && row >= n0 + n1) {
+      si = 2;
+      r = row - n0 - n1;
+    } else if (a.nseg > 1 && row >= n0) {
+      si = 1;
+      r = row - n0;
     }
+    float *y = (si == 2 ? a.seg[2].y : si == 1 ? a.seg[1].y : a.seg[0].y);
+    const int stride = (si == 2 ? a.seg[2].y_stride : si == 1 ? a.seg[1].y_stride : a.seg[0].y_stride);
+    const int accumulate = (si == 2 ? a.seg[2].accumulate : si == 1 ? a.seg[1].accumulate : a.seg[0].accumulate);
+    float *dst = y + (int64_t)t * stride + r;
+    *dst = accumulate ? *dst + out[v] : out[v];
   }
 }
 
@@ -265,14 +249,14 @@ hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s) 
   if (grid.y > 65535) return hipErrorInvalidValue;
   if (a.sums) {
     if (six)
-      gemm_kernel<true, true><<<grid, 256, 0, s>>>(a);
+      gemm_kernel<true, true><<<grid, 512, 0, s>>>(a);
     else
-      gemm_kernel<false, true><<<grid, 256, 0, s>>>(a);
+      gemm_kernel<false, true><<<grid, 512, 0, s>>>(a);
   } else {
     if (six)
-      gemm_kernel<true, false><<<grid, 256, 0, s>>>(a);
+      gemm_kernel<true, false><<<grid, 512, 0, s>>>(a);
     else
-      gemm_kernel<false, false><<<grid, 256, 0, s>>>(a);
+      gemm_kernel<false, false><<<grid, 512, 0, s>>>(a);
   }
   return hipGetLastError();
 }
