@@ -97,6 +97,82 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   }
 }
 
+// (A) for many tokens (a prompt block): one block a (64-position tile, kv head, 32 / mul tokens): the tile's keys
+// staged once in LDS for every (token, head) row of the block, 32 rows; wave w takes rows w, w + 4, ..., a lane one
+// position, and runs the 8 rows' four lane sums side by side over the head (the keys read once for the 8). The
+// rows' tile maxima by wave reductions.
+constexpr int SROWS = 32;  // (token, head) rows a block
+
+template <int HS, bool HALF>
+__global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
+  constexpr int LD = HS + 4, C4 = HS / 4;
+  __shared__ float ks[TILE * LD];
+  __shared__ float qs[SROWS * HS];
+  const int tile = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int mul = a.nh / a.nkv, tt_n = max(1, SROWS / mul);
+  const int t0 = blockIdx.z * tt_n, last = min(t0 + tt_n, a.m) - 1;
+  const int p0 = tile * TILE;
+  if (p0 >= a.pos0 + last + 1) return;  // past every token of the block (uniform: before any barrier)
+  const int kvdim = a.nkv * HS;
+  const int np = min(TILE, a.pos0 + last + 1 - p0);  // positions any token of the block reaches
+  // keys: TILE * C4 float4, and the rows' queries: SROWS * C4 float4, requested together (clamped, unconditional)
+  constexpr int NK = TILE * C4 / 256, NQ = (SROWS * C4 + 255) / 256;
+  float4 kr[NK], qr[NQ];
+#pragma unroll
+  for (int u = 0; u < NK; ++u) {
+    const int i = tid + u * 256, p = min(i / C4, np - 1), c = i % C4;
+    kr[u] = cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
+  }
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int i = min(tid + u * 256, SROWS * C4 - 1), r = i / C4, c = i % C4;
+    const int t = min(t0 + r / mul, last), h = kh * mul + r % mul;
+    qr[u] = *reinterpret_cast<const float4 *>(a.q + (int64_t)t * a.q_stride + (int64_t)h * HS + 4 * c);
+  }
+#pragma unroll
+  for (int u = 0; u < NK; ++u) {
+    const int i = tid + u * 256, p = i / C4, c = i % C4;
+    *reinterpret_cast<float4 *>(ks + p * LD + 4 * c) = kr[u];
+  }
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int i = tid + u * 256;
+    if (i < SROWS * C4) *reinterpret_cast<float4 *>(qs + 4 * i) = qr[u];
+  }
+  __syncthreads();
+  const float isq = 1.0f / __builtin_sqrtf((float)HS);
+  float l[8][4];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) l[u][0] = l[u][1] = l[u][2] = l[u][3] = 0.0f;
+  const float *kp = ks + lane * LD;
+#pragma unroll 4
+  for (int j = 0; j < HS; j += 4) {
+    const float4 kv = *reinterpret_cast<const float4 *>(kp + j);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 qv = *reinterpret_cast<const float4 *>(qs + (wave + 4 * u) * HS + j);
+      l[u][0] = l[u][0] + qv.x * kv.x;
+      l[u][1] = l[u][1] + qv.y * kv.y;
+      l[u][2] = l[u][2] + qv.z * kv.z;
+      l[u][3] = l[u][3] + qv.w * kv.w;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int r = wave + 4 * u, tt = r / mul, hl = r % mul, t = t0 + tt;
+    const bool row = tt < tt_n && t < a.m;  // uniform over the wave
+    const int count = a.pos0 + min(t, a.m - 1) + 1;
+    float sc = -__builtin_inff();
+    if (row && p0 + lane < count) {
+      sc = ((l[u][0] + l[u][2]) + (l[u][1] + l[u][3])) * isq;
+      a.scores[((int64_t)t * a.nh + kh * mul + hl) * a.seq_len + p0 + lane] = sc;
+    }
+    float mx = sc;  // the tile's largest of this (token, head)
+    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+    if (row && lane == 0 && p0 < count) a.tilemax[((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1) + tile] = mx;
+  }
+}
+
 // (B) one block a (head, token): grid (nh, m), block 256. The scores requested at once, the exponentials by every
 // thread into LDS (lane k's positions t % 4 == k side by side), the four ordered sums by four threads, the weights.
 __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
@@ -351,7 +427,12 @@ __global__ __launch_bounds__(256) void pv_ring_kernel(const AttnArgs a) {
 template <int HS, bool HALF>
 hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
-  hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
+  if (a.m <= RING_TOKENS) {
+    hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
+  } else {
+    const int tt = std::max(1, SROWS / (a.nh / a.nkv));
+    hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
+  }
   const int most4 = (a.pos0 + a.m) & ~3;
   const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
