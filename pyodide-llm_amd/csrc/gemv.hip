@@ -535,7 +535,8 @@ hipError_t launch_decode(const MatArgs &a, hipStream_t s) {
   const int steps = (a.k / GS + 31) / 32;  // 1 KiB steps of a row
   if (steps <= 1) return launch_gemv1<4, 1>(a, s);
   if (steps <= 2) return launch_gemv1<4, 2>(a, s);
-  if (steps <= 4) return launch_gemv1<4, 4>(a, s);
+  // 4 KiB rows (measured over the Llama-3-8B shapes): 2 rows a wave for the larger matrices, 1 for 4096 rows or fewer
+  if (steps <= 4) return a.total_rows > 4096 ? launch_gemv1<2, 4>(a, s) : launch_gemv1<1, 4>(a, s);
   if (steps <= 8) return launch_gemv1<2, 8>(a, s);
   if (steps <= 16) return launch_gemv1<1, 16>(a, s);
   if (steps <= 20) return launch_gemv1<1, 20>(a, s);
