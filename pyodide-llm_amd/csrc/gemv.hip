@@ -536,7 +536,11 @@ hipError_t launch_decode(const MatArgs &a, hipStream_t s) {
   if (steps <= 1) return launch_gemv1<4, 1>(a, s);
   if (steps <= 2) return launch_gemv1<4, 2>(a, s);
   // 4 KiB rows (measured over the Llama-3-8B shapes): 2 rows a wave for the larger matrices, 1 for 4096 rows or fewer
-  if (steps <= 4) return a.total_rows > 4096 ? launch_gemv1<2, 4>(a, s) : launch_gemv1<1, 4>(a, s);
+  // (a block that quantizes its own token: 4 rows a wave, so that fewer blocks repeat it)
+  if (steps <= 4) {
+    if (a.xf) return launch_gemv1<4, 4>(a, s);
+    return a.total_rows > 4096 ? launch_gemv1<2, 4>(a, s) : launch_gemv1<1, 4>(a, s);
+  }
   if (steps <= 8) return launch_gemv1<2, 8>(a, s);
   if (steps <= 16) return launch_gemv1<1, 16>(a, s);
   if (steps <= 20) return launch_gemv1<1, 20>(a, s);
