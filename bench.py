@@ -32,8 +32,8 @@ PROFILED_STEPS = 8
 # WRITE_SIZE runs of this script, each counter scaled by what it reads on HIP's device-to-device copy of 1 GiB
 # (FETCH_SIZE read half the bytes copied: x2; WRITE_SIZE all of them: x1). The profile summary names the commands.
 TRAFFIC = {
-    "llama3-8b": {"bytes_per_pass": (2 * (32 * (13900 + 9308 + 64588 + 32447) + 288653)
-                                     + (32 * (24 + 16 + 112 + 32) + 501)) * 1024,
+    "llama3-8b": {"bytes_per_pass": round((2 * (32 * (13889.5 + 9336.5 + 64577.5 + 32450.5) + 288641.6)
+                                           + (32 * (24 + 32 + 112 + 32) + 501)) * 1024),
                   "source": "profiles/decode_gemv_llama3-8b.md"},
 }
 
