@@ -329,7 +329,7 @@ struct F32Source {
 };
 
 hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
-                         const float *xs, const F32Source *f32 = nullptr) {
+                         const float *xs, const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr) {
   const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
   const int32_t step = gemv_tokens(k, e->c.relaxed);
   if (step < 1) return hipErrorInvalidValue;
@@ -354,6 +354,7 @@ hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, 
       a.xnorm = f32->norm;
       a.eps = e->c.rms_norm_eps;
     }
+    if (qkv) a.qkv = *qkv;
     hipError_t err = launch_gemv(a, e->c.six, e->c.relaxed, e->stream);
     if (err != hipSuccess) return err;
   }
@@ -383,12 +384,12 @@ hipError_t gemm_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, in
 }
 
 hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs,
-                  const F32Source *f32 = nullptr) {
+                  const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr) {
   if (use_gemm(e, k, m))
     return timed(e, HE_K_GEMM, matmul_bytes(e, segs, nseg, k, m),
                  [&] { return gemm_launch(e, segs, nseg, k, m, xq, xs); });
   return timed(e, HE_K_GEMV, matmul_bytes(e, segs, nseg, k, m),
-               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, f32); });
+               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, f32, qkv); });
 }
 
 // one token whose rows of k the decode GEMV quantizes itself: it saves a launch where the GEMV is about one block a
@@ -414,11 +415,6 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
         {e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), e->q, qdim, qdim, 0},
         {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), e->k, kvdim, kvdim, 0},
         {e->mat(HE_T_WV, l), e->mat_scales(HE_T_WV, l), e->v, kvdim, kvdim, 0}};
-    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
-                                  W, W / 32, 0, c.rms_norm_eps, e->bias, s);
-    }));
-    HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
     QkvPost qp{};
     qp.q = e->q;
     qp.k = e->k;
@@ -438,8 +434,19 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     qp.pos0 = pos0;
     qp.m = m;
     qp.half = c.half_kv;
-    HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * (qdim + 2 * kvdim) * 8 + (double)m * 2 * kvdim * esz,
-                  [&] { return launch_qkv_post(qp, s); }));
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
+                                  W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+    }));
+    if (m == 1 && decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0)) {
+      // one token: the q/k/v GEMV adds the biases, rotates q and k and writes k and v into the cache itself
+      const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv};
+      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, nullptr, &fuse));
+    } else {
+      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
+      HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * (qdim + 2 * kvdim) * 8 + (double)m * 2 * kvdim * esz,
+                    [&] { return launch_qkv_post(qp, s); }));
+    }
     AttnArgs at{};
     at.q = e->q;
     at.q_stride = qdim;

@@ -52,6 +52,40 @@ __device__ __forceinline__ RowAt row_at(const MatArgs &a, int row) {
   return {a.seg[0].w, a.seg[0].ws, a.seg[0].y, row, a.seg[0].y_stride, a.seg[0].accumulate};
 }
 
+// the decode paths' store of row `row`'s result: y = sum (or y + sum). With a.qkv on (every lane of the wave calls
+// it, rows in pairs on lanes 2i, 2i + 1): + bias, RoPE on q and k rows (kernels/kernel.ts:344-357: pair (v0, v1) ->
+// (v0 c - v1 s, v0 s + v1 c)), and k and v rows into the cache too (float16 by to_f16 where the cache is half).
+__device__ __forceinline__ void store_row(const MatArgs &a, int row, float sum, bool valid) {
+  const RowAt at = row_at(a, min(row, a.total_rows - 1));
+  float *y = at.y + at.r;
+  if (!a.qkv.on) {
+    if (valid) *y = at.accumulate ? *y + sum : sum;
+    return;
+  }
+  const QkvFuse &f = a.qkv;
+  const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
+  const int seg = row < n0 ? 0 : (row < n0 + n1 ? 1 : 2), r = at.r;
+  const float *bias = seg == 0 ? f.bq : (seg == 1 ? f.bk : f.bv);
+  const float v = bias ? sum + bias[r] : sum;
+  const float partner = dpp_xor1(v);  // the pair's other row (lanes 2i, 2i + 1)
+  float o = v;
+  if (seg < 2) {
+    const int ci = (r % f.hs) >> 1;
+    const float c = f.cos_t[(int64_t)f.pos * (f.hs / 2) + ci], s = f.sin_t[(int64_t)f.pos * (f.hs / 2) + ci];
+    const bool even = (r & 1) == 0;
+    const float v0 = even ? v : partner, v1 = even ? partner : v;
+    o = even ? v0 * c - v1 * s : v0 * s + v1 * c;
+  }
+  if (!valid) return;
+  *y = o;
+  if (seg > 0) {
+    void *cache = seg == 1 ? f.kcache : f.vcache;
+    const int64_t i = (int64_t)f.pos * f.kvdim + r;
+    if (f.half) reinterpret_cast<uint16_t *>(cache)[i] = to_f16(o);
+    else reinterpret_cast<float *>(cache)[i] = o;
+  }
+}
+
 template <int M, bool SIX, bool RELAXED, bool SUMS>
 __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
   constexpr int GPI = SIX ? 64 : 32;  // groups a wave step
@@ -356,14 +390,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const int src = (lane < R ? lane : 0) * 4;
   const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
   const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
-  if (lane < R && row0 + lane < a.total_rows) {
-    float sum = ((c0 + c1) + c2) + c3;
+  float sum = ((c0 + c1) + c2) + c3;
+  if (lane < R) {
     const float *tl = P + lane * lay.stride + 4 * lay.q;
     for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
-    const RowAt at = row_at(a, row0 + lane);
-    float *y = at.y + at.r;
-    *y = at.accumulate ? *y + sum : sum;
   }
+  store_row(a, row0 + lane, sum, lane < R && row0 + lane < a.total_rows);
 }
 
 // The int6 decode path (one token, six.ts groups, bias 64: kernels/kernel_relaxed.ts:189-218 matmul_q6r): as
@@ -481,14 +513,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const int src = (lane < R ? lane : 0) * 4;
   const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
   const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
-  if (lane < R && row0 + lane < a.total_rows) {
-    float sum = ((c0 + c1) + c2) + c3;
+  float sum = ((c0 + c1) + c2) + c3;
+  if (lane < R) {
     const float *tl = P + lane * lay.stride + 4 * lay.q;
     for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
-    const RowAt at = row_at(a, row0 + lane);
-    float *y = at.y + at.r;
-    *y = at.accumulate ? *y + sum : sum;
   }
+  store_row(a, row0 + lane, sum, lane < R && row0 + lane < a.total_rows);
 }
 
 template <int R, int NS>
@@ -539,7 +569,7 @@ hipError_t launch_decode(const MatArgs &a, hipStream_t s) {
   // (a block that quantizes its own token: 4 rows a wave, so that fewer blocks repeat it)
   if (steps <= 4) {
     if (a.xf) return launch_gemv1<4, 4>(a, s);
-    return a.total_rows > 4096 ? launch_gemv1<2, 4>(a, s) : launch_gemv1<1, 4>(a, s);
+    return a.total_rows > 4096 || a.qkv.on ? launch_gemv1<2, 4>(a, s) : launch_gemv1<1, 4>(a, s);
   }
   if (steps <= 8) return launch_gemv1<2, 8>(a, s);
   if (steps <= 16) return launch_gemv1<1, 16>(a, s);
@@ -581,9 +611,16 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
 
 bool decode_takes_f32(int32_t k, bool six, bool relaxed) { return !six && relaxed && k <= 4 * 1024 && k % 32 == 0; }
 
+// the decode paths whose waves take rows in pairs: int8 rows up to 8 KiB, int6 rows up to 256 groups (even)
+bool decode_fuses_qkv(int32_t k, bool six, bool relaxed) {
+  if (!relaxed) return false;
+  return six ? (k / GS) % 2 == 0 && k <= 256 * GS : k <= 8 * 1024;
+}
+
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
   if (a.xf && (sums || a.m != 1 || !decode_takes_f32(a.k, six, relaxed))) return hipErrorInvalidValue;
+  if (a.qkv.on && (sums || a.m != 1 || !decode_fuses_qkv(a.k, six, relaxed))) return hipErrorInvalidValue;
   if (!sums && !six && relaxed && a.m == 1 && a.k <= 20 * 1024) return launch_decode(a, s);
   if (!sums && six && relaxed && a.m == 1 && a.k <= 24 * 1024 && (a.k / GS) % 2 == 0) return launch_decode6(a, s);
   if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;

@@ -19,6 +19,16 @@ struct MatSeg {
   int32_t accumulate;
 };
 
+// one token's q / k / v matmul (three segments) finishing the token's attention inputs in its epilogue, as
+// launch_qkv_post does (the bias add, RoPE on q and k, k and v into the cache): the decode path only, rows in pairs
+struct QkvFuse {
+  int32_t on;
+  const float *bq, *bk, *bv;   // Qwen2 biases or null
+  const float *cos_t, *sin_t;  // [seq_len][hs/2]
+  void *kcache, *vcache;       // this layer's [seq_len][kv_dim]
+  int32_t pos, hs, kvdim, half;
+};
+
 struct MatArgs {
   MatSeg seg[3];
   int32_t nseg;
@@ -35,6 +45,7 @@ struct MatArgs {
   const float *xf;
   const float *xnorm;
   float eps;
+  QkvFuse qkv;  // decode_fuses_qkv()
 };
 
 // the most tokens the engine gives one GEMV pass: more go to the MFMA GEMM where it takes them
@@ -44,6 +55,8 @@ constexpr int32_t GEMV_MOST = 8;
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
 // whether a one-token launch_gemv of rows of k takes its activations as float32 (MatArgs.xf)
 bool decode_takes_f32(int32_t k, bool six, bool relaxed);
+// whether a one-token launch_gemv of rows of k finishes q / k / v itself (MatArgs.qkv)
+bool decode_fuses_qkv(int32_t k, bool six, bool relaxed);
 // the most tokens one launch_gemv takes for rows of k (its products of a row fit the block's LDS)
 int32_t gemv_tokens(int32_t k, bool relaxed);
 // prefill GEMM on i8 MFMA, any m (bias 64, int8 or int6): the same bits as launch_gemv per (token, row); with
