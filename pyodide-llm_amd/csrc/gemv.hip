@@ -62,16 +62,19 @@ __device__ __forceinline__ void store_row(const MatArgs &a, int row, float sum, 
     if (valid) *y = at.accumulate ? *y + sum : sum;
     return;
   }
-  const QkvFuse &f = a.qkv;
+  // (every field read by value: a reference into the kernel's argument struct makes the compiler copy it to scratch)
+  const float *bq = a.qkv.bq, *bk = a.qkv.bk, *bv = a.qkv.bv, *cos_t = a.qkv.cos_t, *sin_t = a.qkv.sin_t;
+  void *kcache = a.qkv.kcache, *vcache = a.qkv.vcache;
+  const int pos = a.qkv.pos, hs = a.qkv.hs, kvdim = a.qkv.kvdim, half = a.qkv.half;
   const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
   const int seg = row < n0 ? 0 : (row < n0 + n1 ? 1 : 2), r = at.r;
-  const float *bias = seg == 0 ? f.bq : (seg == 1 ? f.bk : f.bv);
+  const float *bias = seg == 0 ? bq : (seg == 1 ? bk : bv);
   const float v = bias ? sum + bias[r] : sum;
   const float partner = dpp_xor1(v);  // the pair's other row (lanes 2i, 2i + 1)
   float o = v;
   if (seg < 2) {
-    const int ci = (r % f.hs) >> 1;
-    const float c = f.cos_t[(int64_t)f.pos * (f.hs / 2) + ci], s = f.sin_t[(int64_t)f.pos * (f.hs / 2) + ci];
+    const int ci = (r % hs) >> 1;
+    const float c = cos_t[(int64_t)pos * (hs / 2) + ci], s = sin_t[(int64_t)pos * (hs / 2) + ci];
     const bool even = (r & 1) == 0;
     const float v0 = even ? v : partner, v1 = even ? partner : v;
     o = even ? v0 * c - v1 * s : v0 * s + v1 * c;
@@ -79,9 +82,9 @@ __device__ __forceinline__ void store_row(const MatArgs &a, int row, float sum, 
   if (!valid) return;
   *y = o;
   if (seg > 0) {
-    void *cache = seg == 1 ? f.kcache : f.vcache;
-    const int64_t i = (int64_t)f.pos * f.kvdim + r;
-    if (f.half) reinterpret_cast<uint16_t *>(cache)[i] = to_f16(o);
+    void *cache = seg == 1 ? kcache : vcache;
+    const int64_t i = (int64_t)pos * kvdim + r;
+    if (half) reinterpret_cast<uint16_t *>(cache)[i] = to_f16(o);
     else reinterpret_cast<float *>(cache)[i] = o;
   }
 }
