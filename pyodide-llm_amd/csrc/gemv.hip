@@ -575,6 +575,8 @@ hipError_t launch_decode(const MatArgs &a, hipStream_t s) {
     return a.total_rows > 4096 || a.qkv.on ? launch_gemv1<2, 4>(a, s) : launch_gemv1<1, 4>(a, s);
   }
   if (steps <= 8) return launch_gemv1<2, 8>(a, s);
+  // 14 KiB rows (the 8B's w2) in exactly 14 steps: 16 steps a wave idle on 2 of them and run 4% slower
+  if (steps <= 14) return launch_gemv1<1, 14>(a, s);
   if (steps <= 16) return launch_gemv1<1, 16>(a, s);
   if (steps <= 20) return launch_gemv1<1, 20>(a, s);
   return hipErrorInvalidValue;

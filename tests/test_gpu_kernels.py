@@ -66,6 +66,16 @@ def test_int6_decode_bits(k, rows):
     assert same_bits(gl.matmul(xq, xs, w, ws, rows, k, 64, 1), ol.matmul(xq, xs, w, ws, rows, k, 64, 1))
 
 
+@pytest.mark.parametrize("k", [5120, 11008, 14336, 16384, 20480])
+@pytest.mark.parametrize("rows", [37, 130])
+def test_int8_decode_bits(k, rows):
+    """one token against int8 rows longer than 4 KiB: the decode path's 8, 14, 16 and 20-step waves, with and
+    without tail groups"""
+    w, ws = weights(rows, k, 0)
+    xq, xs = activations(1, k, 64)
+    assert same_bits(gl.matmul(xq, xs, w, ws, rows, k, 64, 0), ol.matmul(xq, xs, w, ws, rows, k, 64, 0))
+
+
 GEMM_CASES = [(k, rows, m) for k in (32, 96, 288, 1056, 4096) for rows, m in ((37, 9), (64, 130), (130, 200))]
 
 
