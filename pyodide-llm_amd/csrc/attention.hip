@@ -6,11 +6,13 @@
 //           in four lanes (t % 4) in order, hsum ((l0 + l1) + l2) + l3, the tail added in order; p = e * f32(1 / sum);
 //   out_j: blocks of four positions in order, out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), then the positions past
 //           the fours one at a time, out = out + p v.
-// Three launches: (A) the scores of 64-position tiles, every CU streaming keys once for the nh / nkv query heads
-// that share them, with each tile's maxima; (B) one block a (token, head): the exponentials, their ordered sum from
-// LDS, the weights p written over the scores; (C) the weighted values: for a few tokens (decode) a ring of LDS slots
-// that producer waves fill with the four-position products ahead of the wave that runs the ordered sums; for a prompt
-// block, blocks of tokens that share the values they stage, a thread a (token, head, column) sum.
+// The keys lie as the positions' rows ([seq_len][kv_dim]), the values as the columns' runs of positions
+// ([kv_dim][vstride]). Launches: (A) the scores of 64-position tiles, every CU streaming keys once for the nh / nkv
+// query heads that share them, with each tile's maxima; then for a few tokens (decode) one launch (B + C) a
+// (token, head, 16 columns): the exponentials, their ordered sum, and the weighted values, whose four-position
+// products producer waves put into a ring of LDS slots ahead of the lanes that run the ordered sums; for a prompt
+// block, (B) one block a (token, head) writing the weights p over the scores and (C) blocks of tokens that share the
+// values they stage, a thread a (token, head, column) sum.
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -24,8 +26,7 @@ namespace {
 
 constexpr int TILE = 64;   // positions a block of (A)
 constexpr int MAXMUL = 8;  // query heads a kv head at most
-constexpr int PVJ = 8;     // columns a block of (C)
-constexpr int RING_TOKENS = 8;  // up to this many tokens the weighted values run on the ring kernel (below)
+constexpr int DECODE_TOKENS = 8;  // up to this many tokens a launch runs the decode kernels (below)
 
 template <bool HALF>
 __device__ __forceinline__ float4 cache4(const void *c, int64_t i) {  // four values from element i (i % 4 == 0)
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
 // (C) for many tokens (a prompt block): one block of 256 threads a (kv head, 32 of its columns (16 where hs is not a
 // multiple of 32), 256 / (columns * mul) tokens), a thread a (token, head, column) whose ordered sum over the
 // four-position blocks it runs itself: out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) from LDS, where 128-position
-// chunks of the values (transposed: a column's positions side by side) and of the weights are staged, the next
+// chunks of the values (a column's positions side by side, as the cache holds them) and of the weights are staged, the next
 // chunk's loads in flight meanwhile. The block's tokens share every value they read; each stops at its own last four.
 constexpr int TPC = 128;  // positions a chunk
 
@@ -246,7 +247,6 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
   const int tid = threadIdx.x, kh = blockIdx.y;
   const int mul = a.nh / a.nkv, tt_n = max(1, ROWS / mul);
   const int j0 = blockIdx.x * COLS, t0 = blockIdx.z * tt_n;
-  const int kvdim = a.nkv * HS;
   const int j = tid % COLS, hl = (tid / COLS) % mul, tt = tid / (COLS * mul);
   const bool chain = tt < tt_n && t0 + tt < a.m;
   const int t = min(t0 + tt, a.m - 1);
@@ -261,8 +261,8 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
 #define PVT_FETCH(c_)                                                                                             \
   do {                                                                                                            \
     _Pragma("unroll") for (int u = 0; u < VPT; ++u) {                                                             \
-      const int i = tid + 256 * u, pos = min((c_) * TPC + i / (COLS / 4), most4 - 1), q = i % (COLS / 4);        \
-      v[u] = cache4<HALF>(a.vcache, (int64_t)pos * kvdim + kh * HS + j0 + 4 * q);                                 \
+      const int i = tid + 256 * u, cc = i / (TPC / 4), pos = min((c_) * TPC + 4 * (i % (TPC / 4)), most4 - 4);   \
+      v[u] = cache4<HALF>(a.vcache, (int64_t)(kh * HS + j0 + cc) * a.vstride + pos);                              \
     }                                                                                                             \
     _Pragma("unroll") for (int u = 0; u < WPT; ++u) {                                                             \
       const int i = tid + 256 * u;                                                                                \
@@ -274,12 +274,8 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
 #define PVT_STAGE(buf_)                                                                                           \
   do {                                                                                                            \
     _Pragma("unroll") for (int u = 0; u < VPT; ++u) {                                                             \
-      const int i = tid + 256 * u, pl = i / (COLS / 4), q = i % (COLS / 4);                                       \
-      float *col = vs[(buf_)] + (4 * q) * TVS + pl;                                                               \
-      col[0] = v[u].x;                                                                                            \
-      col[TVS] = v[u].y;                                                                                          \
-      col[2 * TVS] = v[u].z;                                                                                      \
-      col[3 * TVS] = v[u].w;                                                                                      \
+      const int i = tid + 256 * u;                                                                                \
+      *reinterpret_cast<float4 *>(vs[(buf_)] + (i / (TPC / 4)) * TVS + 4 * (i % (TPC / 4))) = v[u];               \
     }                                                                                                             \
     _Pragma("unroll") for (int u = 0; u < WPT; ++u) {                                                             \
       reinterpret_cast<float4 *>(ps[(buf_)])[tid + 256 * u] = w[u]; /* every row, the block's or clamped copies */ \
@@ -308,22 +304,29 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
 #undef PVT_STAGE
   if (chain) {
     const float *pt = a.scores + ((int64_t)t * a.nh + kh * mul + hl) * a.seq_len;
-    for (int p = count4; p < count; ++p) acc = acc + pt[p] * cache1<HALF>(a.vcache, (int64_t)p * kvdim + kh * HS + j0 + j);
+    for (int p = count4; p < count; ++p) acc = acc + pt[p] * cache1<HALF>(a.vcache, (int64_t)(kh * HS + j0 + j) * a.vstride + p);
     a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
   }
 }
 
-// (C) for a few tokens (decode): one block of 256 threads a (token, kv head, 8 of the head's columns), after (B) has
-// turned the scores into the weights p. Wave 0 runs the ordered sums of every (head, column); waves 1-3 each produce
-// every 3rd chunk of 256 positions of what those sums add, the four-position products
-// ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), into a ring of LDS slots, as far ahead as the ring allows, with the loads of
-// their next chunk in flight meanwhile. An LDS flag a slot says it is filled and a counter says how many chunks wave 0
-// has added: no block-wide barrier a chunk. Every wait is on another wave of the same block, for a chunk of a lower
-// index, so every wait ends.
+// (B + C) for a few tokens (decode), in one launch: one block of 512 threads a (token, query head, 16 of the head's
+// columns). The block requests everything it reads at once: the head's tile maxima (wave 0), its scores (every
+// thread), the producer waves' first value chunks and the tail values (wave 0). Then the exponentials go into LDS
+// (lane k's positions t % 4 == k side by side), four lanes of wave 0 run the ordered sums and the block has
+// f32(1 / sum); then producer waves 1-7 each turn every 7th chunk of 256 positions into the four-position products
+// ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) of the 16 columns, p = e * f32(1 / sum), in a ring of LDS slots, and wave 0's
+// first 16 lanes add them in order. An LDS flag a slot says it is filled and a counter says how many chunks wave 0 has
+// added; every wait is on another wave of the block for a chunk of a lower index, so every wait ends.
+// The blocks of the nh / nkv heads that share a kv head's 16 columns are dealt to one XCD (the hardware deals blocks
+// to the 8 XCDs in turn), so that the values they all read come from that XCD's L2 after the first.
+constexpr int AC = 16;                      // columns a block
+constexpr int AWAVES = 8, APROD = AWAVES - 1;
 constexpr int RP = 256, RB = RP / 4, RR = RB + 4;  // positions, four-position blocks, LDS row (floats) of a chunk
-constexpr int NSLOT = 3;                           // ring slots
-constexpr int SLOT = MAXMUL * PVJ * RR;            // floats a slot
-constexpr int NPROD = 3;                           // producer waves
+constexpr int ASLOTS = 8;                   // ring slots at most
+constexpr int ASV = 16;                     // scores a thread a pass (512 * 16 positions)
+constexpr int ALDS = 160 * 1024 - 256;      // LDS a block may take (gfx950: 160 KiB a workgroup), less the static part
+
+__host__ __device__ constexpr int attend_rowstride(int q4) { return ((q4 + 63) & ~63) + 16; }  // rows 16 banks apart
 
 __device__ __forceinline__ int lds_load(const int *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void lds_store(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
@@ -332,117 +335,170 @@ __device__ __forceinline__ void wait_at_least(const int *p, int v) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-template <int HS, bool HALF>
-__global__ __launch_bounds__(256) void pv_ring_kernel(const AttnArgs a) {
-  __shared__ float ring[NSLOT * SLOT];
-  __shared__ int filled[NSLOT], used;
-  const int j0 = blockIdx.x * PVJ, kh = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int count = a.pos0 + t + 1, count4 = count & ~3;
-  const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
-  const float *weights = a.scores + (int64_t)t * a.nh * a.seq_len + (int64_t)kh * mul * a.seq_len;
-  const int64_t vbase = (int64_t)kh * HS + j0;
-  const int chunks = (count4 + RP - 1) / RP;
-
-  if (tid < NSLOT) filled[tid] = 0;
-  if (tid == NSLOT) used = 0;
-  // wave 0, lane hl * 8 + j: the weights and values of the positions past the fours (at most 3), requested now and
-  // used at the end
-  float tp[3], tv[3];
-  if (wave == 0) {
-    const int hl = min(lane / PVJ, mul - 1), j = lane % PVJ;
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      const int p = min(count4 + r, count - 1);
-      tp[r] = weights[(int64_t)hl * a.seq_len + p];
-      tv[r] = cache1<HALF>(a.vcache, (int64_t)p * kvdim + vbase + j);
-    }
+// a chunk's values: lane = four-position block, one float4 of positions a column (clamped: never added past count4)
+#define ATT_FETCH(c, v)                                                               \
+  {                                                                                   \
+    const int64_t at_ = vcol + min((c) * RP + 4 * lane, count4 - 4);                  \
+    _Pragma("unroll") for (int j_ = 0; j_ < AC; ++j_) v[j_] = cache4<HALF>(a.vcache, at_ + (int64_t)j_ * a.vstride); \
   }
 
-  float acc = 0.0f;  // wave 0, lane hl * 8 + j
-  // lane = the four-position block b of the chunk: its 4 value rows (8 columns) and every head's 4 weights; a
-  // producer's first chunk is requested before the block's barrier
-  float4 va[8], vn[8], pa[MAXMUL], pn[MAXMUL];
-  auto fetch = [&](int c, float4 *v, float4 *pw) {
-    const int p = min(c * RP + 4 * lane, count4 - 4);  // clamped: never added past count4
-    const int64_t at = (int64_t)p * kvdim + vbase;
+template <int HS, bool HALF>
+__global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int nslot) {
+  extern __shared__ float4 lds4[];
+  float *const lds = reinterpret_cast<float *>(lds4);
+  __shared__ float shared_mx, shared_inv;
+  __shared__ int filled[ASLOTS], used;
+  constexpr int S = HS / AC;  // column slices a kv head
+  const int mul = a.nh / a.nkv, groups = a.nkv * S;
+  const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3, hl = idx % mul, g = (idx / mul) * 8 + xcd;
+  if (g >= groups) return;  // the grid's rounding up: whole blocks leave
+  const int kh = g / S, j0 = (g % S) * AC, h = kh * mul + hl;
+  const int t = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, pw = wave - 1;
+  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, rs = attend_rowstride(q4);
+  float *const e4 = lds;              // [4][rs]
+  float *const tail = lds + 4 * rs;   // [4]
+  float *const ring = tail + 4;       // [nslot][AC][RR]
+  const float *sc = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
+  const int64_t vcol = (int64_t)(kh * HS + j0) * a.vstride;  // the block's first value column
+  const int chunks = (count4 + RP - 1) / RP;
+
+  if (tid < ASLOTS) filled[tid] = 0;
+  if (tid == ASLOTS) used = 0;
+  // every load of the block, requested before anything waits: tile maxima, scores, values
+  const int tiles = (count + TILE - 1) / TILE;
+  const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
+  float tmr[2];
+  if (wave == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      v[2 * r] = cache4<HALF>(a.vcache, at + r * kvdim);
-      v[2 * r + 1] = cache4<HALF>(a.vcache, at + r * kvdim + 4);
+    for (int u = 0; u < 2; ++u) tmr[u] = tm[min(lane + 64 * u, tiles - 1)];  // clamped: a repeat changes no max
+  }
+  float sv[ASV];
+#pragma unroll
+  for (int u = 0; u < ASV; ++u) sv[u] = sc[min(tid + 512 * u, count - 1)];
+  float4 va[AC], vn[AC];
+  if (wave > 0 && pw < chunks) ATT_FETCH(pw, va);
+  if (wave > 0 && pw + APROD < chunks) ATT_FETCH(pw + APROD, vn);
+  float tv[3];  // wave 0, lane j < 16: column j's values past the fours (at most 3)
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+      tv[r] = cache1<HALF>(a.vcache, vcol + (int64_t)(lane % AC) * a.vstride + min(count4 + r, count - 1));
+  }
+  if (wave == 0) {
+    float mx = wmax(tmr[0], tmr[1]);
+    for (int i = lane + 128; i < tiles; i += 64) mx = wmax(mx, tm[i]);  // past 8192 positions
+    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) shared_mx = mx;
+  }
+  __syncthreads();
+  const float mx = shared_mx;
+  for (int base = 0; base < count; base += 512 * ASV) {
+    if (base > 0) {
+#pragma unroll
+      for (int u = 0; u < ASV; ++u) sv[u] = sc[min(base + tid + 512 * u, count - 1)];
     }
 #pragma unroll
-    for (int hl = 0; hl < MAXMUL; ++hl)
-      pw[hl] = *reinterpret_cast<const float4 *>(weights + (int64_t)min(hl, mul - 1) * a.seq_len + p);
-  };
-  if (wave > 0 && wave - 1 < chunks) fetch(wave - 1, va, pa);
+    for (int u = 0; u < ASV; ++u) {
+      const int i = base + tid + 512 * u;
+      if (i < count) {
+        const float d = sv[u] - mx;
+        if (i < count4) e4[(i & 3) * rs + (i >> 2)] = vexp(d);
+        else tail[i - count4] = fexp(d);
+      }
+    }
+  }
   __syncthreads();
+  if (wave == 0) {
+    // lanes 0-3: lane k's sum; ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
+    const float part = lane < 4 ? lds_chain(e4 + lane * rs, q4, 0.0f) : 0.0f;
+    const float c1 = __shfl(part, 1, 64), c2 = __shfl(part, 2, 64), c3 = __shfl(part, 3, 64);
+    if (lane == 0) {
+      float sum = ((part + c1) + c2) + c3;
+      for (int r = 0; r < count - count4; ++r) sum = sum + tail[r];
+      shared_inv = 1.0f / sum;
+    }
+  }
+  __syncthreads();
+  const float inv = shared_inv;
   if (wave > 0) {
-    for (int c = wave - 1; c < chunks; c += NPROD) {
-      if (c + NPROD < chunks) fetch(c + NPROD, vn, pn);  // the wave's next chunk flies meanwhile
-      wait_at_least(&used, c - NSLOT + 1);                // the slot's last chunk has been added
-      float *slot = ring + (c % NSLOT) * SLOT;
+    for (int c = pw; c < chunks; c += APROD) {
+      wait_at_least(&used, c - nslot + 1);  // the slot's last chunk has been added
+      float *slot = ring + (c % nslot) * (AC * RR) + lane;
+      const int b = min(c * RB + lane, q4 - 1);  // the lane's four-position block (clamped: never added past q4)
+      const float p0 = e4[b] * inv, p1 = e4[rs + b] * inv, p2 = e4[2 * rs + b] * inv, p3 = e4[3 * rs + b] * inv;
 #pragma unroll
-      for (int hl = 0; hl < MAXMUL; ++hl) {
-        if (hl < mul) {
-          const float p0 = pa[hl].x, p1 = pa[hl].y, p2 = pa[hl].z, p3 = pa[hl].w;
-          float *row = slot + hl * PVJ * RR + lane;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float4 x0 = va[h], x1 = va[2 + h], x2 = va[4 + h], x3 = va[6 + h];
-            row[(4 * h + 0) * RR] = (p0 * x0.x + p1 * x1.x) + (p2 * x2.x + p3 * x3.x);
-            row[(4 * h + 1) * RR] = (p0 * x0.y + p1 * x1.y) + (p2 * x2.y + p3 * x3.y);
-            row[(4 * h + 2) * RR] = (p0 * x0.z + p1 * x1.z) + (p2 * x2.z + p3 * x3.z);
-            row[(4 * h + 3) * RR] = (p0 * x0.w + p1 * x1.w) + (p2 * x2.w + p3 * x3.w);
-          }
-        }
+      for (int j = 0; j < AC; ++j) {
+        const float4 x = va[j];
+        slot[j * RR] = (p0 * x.x + p1 * x.y) + (p2 * x.z + p3 * x.w);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) lds_store(&filled[c % NSLOT], c + 1);
+      if (lane == 0) lds_store(&filled[c % nslot], c + 1);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) va[i] = vn[i];
-#pragma unroll
-      for (int hl = 0; hl < MAXMUL; ++hl) pa[hl] = pn[hl];
+      for (int j = 0; j < AC; ++j) va[j] = vn[j];
+      if (c + 2 * APROD < chunks) ATT_FETCH(c + 2 * APROD, vn);  // in flight while the wave waits
     }
   } else {
+    float acc = 0.0f;  // lane j < 16: column j0 + j
     for (int c = 0; c < chunks; ++c) {
-      wait_at_least(&filled[c % NSLOT], c + 1);
-      if (lane < mul * PVJ) {
+      wait_at_least(&filled[c % nslot], c + 1);
+      if (lane < AC) {
         const int nb = min(RP, count4 - c * RP) >> 2;
-        acc = lds_chain(ring + (c % NSLOT) * SLOT + lane * RR, nb, acc);
+        acc = lds_chain(ring + (c % nslot) * (AC * RR) + lane * RR, nb, acc);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) lds_store(&used, c + 1);
     }
-    if (lane < mul * PVJ) {
-      const int hl = lane / PVJ, j = lane % PVJ;
+    if (lane < AC) {
 #pragma unroll
       for (int r = 0; r < 3; ++r)
-        if (r < count - count4) acc = acc + tp[r] * tv[r];
-      a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
+        if (r < count - count4) acc = acc + (tail[r] * inv) * tv[r];
+      a.out[(int64_t)t * a.out_stride + h * HS + j0 + lane] = acc;
     }
   }
+}
+#undef ATT_FETCH
+
+// LDS bytes of attend_kernel for the largest count of a launch (ring slots into *nslot), 0 where it does not fit
+int attend_lds(const AttnArgs &a, int *nslot) {
+  const int count = a.pos0 + a.m;
+  const int head = (int)sizeof(float) * (4 * attend_rowstride((count & ~3) >> 2) + 4);
+  const int slot = (int)sizeof(float) * AC * RR;
+  const int n = std::min(ASLOTS, (ALDS - head) / slot);
+  if (n < 2) return 0;
+  *nslot = n;
+  return head + n * slot;
 }
 
 template <int HS, bool HALF>
 hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
-  if (a.m <= RING_TOKENS) {
+  if (a.m <= DECODE_TOKENS) {
     hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
   } else {
     const int tt = std::max(1, SROWS / (a.nh / a.nkv));
     hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   }
+  int nslot = 0;
+  const int fused = a.m <= DECODE_TOKENS ? attend_lds(a, &nslot) : 0;
+  if (fused) {
+    static bool sized = false;  // once a process: let the kernel take LDS past 64 KiB
+    if (!sized) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend_kernel<HS, HALF>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, ALDS);
+      if (e != hipSuccess) return e;
+      sized = true;
+    }
+    const int groups = a.nkv * (HS / AC), g8 = (groups + 7) & ~7;
+    hipLaunchKernelGGL((attend_kernel<HS, HALF>), dim3(g8 * (a.nh / a.nkv), 1, a.m), dim3(64 * AWAVES), fused, s, a,
+                       nslot);
+    return hipGetLastError();
+  }
   const int most4 = (a.pos0 + a.m) & ~3;
   const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
-  if (a.m <= RING_TOKENS) {
-    hipLaunchKernelGGL((pv_ring_kernel<HS, HALF>), dim3(HS / PVJ, a.nkv, a.m), dim3(256), 0, s, a);
-  } else {
-    constexpr int COLS = HS % 32 == 0 ? 32 : 16;
-    const int tt = std::max(1, 256 / COLS / (a.nh / a.nkv));
-    hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / COLS, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
-  }
+  constexpr int COLS = HS % 32 == 0 ? 32 : 16;
+  const int tt = std::max(1, 256 / COLS / (a.nh / a.nkv));
+  hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / COLS, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -14,11 +14,12 @@ namespace ple {
 // ---- integer helpers ----
 
 // i32.trunc_sat_f32_s: NaN to 0, out of range to the nearest end (the conversion of quantize_x, kernels/kernel.ts:145)
+// (as selects: the clamped conversion, then the top end and NaN)
 __device__ __forceinline__ int32_t trunc_sat(float f) {
-  if (f != f) return 0;
-  if (f >= 2147483648.0f) return 2147483647;
-  if (f < -2147483648.0f) return (-2147483647 - 1);
-  return (int32_t)f;
+  const float c = __builtin_fminf(__builtin_fmaxf(f, -2147483648.0f), 2147483520.0f);
+  int32_t r = (int32_t)c;
+  r = f >= 2147483648.0f ? 2147483647 : r;
+  return __builtin_isnan(f) ? 0 : r;
 }
 __device__ __forceinline__ int32_t sat16(int32_t v) { return v > 32767 ? 32767 : (v < -32768 ? -32768 : v); }
 __device__ __forceinline__ int32_t sat8(int32_t v) { return v > 127 ? 127 : (v < -128 ? -128 : v); }
@@ -55,16 +56,19 @@ __device__ __forceinline__ void six_widen(const uint32_t L[4], uint32_t T0, uint
 
 __device__ __forceinline__ float bits_f32(uint32_t u) { return __uint_as_float(u); }
 
-// f32x4.max / f32x4.min of WebAssembly: NaN if either is, else the larger / smaller (+0 above -0)
+// f32x4.max / f32x4.min of WebAssembly: NaN if either is, else the larger / smaller (+0 above -0); written as
+// selects, so that no branch splits a wave
 __device__ __forceinline__ float wmax(float a, float b) {
-  if (a != a || b != b) return a + b;
-  if (a == b) return __builtin_signbitf(a) ? b : a;
-  return a > b ? a : b;
+  const float larger = a > b ? a : b;
+  const float equal = __builtin_signbitf(a) ? b : a;
+  const float r = a == b ? equal : larger;
+  return __builtin_isunordered(a, b) ? a + b : r;
 }
 __device__ __forceinline__ float wmin(float a, float b) {
-  if (a != a || b != b) return a + b;
-  if (a == b) return __builtin_signbitf(a) ? a : b;
-  return a < b ? a : b;
+  const float smaller = a < b ? a : b;
+  const float equal = __builtin_signbitf(a) ? a : b;
+  const float r = a == b ? equal : smaller;
+  return __builtin_isunordered(a, b) ? a + b : r;
 }
 
 // the Cephes expf polynomial (S. L. Moshier's Cephes library) in the steps of kernels/kernel.ts:18-28

@@ -103,7 +103,7 @@ struct he_engine {
   const uint8_t *values[HE_T_COUNT]{};
   const float *scales[HE_T_COUNT]{};
   float *cos_t = nullptr, *sin_t = nullptr;
-  void *keys = nullptr, *vals = nullptr;  // [layers][seq_len][kv_dim]
+  void *keys = nullptr, *vals = nullptr;  // keys [layers][seq_len][kv_dim], values [layers][kv_dim][value_stride]
   int32_t qdim = 0, kvdim = 0, bias = 64, max_block = 1, chunk = 1, xw = 0, widest = 0;
   // activations of `chunk` tokens
   float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *hb = nullptr, *hb2 = nullptr;
@@ -246,10 +246,11 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   HIP_TRY(hipMemcpy(e->cos_t, rope_cos, table, hipMemcpyHostToDevice));
   HIP_TRY(hipMemcpy(e->sin_t, rope_sin, table, hipMemcpyHostToDevice));
   const size_t kv = (size_t)c.n_layers * c.seq_len * e->kvdim * (c.half_kv ? 2 : 4);
+  const size_t kv_values = (size_t)c.n_layers * value_stride(c.seq_len) * e->kvdim * (c.half_kv ? 2 : 4);
   ALLOC(e->keys, kv);
-  ALLOC(e->vals, kv);
+  ALLOC(e->vals, kv_values);
   HIP_TRY(hipMemset(e->keys, 0, kv));
-  HIP_TRY(hipMemset(e->vals, 0, kv));
+  HIP_TRY(hipMemset(e->vals, 0, kv_values));
   ALLOC(e->x, sizeof(float) * T * c.dim);
   ALLOC(e->xb, sizeof(float) * T * e->xw);
   ALLOC(e->q, sizeof(float) * T * e->qdim);
@@ -427,20 +428,22 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     qp.cos_t = e->cos_t;
     qp.sin_t = e->sin_t;
     qp.kcache = reinterpret_cast<uint8_t *>(e->keys) + (size_t)l * c.seq_len * kvdim * esz;
-    qp.vcache = reinterpret_cast<uint8_t *>(e->vals) + (size_t)l * c.seq_len * kvdim * esz;
+    qp.vcache = reinterpret_cast<uint8_t *>(e->vals) + (size_t)l * value_stride(c.seq_len) * kvdim * esz;
     qp.nh = c.n_heads;
     qp.nkv = c.n_kv_heads;
     qp.hs = hs;
     qp.pos0 = pos0;
     qp.m = m;
     qp.half = c.half_kv;
+    qp.vstride = value_stride(c.seq_len);
     HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
       return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
                                   W, W / 32, 0, c.rms_norm_eps, e->bias, s);
     }));
     if (m == 1 && decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0)) {
       // one token: the q/k/v GEMV adds the biases, rotates q and k and writes k and v into the cache itself
-      const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv};
+      const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv,
+                         qp.vstride};
       HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, nullptr, &fuse));
     } else {
       HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
@@ -463,6 +466,7 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.m = m;
     at.seq_len = c.seq_len;
     at.half = c.half_kv;
+    at.vstride = qp.vstride;
     double kv_rows = 0;
     for (int32_t t = 0; t < m; ++t) kv_rows += pos0 + t + 1;
     HIP_TRY(timed(e, HE_K_ATTENTION, kv_rows * 2 * kvdim * esz + (double)m * qdim * 8,
@@ -727,28 +731,35 @@ int32_t he_logits(he_engine *e, float *out) {
 int32_t he_kv_read(he_engine *e, int32_t from, int32_t count, float *keys, float *values) {
   if (!e || !keys || !values) return fail(HE_E_ARG, "a required pointer is null");
   if (from < 0 || count < 0 || (int64_t)from + count > e->c.seq_len) return fail(HE_E_ARG, "positions out of range");
-  const size_t esz = e->c.half_kv ? 2 : 4;
-  std::vector<uint8_t> row((size_t)count * e->kvdim * esz);
-  for (int pass = 0; pass < 2; ++pass) {
-    const uint8_t *src = reinterpret_cast<const uint8_t *>(pass ? e->vals : e->keys);
-    float *dst = pass ? values : keys;
-    for (int32_t l = 0; l < e->c.n_layers; ++l) {
-      HIP_TRY(hipMemcpy(row.data(), src + ((size_t)l * e->c.seq_len + from) * e->kvdim * esz, row.size(),
-                        hipMemcpyDeviceToHost));
-      float *o = dst + (size_t)l * count * e->kvdim;
-      for (size_t i = 0; i < (size_t)count * e->kvdim; ++i) {
-        if (esz == 4) {
-          std::memcpy(&o[i], &row[i * 4], 4);
-        } else {
-          uint16_t h;
-          std::memcpy(&h, &row[i * 2], 2);
-          int32_t bits = ((int32_t)(int16_t)h << 13) & (int32_t)0x8fffffff;
-          float f;
-          std::memcpy(&f, &bits, 4);
-          o[i] = f * 5.192296858534828e33f;
-        }
-      }
+  const size_t esz = e->c.half_kv ? 2 : 4, kvdim = e->kvdim, vs = value_stride(e->c.seq_len);
+  std::vector<uint8_t> rows((size_t)count * kvdim * esz);
+  auto widen = [&](size_t i) {  // element i of rows as float32
+    if (esz == 4) {
+      float f;
+      std::memcpy(&f, &rows[i * 4], 4);
+      return f;
     }
+    uint16_t h;
+    std::memcpy(&h, &rows[i * 2], 2);
+    int32_t bits = ((int32_t)(int16_t)h << 13) & (int32_t)0x8fffffff;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f * 5.192296858534828e33f;
+  };
+  for (int32_t l = 0; l < e->c.n_layers; ++l) {
+    // keys: the positions' rows as they lie
+    const uint8_t *k = reinterpret_cast<const uint8_t *>(e->keys) + ((size_t)l * e->c.seq_len + from) * kvdim * esz;
+    HIP_TRY(hipMemcpy(rows.data(), k, rows.size(), hipMemcpyDeviceToHost));
+    float *ko = keys + (size_t)l * count * kvdim;
+    for (size_t i = 0; i < (size_t)count * kvdim; ++i) ko[i] = widen(i);
+    if (count == 0) continue;
+    // values: kv_dim columns of count positions each, turned into the positions' rows
+    const uint8_t *v = reinterpret_cast<const uint8_t *>(e->vals) + ((size_t)l * kvdim * vs + from) * esz;
+    HIP_TRY(hipMemcpy2D(rows.data(), (size_t)count * esz, v, vs * esz, (size_t)count * esz, kvdim,
+                        hipMemcpyDeviceToHost));
+    float *vo = values + (size_t)l * count * kvdim;
+    for (size_t col = 0; col < kvdim; ++col)
+      for (size_t p = 0; p < (size_t)count; ++p) vo[p * kvdim + col] = widen(col * count + p);
   }
   return HE_OK;
 }

@@ -19,14 +19,18 @@ struct MatSeg {
   int32_t accumulate;
 };
 
+// the value cache holds a column's positions side by side, each column seq_len rounded up to 64 positions (256 bytes
+// of float32): the weighted sums read a column's values as contiguous runs
+inline int32_t value_stride(int32_t seq_len) { return (seq_len + 63) & ~63; }
+
 // one token's q / k / v matmul (three segments) finishing the token's attention inputs in its epilogue, as
 // launch_qkv_post does (the bias add, RoPE on q and k, k and v into the cache): the decode path only, rows in pairs
 struct QkvFuse {
   int32_t on;
   const float *bq, *bk, *bv;   // Qwen2 biases or null
   const float *cos_t, *sin_t;  // [seq_len][hs/2]
-  void *kcache, *vcache;       // this layer's [seq_len][kv_dim]
-  int32_t pos, hs, kvdim, half;
+  void *kcache, *vcache;       // this layer's keys [seq_len][kv_dim] and values [kv_dim][vstride]
+  int32_t pos, hs, kvdim, half, vstride;
 };
 
 struct MatArgs {
@@ -86,8 +90,8 @@ struct QkvPost {
   int32_t q_stride, kv_stride;
   const float *bq, *bk, *bv;
   const float *cos_t, *sin_t;  // [seq_len][hs/2]
-  void *kcache, *vcache;       // this layer's [seq_len][kv_dim]
-  int32_t nh, nkv, hs, pos0, m, half;
+  void *kcache, *vcache;       // this layer's keys [seq_len][kv_dim] and values [kv_dim][vstride]
+  int32_t nh, nkv, hs, pos0, m, half, vstride;
 };
 hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s);
 
@@ -95,12 +99,12 @@ hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s);
 struct AttnArgs {
   const float *q;
   int32_t q_stride;
-  const void *kcache, *vcache;
+  const void *kcache, *vcache;  // keys [seq_len][kv_dim] (a position's row), values [kv_dim][vstride] (a column's)
   float *out;
   int32_t out_stride;
   float *scores;  // [m][nh][seq_len]
   float *tilemax; // [m][nh][seq_len / 64 + 1]
-  int32_t nh, nkv, hs, pos0, m, seq_len, half;
+  int32_t nh, nkv, hs, pos0, m, seq_len, half, vstride;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the head sizes and grouping the attention kernels take (hs in {16, 32, 48, 64, 96, 128, 256}, nh / nkv <= 8)

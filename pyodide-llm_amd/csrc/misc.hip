@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPost a) {
       float o = v[i];
       if (a.bv) o = o + a.bv[i];
       v[i] = o;
-      const int64_t at = (int64_t)pos * kvdim + i;
+      const int64_t at = (int64_t)i * a.vstride + pos;
       if (a.half) reinterpret_cast<uint16_t *>(a.vcache)[at] = to_f16(o);
       else reinterpret_cast<float *>(a.vcache)[at] = o;
     }

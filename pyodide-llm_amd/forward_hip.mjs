@@ -56,7 +56,8 @@ export function footprint(header, size, { halfKV = false, head_dim = 0, promptBl
   const vocab = Math.abs(signedVocab), headSize = head_dim || dim / heads;
   const kvDim = kvHeads * headSize, qDim = heads * headSize, wide = Math.max(dim, qDim, hidden);
   const half = halfKV && kvHeads >= heads;
-  const keys = 2 * layers * seqLen * kvDim * (half ? 2 : 4);
+  // keys by position, values by column (each column's positions rounded up to 64)
+  const keys = layers * (seqLen + Math.ceil(seqLen / 64) * 64) * kvDim * (half ? 2 : 4);
   const chunk = Math.min(promptBlock, 16);
   const frames = chunk * (4 * (2 * dim + qDim + 2 * kvDim + 2 * hidden) + wide + wide / 8 + 4 * heads * seqLen);
   return keys + 2 * seqLen * headSize * 2 + frames + vocab * 4 + 2 ** 20;

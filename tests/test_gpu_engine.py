@@ -121,3 +121,56 @@ def test_long_context_crosses_attention_chunks(half_kv):
         assert same_bits(eng.logits(), ref.logits()), pos
     a, (k, v) = eng.keysAndValues(0, 1100), ref.kv(0, 1100)
     assert same_bits(a["keys"], k.reshape(-1)) and same_bits(a["values"], v.reshape(-1))
+
+
+LONG = {
+    # head size 128, four query heads a kv head (the 8B's grouping): 15 chunks of 256 positions, past the producers'
+    # two chunks in registers
+    "hs128_mul4": (dict(dim=512, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=1, head_size=128, vocab_size=320,
+                        seq_len=3700, shared_classifier=1), 3600),
+    # eight query heads a kv head past 2048 positions: more exponentials than one block's LDS takes, so the decode
+    # steps run the separate softmax and weighted-value kernels
+    "mul8_past_lds": (dict(dim=256, hidden_dim=128, n_layers=1, n_heads=16, n_kv_heads=2, head_size=16,
+                           vocab_size=320, seq_len=2200, shared_classifier=1), 2100),
+}
+
+
+@pytest.mark.parametrize("name", sorted(LONG))
+@pytest.mark.parametrize("half_kv", [0, 1])
+def test_long_decode_attention(name, half_kv):
+    """decode steps after a long prompt, every count % 4, against the oracle to the bit"""
+    fields, prompt = LONG[name]
+    cfg = ol.config(**{**fields, "half_kv": half_kv})
+    tensors, size = ol.places(cfg)
+    ck = ol.synth_checkpoint(cfg, tensors, size, seed=9)
+    cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, 10000.0)
+    tokens = [int(t) for t in np.random.default_rng(12).integers(0, cfg.vocab_size, size=prompt + 8)]
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=512)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=prompt)
+    eng.forwardMany(tokens[:prompt], 0)
+    ref.run(tokens[:prompt], 0, False)
+    for pos in range(prompt, prompt + 8):
+        eng.forward(tokens[pos], pos, True)
+        ref.run([tokens[pos]], pos, True)
+        assert same_bits(eng.logits(), ref.logits()), pos
+    eng.release()
+
+
+@pytest.mark.parametrize("piece", [3, 5, 8])
+def test_prompt_in_small_pieces_equals_one_at_a_time(piece):
+    """prompt pieces of up to 8 tokens run the decode attention with several tokens a launch"""
+    cfg, tensors, ck, cos, sin, _ = build("tiny_qwen_int6")
+    pk = package()
+    rng = np.random.default_rng(8)
+    tokens = [int(t) for t in rng.integers(0, cfg.vocab_size, size=41)]
+    one = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    for pos, tok in enumerate(tokens):
+        one.forward(tok, pos, pos == len(tokens) - 1)
+    many = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    for at in range(0, len(tokens) - 1, piece):
+        many.forwardMany(tokens[at:min(at + piece, len(tokens) - 1)], at)
+    many.forward(tokens[-1], len(tokens) - 1, True)
+    assert same_bits(one.logits(), many.logits())
+    a, b = one.keysAndValues(0, len(tokens)), many.keysAndValues(0, len(tokens))
+    assert same_bits(a["keys"], b["keys"]) and same_bits(a["values"], b["values"])
