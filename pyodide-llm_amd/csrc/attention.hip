@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   __shared__ float part[4];
   __shared__ float shared_mx, shared_inv;
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = (q4 + 3) & ~3;
+  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = chain_rowstride(q4);
   const int tiles = (count + TILE - 1) / TILE;
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
@@ -326,7 +326,6 @@ constexpr int ASLOTS = 8;                   // ring slots at most
 constexpr int ASV = 16;                     // scores a thread a pass (512 * 16 positions)
 constexpr int ALDS = 160 * 1024 - 256;      // LDS a block may take (gfx950: 160 KiB a workgroup), less the static part
 
-__host__ __device__ constexpr int attend_rowstride(int q4) { return ((q4 + 63) & ~63) + 16; }  // rows 16 banks apart
 
 __device__ __forceinline__ int lds_load(const int *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void lds_store(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
@@ -354,7 +353,7 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
   if (g >= groups) return;  // the grid's rounding up: whole blocks leave
   const int kh = g / S, j0 = (g % S) * AC, h = kh * mul + hl;
   const int t = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, pw = wave - 1;
-  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, rs = attend_rowstride(q4);
+  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, rs = chain_rowstride(q4);
   float *const e4 = lds;              // [4][rs]
   float *const tail = lds + 4 * rs;   // [4]
   float *const ring = tail + 4;       // [nslot][AC][RR]
@@ -461,7 +460,7 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
 // LDS bytes of attend_kernel for the largest count of a launch (ring slots into *nslot), 0 where it does not fit
 int attend_lds(const AttnArgs &a, int *nslot) {
   const int count = a.pos0 + a.m;
-  const int head = (int)sizeof(float) * (4 * attend_rowstride((count & ~3) >> 2) + 4);
+  const int head = (int)sizeof(float) * (4 * chain_rowstride((count & ~3) >> 2) + 4);
   const int slot = (int)sizeof(float) * AC * RR;
   const int n = std::min(ASLOTS, (ALDS - head) / slot);
   if (n < 2) return 0;
@@ -494,7 +493,7 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
     return hipGetLastError();
   }
   const int most4 = (a.pos0 + a.m) & ~3;
-  const size_t lds_b = sizeof(float) * (size_t)(4 * ((most4 / 4 + 3) & ~3) + 4);
+  const size_t lds_b = sizeof(float) * (size_t)(4 * chain_rowstride(most4 / 4) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
   constexpr int COLS = HS % 32 == 0 ? 32 : 16;
   const int tt = std::max(1, 256 / COLS / (a.nh / a.nkv));

@@ -158,38 +158,32 @@ __device__ __forceinline__ float add32(float acc, const float4 v[8]) {
   return acc;
 }
 
-// acc + c[0] + c[1] + ... + c[n-1] in order (every add rounded), the values read from LDS 32 at a time into two sets
-// of registers in turn: the next 32 are requested before this 32's adds (the scheduling barriers keep the compiler
-// from sinking the loads among the adds), so the dependent adds run back to back instead of waiting on the LDS.
-// c 16-byte aligned.
+// the row stride (floats) of four ordered sums' values side by side in LDS: rows of q4 values 16-byte aligned and
+// 64 bytes apart modulo 256, so that the four lanes' 16-byte reads of one step fall on distinct banks
+__host__ __device__ constexpr int chain_rowstride(int q4) { return ((q4 + 63) & ~63) + 16; }
+
+// acc + c[0] + c[1] + ... + c[n-1] in order (every add rounded), the values read from LDS 64 at a time: the second
+// 32's reads fly while the first 32 are added. (No reads carried across iterations: a loop-carried set of registers
+// makes the compiler copy it every iteration, which costs more than the latency it hides.) c 16-byte aligned.
 __device__ __forceinline__ float lds_chain(const float *c, int n, float acc) {
   const float4 *c4 = reinterpret_cast<const float4 *>(c);
   const int n4 = n >> 2;
   int i = 0;
-  if (n4 >= 8) {
+  for (; i + 16 <= n4; i += 16) {
     float4 a[8], b[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = c4[u];
-    for (i = 8; i + 16 <= n4; i += 16) {
+    for (int u = 0; u < 8; ++u) a[u] = c4[i + u];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) b[u] = c4[i + u];
-      __builtin_amdgcn_sched_barrier(0);
-      acc = add32(acc, a);
+    for (int u = 0; u < 8; ++u) b[u] = c4[i + 8 + u];
+    acc = add32(acc, a);
+    acc = add32(acc, b);
+  }
+  if (i + 8 <= n4) {
+    float4 a[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) a[u] = c4[i + 8 + u];
-      __builtin_amdgcn_sched_barrier(0);
-      acc = add32(acc, b);
-    }
-    if (i + 8 <= n4) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) b[u] = c4[i + u];
-      __builtin_amdgcn_sched_barrier(0);
-      acc = add32(acc, a);
-      acc = add32(acc, b);
-      i += 8;
-    } else {
-      acc = add32(acc, a);
-    }
+    for (int u = 0; u < 8; ++u) a[u] = c4[i + u];
+    acc = add32(acc, a);
+    i += 8;
   }
   for (; i < n4; ++i) {
     const float4 v = c4[i];

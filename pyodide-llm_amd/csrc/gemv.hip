@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 template <int MAXU>
 __device__ __forceinline__ void stage_from_f32(const MatArgs &a, uint8_t *xl, float *xsl, float *sq) {
   __shared__ float part[4], sval;
-  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = (q4 + 3) & ~3;
+  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = chain_rowstride(q4);
   float xv[MAXU], wv[MAXU];
 #pragma unroll
   for (int u = 0; u < MAXU; ++u) {
@@ -552,7 +552,7 @@ hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const size_t g16 = ((a.k / GS) + 3) & ~3;
   const size_t head = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R);
   size_t products = sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
-  if (a.xf) products = std::max(products, sizeof(float) * 4 * (size_t)(((a.k / 4) + 3) & ~3));  // the squares
+  if (a.xf) products = std::max(products, sizeof(float) * 4 * (size_t)chain_rowstride(a.k / 4));  // the squares
   const size_t lds = head + products;
   if constexpr (NS <= 4) {
     if (a.xf) {

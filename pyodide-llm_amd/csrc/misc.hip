@@ -40,10 +40,10 @@ __global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *
                                                             int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                                             float eps, int32_t bias) {
   extern __shared__ float sm[];
-  const int n4 = n & ~3, q4 = n4 >> 2, qs = (q4 + 3) & ~3;
+  const int n4 = n & ~3, q4 = n4 >> 2, qs = chain_rowstride(q4);
   float *xv = sm;            // n
   float *wv = sm + n;        // n
-  float *sq = sm + 2 * n;    // 4 * qs, transposed: lane k's squares side by side (16-byte aligned rows)
+  float *sq = sm + 2 * n;    // 4 * qs, transposed: lane k's squares side by side
   __shared__ float part[4];
   __shared__ float sval;
   const int t = blockIdx.x, tid = threadIdx.x;
@@ -309,7 +309,7 @@ hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int
 hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s) {
-  const size_t lds = sizeof(float) * (size_t)(3 * n + 16);
+  const size_t lds = sizeof(float) * (size_t)(2 * n + 4 * chain_rowstride((n & ~3) >> 2) + 16);
   // one token: 4 blocks share its groups (more tokens fill the chip by themselves)
   const int split = m < 64 ? 4 : 1;
   hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m, split), dim3(1024), lds, s, xq, xs, out, x, w, n, x_stride,
