@@ -442,7 +442,17 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
       wait_at_least(&filled[c % nslot], c + 1);
       if (lane < AC) {
         const int nb = min(RP, count4 - c * RP) >> 2;
-        acc = lds_chain(ring + (c % nslot) * (AC * RR) + lane * RR, nb, acc);
+        const float *row = ring + (c % nslot) * (AC * RR) + lane * RR;
+        if (nb == RB) {  // a whole chunk: its 16 reads requested together (the scheduling barrier keeps them so)
+          float4 x[RB / 4];
+#pragma unroll
+          for (int u = 0; u < RB / 4; ++u) x[u] = reinterpret_cast<const float4 *>(row)[u];
+          __builtin_amdgcn_sched_barrier(0);
+          acc = add32(acc, x);
+          acc = add32(acc, x + 8);
+        } else {
+          acc = lds_chain(row, nb, acc);
+        }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) lds_store(&used, c + 1);
