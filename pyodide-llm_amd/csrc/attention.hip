@@ -309,23 +309,29 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
   }
 }
 
-// (B + C) for a few tokens (decode), in one launch: one block of 512 threads a (token, query head, 16 of the head's
-// columns). The block requests everything it reads at once: the head's tile maxima (wave 0), its scores (every
-// thread), the producer waves' first value chunks and the tail values (wave 0). Then the exponentials go into LDS
-// (lane k's positions t % 4 == k side by side), four lanes of wave 0 run the ordered sums and the block has
-// f32(1 / sum); then producer waves 1-7 each turn every 7th chunk of 256 positions into the four-position products
-// ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) of the 16 columns, p = e * f32(1 / sum), in a ring of LDS slots, and wave 0's
-// first 16 lanes add them in order. An LDS flag a slot says it is filled and a counter says how many chunks wave 0 has
-// added; every wait is on another wave of the block for a chunk of a lower index, so every wait ends.
-// The blocks of the nh / nkv heads that share a kv head's 16 columns are dealt to one XCD (the hardware deals blocks
-// to the 8 XCDs in turn), so that the values they all read come from that XCD's L2 after the first.
-constexpr int AC = 16;                      // columns a block
-constexpr int AWAVES = 8, APROD = AWAVES - 1;
+// (B + C) for a few tokens (decode), in one launch: one block a (token, query head, 32 of the head's columns: one
+// quantization group, 16 where the head size is not a multiple of 32). The block requests everything it reads at
+// once: the head's tile maxima (wave 0), its scores (every thread), the producer waves' first value chunks and the
+// tail values (wave 0). Then the exponentials go into LDS (lane k's positions t % 4 == k side by side), four lanes of
+// wave 0 run the ordered sums and the block has f32(1 / sum); then the producer waves each turn every NP-th item (a
+// chunk of 256 positions and 16 columns, the next two requested ahead) into the four-position products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)),
+// p = e * f32(1 / sum), in a ring of LDS slots, and wave 0's first lanes add them in order, a lane a column. An LDS flag
+// a (slot, half) says it is filled and a counter says how many chunks wave 0 has added; every wait is on another wave
+// of the block for a chunk of a lower index, so every wait ends. With a whole group, wave 0 also runs quantize_x on
+// its 32 sums (the output projection's activations, no launch of their own).
+// The blocks of the nh / nkv heads that share a kv head's columns are dealt to one XCD (the hardware deals blocks to
+// the 8 XCDs in turn), so that the values they all read come from that XCD's L2 after the first.
 constexpr int RP = 256, RB = RP / 4, RR = RB + 4;  // positions, four-position blocks, LDS row (floats) of a chunk
 constexpr int ASLOTS = 8;                   // ring slots at most
-constexpr int ASV = 16;                     // scores a thread a pass (512 * 16 positions)
 constexpr int ALDS = 160 * 1024 - 256;      // LDS a block may take (gfx950: 160 KiB a workgroup), less the static part
 
+template <int HS> struct Attend {
+  static constexpr int AC = HS % 32 == 0 ? 32 : 16;  // columns a block
+  static constexpr int H = AC / 16;                   // 16-column items a chunk
+  static constexpr int NT = 512;                      // threads a block
+  static constexpr int NP = NT / 64 - 1;              // producer waves
+  static constexpr int SV = 16;                       // scores a thread a pass (8192 positions)
+};
 
 __device__ __forceinline__ int lds_load(const int *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
 __device__ __forceinline__ void lds_store(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
@@ -334,19 +340,22 @@ __device__ __forceinline__ void wait_at_least(const int *p, int v) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// a chunk's values: lane = four-position block, one float4 of positions a column (clamped: never added past count4)
-#define ATT_FETCH(c, v)                                                               \
-  {                                                                                   \
-    const int64_t at_ = vcol + min((c) * RP + 4 * lane, count4 - 4);                  \
-    _Pragma("unroll") for (int j_ = 0; j_ < AC; ++j_) v[j_] = cache4<HALF>(a.vcache, at_ + (int64_t)j_ * a.vstride); \
+// an item's values: lane = four-position block, one float4 of positions a column of the item's 16 (clamped: never
+// added past count4)
+#define ATT_FETCH(item, v)                                                                                    \
+  {                                                                                                           \
+    const int64_t at_ = vcol + (int64_t)((item) % H * 16) * a.vstride + min((item) / H * RP + 4 * lane, count4 - 4); \
+    _Pragma("unroll") for (int j_ = 0; j_ < 16; ++j_) v[j_] = cache4<HALF>(a.vcache, at_ + (int64_t)j_ * a.vstride); \
   }
 
 template <int HS, bool HALF>
-__global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int nslot) {
+__global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a, const int nslot) {
+  using P = Attend<HS>;
+  constexpr int AC = P::AC, H = P::H, NT = P::NT, NP = P::NP, ASV = P::SV;
   extern __shared__ float4 lds4[];
   float *const lds = reinterpret_cast<float *>(lds4);
   __shared__ float shared_mx, shared_inv;
-  __shared__ int filled[ASLOTS], used;
+  __shared__ int filled[ASLOTS][H], used;
   constexpr int S = HS / AC;  // column slices a kv head
   const int mul = a.nh / a.nkv, groups = a.nkv * S;
   const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3, hl = idx % mul, g = (idx / mul) * 8 + xcd;
@@ -359,10 +368,10 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
   float *const ring = tail + 4;       // [nslot][AC][RR]
   const float *sc = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   const int64_t vcol = (int64_t)(kh * HS + j0) * a.vstride;  // the block's first value column
-  const int chunks = (count4 + RP - 1) / RP;
+  const int chunks = (count4 + RP - 1) / RP, items = chunks * H;
 
-  if (tid < ASLOTS) filled[tid] = 0;
-  if (tid == ASLOTS) used = 0;
+  if (tid < ASLOTS * H) filled[tid / H][tid % H] = 0;
+  if (tid == ASLOTS * H) used = 0;
   // every load of the block, requested before anything waits: tile maxima, scores, values
   const int tiles = (count + TILE - 1) / TILE;
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
@@ -373,11 +382,11 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
   }
   float sv[ASV];
 #pragma unroll
-  for (int u = 0; u < ASV; ++u) sv[u] = sc[min(tid + 512 * u, count - 1)];
-  float4 va[AC], vn[AC];
-  if (wave > 0 && pw < chunks) ATT_FETCH(pw, va);
-  if (wave > 0 && pw + APROD < chunks) ATT_FETCH(pw + APROD, vn);
-  float tv[3];  // wave 0, lane j < 16: column j's values past the fours (at most 3)
+  for (int u = 0; u < ASV; ++u) sv[u] = sc[min(tid + NT * u, count - 1)];
+  float4 va[16], vn[16];  // a producer's next two items
+  if (wave > 0 && pw < items) ATT_FETCH(pw, va);
+  if (wave > 0 && pw + NP < items) ATT_FETCH(pw + NP, vn);
+  float tv[3];  // wave 0, lane j < AC: column j's values past the fours (at most 3)
   if (wave == 0) {
 #pragma unroll
     for (int r = 0; r < 3; ++r)
@@ -391,14 +400,14 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
   }
   __syncthreads();
   const float mx = shared_mx;
-  for (int base = 0; base < count; base += 512 * ASV) {
+  for (int base = 0; base < count; base += NT * ASV) {
     if (base > 0) {
 #pragma unroll
-      for (int u = 0; u < ASV; ++u) sv[u] = sc[min(base + tid + 512 * u, count - 1)];
+      for (int u = 0; u < ASV; ++u) sv[u] = sc[min(base + tid + NT * u, count - 1)];
     }
 #pragma unroll
     for (int u = 0; u < ASV; ++u) {
-      const int i = base + tid + 512 * u;
+      const int i = base + tid + NT * u;
       if (i < count) {
         const float d = sv[u] - mx;
         if (i < count4) e4[(i & 3) * rs + (i >> 2)] = vexp(d);
@@ -420,26 +429,28 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
   __syncthreads();
   const float inv = shared_inv;
   if (wave > 0) {
-    for (int c = pw; c < chunks; c += APROD) {
+    for (int it = pw; it < items; it += NP) {
+      const int c = it / H, half = it % H;
       wait_at_least(&used, c - nslot + 1);  // the slot's last chunk has been added
-      float *slot = ring + (c % nslot) * (AC * RR) + lane;
+      float *slot = ring + (c % nslot) * (AC * RR) + half * 16 * RR + lane;
       const int b = min(c * RB + lane, q4 - 1);  // the lane's four-position block (clamped: never added past q4)
       const float p0 = e4[b] * inv, p1 = e4[rs + b] * inv, p2 = e4[2 * rs + b] * inv, p3 = e4[3 * rs + b] * inv;
 #pragma unroll
-      for (int j = 0; j < AC; ++j) {
+      for (int j = 0; j < 16; ++j) {
         const float4 x = va[j];
         slot[j * RR] = (p0 * x.x + p1 * x.y) + (p2 * x.z + p3 * x.w);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0) lds_store(&filled[c % nslot], c + 1);
+      if (lane == 0) lds_store(&filled[c % nslot][half], c + 1);
 #pragma unroll
-      for (int j = 0; j < AC; ++j) va[j] = vn[j];
-      if (c + 2 * APROD < chunks) ATT_FETCH(c + 2 * APROD, vn);  // in flight while the wave waits
+      for (int j = 0; j < 16; ++j) va[j] = vn[j];
+      if (it + 2 * NP < items) ATT_FETCH(it + 2 * NP, vn);  // in flight while the wave waits
     }
   } else {
-    float acc = 0.0f;  // lane j < 16: column j0 + j
+    float acc = 0.0f;  // lane j < AC: column j0 + j
     for (int c = 0; c < chunks; ++c) {
-      wait_at_least(&filled[c % nslot], c + 1);
+#pragma unroll
+      for (int hh = 0; hh < H; ++hh) wait_at_least(&filled[c % nslot][hh], c + 1);
       if (lane < AC) {
         const int nb = min(RP, count4 - c * RP) >> 2;
         const float *row = ring + (c % nslot) * (AC * RR) + lane * RR;
@@ -457,21 +468,29 @@ __global__ __launch_bounds__(512) void attend_kernel(const AttnArgs a, const int
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) lds_store(&used, c + 1);
     }
-    if (lane < AC) {
 #pragma unroll
-      for (int r = 0; r < 3; ++r)
-        if (r < count - count4) acc = acc + (tail[r] * inv) * tv[r];
-      a.out[(int64_t)t * a.out_stride + h * HS + j0 + lane] = acc;
+    for (int r = 0; r < 3; ++r)
+      if (r < count - count4) acc = acc + (tail[r] * inv) * tv[r];
+    const int col = h * HS + j0 + lane;
+    if (lane < AC) a.out[(int64_t)t * a.out_stride + col] = acc;
+    if (AC == 32 && a.xq) {
+      // quantize_x of the group (lanes 0-31): the largest magnitude, scale = amax / qmax, the values
+      const float amax = wave_max32(__builtin_fabsf(acc));
+      const float scale = amax / (a.bias == 0 ? 127.0f : 63.0f);
+      const float qinv = scale > 0 ? 1.0f / scale : 0.0f;
+      if (lane < 32) a.xq[(int64_t)t * a.xq_stride + col] = quant_value(acc, qinv, a.bias);
+      if (lane == 0) a.xs[(int64_t)t * a.xs_stride + col / GS] = scale;
     }
   }
 }
 #undef ATT_FETCH
 
 // LDS bytes of attend_kernel for the largest count of a launch (ring slots into *nslot), 0 where it does not fit
+template <int HS>
 int attend_lds(const AttnArgs &a, int *nslot) {
   const int count = a.pos0 + a.m;
   const int head = (int)sizeof(float) * (4 * chain_rowstride((count & ~3) >> 2) + 4);
-  const int slot = (int)sizeof(float) * AC * RR;
+  const int slot = (int)sizeof(float) * Attend<HS>::AC * RR;
   const int n = std::min(ASLOTS, (ALDS - head) / slot);
   if (n < 2) return 0;
   *nslot = n;
@@ -488,7 +507,7 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   }
   int nslot = 0;
-  const int fused = a.m <= DECODE_TOKENS ? attend_lds(a, &nslot) : 0;
+  const int fused = a.m <= DECODE_TOKENS ? attend_lds<HS>(a, &nslot) : 0;
   if (fused) {
     static bool sized = false;  // once a process: let the kernel take LDS past 64 KiB
     if (!sized) {
@@ -497,9 +516,9 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
       if (e != hipSuccess) return e;
       sized = true;
     }
-    const int groups = a.nkv * (HS / AC), g8 = (groups + 7) & ~7;
-    hipLaunchKernelGGL((attend_kernel<HS, HALF>), dim3(g8 * (a.nh / a.nkv), 1, a.m), dim3(64 * AWAVES), fused, s, a,
-                       nslot);
+    const int groups = a.nkv * (HS / Attend<HS>::AC), g8 = (groups + 7) & ~7;
+    hipLaunchKernelGGL((attend_kernel<HS, HALF>), dim3(g8 * (a.nh / a.nkv), 1, a.m), dim3(Attend<HS>::NT), fused, s,
+                       a, nslot);
     return hipGetLastError();
   }
   const int most4 = (a.pos0 + a.m) & ~3;
@@ -530,6 +549,19 @@ hipError_t launch_half(const AttnArgs &a, hipStream_t s) {
 bool attention_supported(int32_t hs, int32_t nh, int32_t nkv) {
   const bool sizes = hs == 16 || hs == 32 || hs == 48 || hs == 64 || hs == 96 || hs == 128 || hs == 256;
   return sizes && nkv > 0 && nh % nkv == 0 && nh / nkv <= MAXMUL;
+}
+
+bool attention_quantizes(const AttnArgs &a) {
+  if (!attention_supported(a.hs, a.nh, a.nkv) || a.m > DECODE_TOKENS || a.hs % 32) return false;
+  int nslot = 0;
+  switch (a.hs) {
+    case 32: return attend_lds<32>(a, &nslot) > 0;
+    case 64: return attend_lds<64>(a, &nslot) > 0;
+    case 96: return attend_lds<96>(a, &nslot) > 0;
+    case 128: return attend_lds<128>(a, &nslot) > 0;
+    case 256: return attend_lds<256>(a, &nslot) > 0;
+    default: return false;
+  }
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {

@@ -467,12 +467,21 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.seq_len = c.seq_len;
     at.half = c.half_kv;
     at.vstride = qp.vstride;
+    at.xq = e->xq;
+    at.xs = e->xs;
+    at.xq_stride = W;
+    at.xs_stride = W / 32;
+    at.bias = e->bias;
+    const bool quantized = attention_quantizes(at);
+    if (!quantized) at.xq = nullptr;
     double kv_rows = 0;
     for (int32_t t = 0; t < m; ++t) kv_rows += pos0 + t + 1;
     HIP_TRY(timed(e, HE_K_ATTENTION, kv_rows * 2 * kvdim * esz + (double)m * qdim * 8,
                   [&] { return launch_attention(at, s); }));
     const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
-    if (quantizes_itself(e, qdim, m, dim)) {
+    if (quantized) {
+      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
+    } else if (quantizes_itself(e, qdim, m, dim)) {
       const F32Source src{e->xb, nullptr};
       HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs, &src));
     } else {

@@ -242,18 +242,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 // in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
 // out = w * (s * x)), then quantize_x with bias 64 (kernels/kernel.ts:129-156) a half-wave a group, stored centred
 // (q - 64) into xl with the group scales into xsl. Every block computes the same bits. Thread tid takes positions
-// tid + 256 u (group tid / 32 + 8 u), all requested at once. MAXU * 256 >= K; sq: 4 * (K / 4 + 3 & ~3) floats of LDS.
+// tid + 256 u (group tid / 32 + 8 u), requested by load_f32 before the rows. MAXU * 256 >= K; sq: 4 *
+// chain_rowstride(K / 4) floats of LDS.
 template <int MAXU>
-__device__ __forceinline__ void stage_from_f32(const MatArgs &a, uint8_t *xl, float *xsl, float *sq) {
-  __shared__ float part[4], sval;
-  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = chain_rowstride(q4);
-  float xv[MAXU], wv[MAXU];
+__device__ __forceinline__ void load_f32(const MatArgs &a, float (&xv)[MAXU], float (&wv)[MAXU]) {
 #pragma unroll
   for (int u = 0; u < MAXU; ++u) {
-    const int j = min(tid + 256 * u, K - 1);  // clamped: every load unconditional
+    const int j = min((int)threadIdx.x + 256 * u, a.k - 1);  // clamped: every load unconditional
     xv[u] = a.xf[j];
     wv[u] = a.xnorm ? a.xnorm[j] : 1.0f;
   }
+}
+template <int MAXU>
+__device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&xv)[MAXU], const float (&wv)[MAXU],
+                                               uint8_t *xl, float *xsl, float *sq) {
+  __shared__ float part[4], sval;
+  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = chain_rowstride(q4);
   float sc = 1.0f;
   if (a.xnorm) {
 #pragma unroll
@@ -268,15 +272,22 @@ __device__ __forceinline__ void stage_from_f32(const MatArgs &a, uint8_t *xl, fl
     __syncthreads();
     sc = sval;
   }
+  // every group's maximum, scale and values computed unconditionally (positions past K repeat the last one and are
+  // not stored), so that the MAXU half-wave reductions overlap instead of running one after another
+  const bool norm = a.xnorm != nullptr;
+  float o[MAXU], amax[MAXU];
+#pragma unroll
+  for (int u = 0; u < MAXU; ++u) o[u] = norm ? wv[u] * (sc * xv[u]) : xv[u];
+#pragma unroll
+  for (int u = 0; u < MAXU; ++u) amax[u] = wave_max32(__builtin_fabsf(o[u]));
 #pragma unroll
   for (int u = 0; u < MAXU; ++u) {
     const int j = tid + 256 * u;
-    if (j - (tid & 31) < K) {  // whole half-waves (K is a multiple of 32)
-      const float o = a.xnorm ? wv[u] * (sc * xv[u]) : xv[u];
-      const float amax = wave_max32(__builtin_fabsf(o));
-      const float scale = amax / 63.0f;
-      const float inv = scale > 0 ? 1.0f / scale : 0.0f;
-      xl[j] = (uint8_t)(quant_value(o, inv, 64) - 64);
+    const float scale = amax[u] / 63.0f;
+    const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+    const uint8_t q = (uint8_t)(quant_value(o[u], inv, 64) - 64);
+    if (j < K) {  // whole half-waves (K is a multiple of 32)
+      xl[j] = q;
       if ((tid & 31) == 0) xsl[j >> 5] = scale;
     }
   }
@@ -302,20 +313,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const bool holder = (lane & 1) == 0;
   const int half = (lane & 1) * 16;
   const int row0 = min((blockIdx.x * WAVES + wave) * R, a.total_rows - 1);
+  // every load of the block, in the order their uses come: the token's activations (small, staged first), the rows'
+  // scales, the rows (about 16 KiB a wave); unconditional loads from clamped (always valid) addresses, since a load
+  // under a branch is waited for before the next
+  constexpr int XL = (NS * 1024 / 16 + 255) / 256;
+  constexpr int XSV = (NS * 32 + 255) / 256;
+  constexpr int FU = F32 ? NS * 4 : 1;
+  uint4 xv[XL];
+  float sv[XSV];
+  float fx[FU], fw[FU];
+  if constexpr (F32) {
+    static_assert(NS <= 4, "the float32 token is held a thread at a time");
+    load_f32<FU>(a, fx, fw);
+  } else {
+#pragma unroll
+    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
+#pragma unroll
+    for (int u = 0; u < XSV; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
+  }
   uint32_t wr[R][NS][4];
   float4 sr[R][SV];
+  const uint8_t *wrow[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const RowAt at = row_at(a, min(row0 + i, a.total_rows - 1));  // rows past the end: the last again, unused
-    const uint8_t *w = at.w + (int64_t)at.r * K;
+    wrow[i] = at.w + (int64_t)at.r * K;
     const float *ws = at.ws + (int64_t)at.r * G;
-    // unconditional loads from clamped (always valid) addresses: a load under a branch is waited for before the next
-#pragma unroll
-    for (int u = 0; u < NS; ++u) {
-      const int g = min(u * 32 + (lane >> 1), G - 1);
-      const uint4 v = *reinterpret_cast<const uint4 *>(w + (int64_t)g * 32 + half);
-      wr[i][u][0] = v.x; wr[i][u][1] = v.y; wr[i][u][2] = v.z; wr[i][u][3] = v.w;
-    }
     // the row's scales as float4 (a row's scales start 4-byte aligned only: read them one float at a time where
     // the row does not start on 16 bytes)
 #pragma unroll
@@ -328,19 +351,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       }
     }
   }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int g = min(u * 32 + (lane >> 1), G - 1);
+      const uint4 v = *reinterpret_cast<const uint4 *>(wrow[i] + (int64_t)g * 32 + half);
+      wr[i][u][0] = v.x; wr[i][u][1] = v.y; wr[i][u][2] = v.z; wr[i][u][3] = v.w;
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
-  // the block's activations: K / 16 uint4, up to NS * 4 a thread (or made here from the float32 token)
+  // the block's activations into LDS: K / 16 uint4, centred (or made here from the float32 token)
   if constexpr (F32) {
-    static_assert(NS <= 4, "the float32 token is held a thread at a time");
-    stage_from_f32<NS * 4>(a, reinterpret_cast<uint8_t *>(xl), xsl, P - wave * R * lay.stride);
+    stage_from_f32<FU>(a, fx, fw, reinterpret_cast<uint8_t *>(xl), xsl, P - wave * R * lay.stride);
   } else {
-    constexpr int XL = (NS * 1024 / 16 + 255) / 256;
-    uint4 xv[XL];
-    float sv[(NS * 32 + 255) / 256];
-#pragma unroll
-    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
-#pragma unroll
-    for (int u = 0; u < (NS * 32 + 255) / 256; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
 #pragma unroll
     for (int u = 0; u < XL; ++u) {
       const int i = threadIdx.x + 256 * u;
@@ -349,7 +373,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
                                                       centre4(xv[u].w));
     }
 #pragma unroll
-    for (int u = 0; u < (NS * 32 + 255) / 256; ++u) {
+    for (int u = 0; u < XSV; ++u) {
       const int i = threadIdx.x + 256 * u;
       if (i < G) xsl[i] = sv[u];
     }

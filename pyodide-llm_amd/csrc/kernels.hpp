@@ -105,10 +105,17 @@ struct AttnArgs {
   float *scores;  // [m][nh][seq_len]
   float *tilemax; // [m][nh][seq_len / 64 + 1]
   int32_t nh, nkv, hs, pos0, m, seq_len, half, vstride;
+  // where attention_quantizes(): quantize_x(bias) of out as well, [m][xq_stride] and [m][xs_stride] (null: not)
+  int8_t *xq;
+  float *xs;
+  int32_t xq_stride, xs_stride, bias;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the head sizes and grouping the attention kernels take (hs in {16, 32, 48, 64, 96, 128, 256}, nh / nkv <= 8)
 bool attention_supported(int32_t hs, int32_t nh, int32_t nkv);
+// whether launch_attention writes quantize_x of its output too (a.xq): decode launches whose head size is a multiple
+// of 32 (a block holds a whole group) and whose context fits the decode kernel's LDS
+bool attention_quantizes(const AttnArgs &a);
 
 // greedy: the first index of the largest logit into *out (and the value into *value)
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
