@@ -44,6 +44,9 @@ __device__ __forceinline__ float cache1(const void *c, int64_t i) {
   else return reinterpret_cast<const float *>(c)[i];
 }
 
+// the launch's first position: from device memory in a replayed decode step (where a.pos0 only bounds it)
+__device__ __forceinline__ int first_position(const AttnArgs &a) { return a.dpos ? *a.dpos : a.pos0; }
+
 // (A) grid (tiles, nkv, m)
 template <int HS, bool HALF>
 __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
@@ -51,7 +54,7 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   __shared__ float ks[TILE * LD];
   __shared__ float qs[MAXMUL * HS];
   const int tile = blockIdx.x, kh = blockIdx.y, t = blockIdx.z;
-  const int count = a.pos0 + t + 1;
+  const int count = first_position(a) + t + 1;
   const int p0 = tile * TILE;
   if (p0 >= count) return;
   const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
@@ -112,10 +115,10 @@ __global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
   const int tile = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mul = a.nh / a.nkv, tt_n = max(1, SROWS / mul);
   const int t0 = blockIdx.z * tt_n, last = min(t0 + tt_n, a.m) - 1;
-  const int p0 = tile * TILE;
-  if (p0 >= a.pos0 + last + 1) return;  // past every token of the block (uniform: before any barrier)
+  const int p0 = tile * TILE, pos0 = first_position(a);
+  if (p0 >= pos0 + last + 1) return;  // past every token of the block (uniform: before any barrier)
   const int kvdim = a.nkv * HS;
-  const int np = min(TILE, a.pos0 + last + 1 - p0);  // positions any token of the block reaches
+  const int np = min(TILE, pos0 + last + 1 - p0);  // positions any token of the block reaches
   // keys: TILE * C4 float4, and the rows' queries: SROWS * C4 float4, requested together (clamped, unconditional)
   constexpr int NK = TILE * C4 / 256, NQ = (SROWS * C4 + 255) / 256;
   float4 kr[NK], qr[NQ];
@@ -162,7 +165,7 @@ __global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
   for (int u = 0; u < 8; ++u) {
     const int r = wave + 4 * u, tt = r / mul, hl = r % mul, t = t0 + tt;
     const bool row = tt < tt_n && t < a.m;  // uniform over the wave
-    const int count = a.pos0 + min(t, a.m - 1) + 1;
+    const int count = first_position(a) + min(t, a.m - 1) + 1;
     float sc = -__builtin_inff();
     if (row && p0 + lane < count) {
       sc = ((l[u][0] + l[u][2]) + (l[u][1] + l[u][3])) * isq;
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   __shared__ float part[4];
   __shared__ float shared_mx, shared_inv;
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = chain_rowstride(q4);
+  const int count = first_position(a) + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = chain_rowstride(q4);
   const int tiles = (count + TILE - 1) / TILE;
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
@@ -250,9 +253,9 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
   const int j = tid % COLS, hl = (tid / COLS) % mul, tt = tid / (COLS * mul);
   const bool chain = tt < tt_n && t0 + tt < a.m;
   const int t = min(t0 + tt, a.m - 1);
-  const int count = a.pos0 + t + 1, count4 = count & ~3;
+  const int pos0 = first_position(a), count = pos0 + t + 1, count4 = count & ~3;
   const int last = min(t0 + tt_n, a.m) - 1;  // the block's last token reads the most positions
-  const int most4 = (a.pos0 + last + 1) & ~3;
+  const int most4 = (pos0 + last + 1) & ~3;
   const int chunks = (most4 + TPC - 1) / TPC;
   const int rows = (last - t0 + 1) * mul;  // weight rows of the block
   float4 v[VPT], w[WPT];
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a
   if (g >= groups) return;  // the grid's rounding up: whole blocks leave
   const int kh = g / S, j0 = (g % S) * AC, h = kh * mul + hl;
   const int t = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, pw = wave - 1;
-  const int count = a.pos0 + t + 1, count4 = count & ~3, q4 = count4 >> 2, rs = chain_rowstride(q4);
+  const int count = first_position(a) + t + 1, count4 = count & ~3, q4 = count4 >> 2, rs = chain_rowstride(q4);
   float *const e4 = lds;              // [4][rs]
   float *const tail = lds + 4 * rs;   // [4]
   float *const ring = tail + 4;       // [nslot][AC][RR]

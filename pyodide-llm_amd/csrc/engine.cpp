@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -118,6 +119,16 @@ struct he_engine {
   int32_t *best_i = nullptr;
   uint64_t device_bytes = 0;
   bool have_logits = false;
+  // greedy decode steps replayed from one captured graph of a whole step (embedding to argmax), which reads its token
+  // (tokens[0]) and position (state[0]) from device memory and advances them itself
+  int32_t *state = nullptr;                           // [0] position, [1] step of the round
+  int32_t *step_ids = nullptr;                        // [STEPS_A_ROUND] tokens of a round
+  float *step_values = nullptr;                       // their logits
+  int32_t *host_ids = nullptr, *host_state = nullptr;  // pinned
+  float *host_values = nullptr;                       // pinned
+  hipGraphExec_t graph = nullptr;
+  bool graph_tried = false;
+  bool replayable = false;  // run_chunk is building the graph (positions from state, no host copies)
   // he_profile_forward: event pairs around every launch while `profiling` is set
   struct Mark {
     int kind;
@@ -141,13 +152,19 @@ struct he_engine {
 
 namespace {
 
+constexpr int32_t STEPS_A_ROUND = 64;  // replayed steps between two reads of their tokens
+
 void destroy(he_engine *e) {
   if (!e) return;
+  if (e->graph) (void)hipGraphExecDestroy(e->graph);
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
-                  e->best_v, e->best_i};
+                  e->best_v, e->best_i, e->state, e->step_ids, e->step_values};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
+  void *pinned[] = {e->host_ids, e->host_state, e->host_values};
+  for (void *p : pinned)
+    if (p) (void)hipHostFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -268,7 +285,13 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->amax_i, sizeof(int32_t) * 256);
   ALLOC(e->best_v, sizeof(float) * 4);
   ALLOC(e->best_i, sizeof(int32_t) * 4);
+  ALLOC(e->state, sizeof(int32_t) * 4);
+  ALLOC(e->step_ids, sizeof(int32_t) * STEPS_A_ROUND);
+  ALLOC(e->step_values, sizeof(float) * STEPS_A_ROUND);
 #undef ALLOC
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_ids), sizeof(int32_t) * STEPS_A_ROUND));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_values), sizeof(float) * STEPS_A_ROUND));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_state), sizeof(int32_t) * 4));
   return HE_OK;
 }
 
@@ -406,7 +429,8 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
   const int32_t dim = c.dim, hidden = c.hidden_dim, qdim = e->qdim, kvdim = e->kvdim, hs = c.head_size;
   const int32_t W = e->widest;
   const size_t esz = c.half_kv ? 2 : 4;
-  HIP_TRY(hipMemcpyAsync(e->tokens, tokens, sizeof(int32_t) * m, hipMemcpyHostToDevice, s));
+  const int32_t *dpos = e->replayable ? e->state : nullptr;  // a replayed step: the position in device memory
+  if (!e->replayable) HIP_TRY(hipMemcpyAsync(e->tokens, tokens, sizeof(int32_t) * m, hipMemcpyHostToDevice, s));
   HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * dim * (c.six ? 0.75 + 0.125 + 4 : 1 + 0.125 + 4), [&] {
     return launch_embed(e->x, e->tokens, e->values[HE_T_EMBEDDING], e->scales[HE_T_EMBEDDING], m, dim, dim,
                         c.six ? 32 : group_size(dim), c.six, s);
@@ -436,6 +460,7 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     qp.m = m;
     qp.half = c.half_kv;
     qp.vstride = value_stride(c.seq_len);
+    qp.dpos = dpos;
     HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
       return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
                                   W, W / 32, 0, c.rms_norm_eps, e->bias, s);
@@ -443,7 +468,7 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     if (m == 1 && decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0)) {
       // one token: the q/k/v GEMV adds the biases, rotates q and k and writes k and v into the cache itself
       const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv,
-                         qp.vstride};
+                         qp.vstride, dpos};
       HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, nullptr, &fuse));
     } else {
       HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
@@ -467,6 +492,7 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.seq_len = c.seq_len;
     at.half = c.half_kv;
     at.vstride = qp.vstride;
+    at.dpos = dpos;
     at.xq = e->xq;
     at.xs = e->xs;
     at.xq_stride = W;
@@ -612,27 +638,102 @@ int32_t he_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int3
   return HE_OK;
 }
 
+namespace {
+// the graph of one greedy decode step (the caller has run at least one step eagerly, so that every launch's one-time
+// set-up is done): captured with positions bounded by seq_len - 1 and read from state[0]
+void build_graph(he_engine *e) {
+  e->graph_tried = true;
+  // PYODIDE_LLM_HIP_GRAPH=0 keeps every step eager (a kernel-trace profiler that does not follow graph launches)
+  const char *env = std::getenv("PYODIDE_LLM_HIP_GRAPH");
+  if (env && env[0] == '0') return;
+  hipGraph_t g = nullptr;
+  e->replayable = true;
+  hipError_t err = hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal);
+  int32_t rc = HE_OK;
+  if (err == hipSuccess) {
+    rc = run_chunk(e, nullptr, 1, e->c.seq_len - 1, true);
+    if (rc == HE_OK) {
+      hipError_t le = launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream);
+      if (le == hipSuccess)
+        le = launch_advance(e->tokens, e->state, e->best_i, e->best_v, e->step_ids, e->step_values, e->stream);
+      if (le != hipSuccess) rc = HE_E_HIP;
+    }
+    const hipError_t end = hipStreamEndCapture(e->stream, &g);
+    if (err == hipSuccess) err = end;
+  }
+  e->replayable = false;
+  if (err == hipSuccess && rc == HE_OK && g) err = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (err != hipSuccess || rc != HE_OK) {
+    e->graph = nullptr;  // the steps stay eager
+    (void)hipGetLastError();
+  }
+}
+
+// one eager greedy step: its token into *best and the largest logit into *value
+int32_t eager_step(he_engine *e, int32_t token, int32_t pos, int32_t *best, float *value) {
+  int32_t rc = run_tokens(e, &token, 1, pos, true);
+  if (rc) return rc;
+  HIP_TRY(launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream));
+  HIP_TRY(hipMemcpyAsync(best, e->best_i, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipMemcpyAsync(value, e->best_v, sizeof(float), hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  return HE_OK;
+}
+}  // namespace
+
 int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, int32_t count, const int32_t *stops,
                          int32_t n_stops, int32_t *ids, int32_t *n_ids) {
   if (!e || !ids || !n_ids) return fail(HE_E_ARG, "a required pointer is null");
   if (count < 1) return fail(HE_E_ARG, "count must be at least 1");
   if ((int64_t)pos + count > e->c.seq_len) return fail(HE_E_STATE, "the steps run past the context (seq_len)");
+  if (token < 0 || token >= e->c.vocab_size) return fail(HE_E_ARG, "a token is outside the vocabulary");
   *n_ids = 0;
-  for (int32_t i = 0; i < count; ++i) {
-    int32_t rc = run_tokens(e, &token, 1, pos + i, true);
-    if (rc) return rc;
-    HIP_TRY(launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream));
+  auto is_stop = [&](int32_t id) {
+    for (int32_t j = 0; j < n_stops; ++j)
+      if (stops[j] == id) return true;
+    return false;
+  };
+  int32_t done = 0;
+  // eager steps until the graph exists (the first step of an engine's first call builds it)
+  while (done < count && !e->graph) {
     int32_t best = 0;
     float value = 0.0f;
-    HIP_TRY(hipMemcpyAsync(&best, e->best_i, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
-    HIP_TRY(hipMemcpyAsync(&value, e->best_v, sizeof(float), hipMemcpyDeviceToHost, e->stream));
-    HIP_TRY(hipStreamSynchronize(e->stream));
+    const int32_t rc = eager_step(e, token, pos + done, &best, &value);
+    if (rc) return rc;
     if (!std::isfinite(value)) return fail(HE_E_NOTFINITE, "the largest logit is not finite");
     ids[(*n_ids)++] = best;
     token = best;
-    bool stop = false;
-    for (int32_t j = 0; j < n_stops; ++j) stop = stop || stops[j] == best;
-    if (stop) break;
+    ++done;
+    if (is_stop(best)) return HE_OK;
+    if (!e->graph_tried) build_graph(e);
+  }
+  // replayed steps, a round of up to STEPS_A_ROUND at a time: without stop tokens the round runs back to back and its
+  // tokens are read once at its end; with them, each step's token is read before the next step starts
+  while (done < count) {
+    const int32_t n = std::min(STEPS_A_ROUND, count - done);
+    e->host_state[0] = token;
+    e->host_state[1] = pos + done;
+    e->host_state[2] = 0;
+    HIP_TRY(hipMemcpyAsync(e->tokens, e->host_state, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
+    HIP_TRY(hipMemcpyAsync(e->state, e->host_state + 1, 2 * sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
+    for (int32_t i = 0; i < n; ++i) {
+      HIP_TRY(hipGraphLaunch(e->graph, e->stream));
+      if (n_stops == 0 && i + 1 < n) continue;
+      const int32_t from = n_stops == 0 ? 0 : i, k = i + 1 - from;
+      HIP_TRY(hipMemcpyAsync(e->host_ids + from, e->step_ids + from, sizeof(int32_t) * k, hipMemcpyDeviceToHost,
+                             e->stream));
+      HIP_TRY(hipMemcpyAsync(e->host_values + from, e->step_values + from, sizeof(float) * k, hipMemcpyDeviceToHost,
+                             e->stream));
+      HIP_TRY(hipStreamSynchronize(e->stream));
+      for (int32_t j = from; j <= i; ++j) {
+        if (!std::isfinite(e->host_values[j])) return fail(HE_E_NOTFINITE, "the largest logit is not finite");
+        ids[(*n_ids)++] = e->host_ids[j];
+        if (is_stop(e->host_ids[j])) return HE_OK;
+      }
+    }
+    token = ids[*n_ids - 1];
+    done += n;
   }
   return HE_OK;
 }

@@ -65,7 +65,9 @@ __device__ __forceinline__ void store_row(const MatArgs &a, int row, float sum, 
   // (every field read by value: a reference into the kernel's argument struct makes the compiler copy it to scratch)
   const float *bq = a.qkv.bq, *bk = a.qkv.bk, *bv = a.qkv.bv, *cos_t = a.qkv.cos_t, *sin_t = a.qkv.sin_t;
   void *kcache = a.qkv.kcache, *vcache = a.qkv.vcache;
-  const int pos = a.qkv.pos, hs = a.qkv.hs, kvdim = a.qkv.kvdim, half = a.qkv.half, vstride = a.qkv.vstride;
+  const int32_t *dpos = a.qkv.dpos;
+  const int pos = dpos ? *dpos : a.qkv.pos, hs = a.qkv.hs, kvdim = a.qkv.kvdim, half = a.qkv.half;
+  const int vstride = a.qkv.vstride;
   const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
   const int seg = row < n0 ? 0 : (row < n0 + n1 ? 1 : 2), r = at.r;
   const float *bias = seg == 0 ? bq : (seg == 1 ? bk : bv);

@@ -31,6 +31,7 @@ struct QkvFuse {
   const float *cos_t, *sin_t;  // [seq_len][hs/2]
   void *kcache, *vcache;       // this layer's keys [seq_len][kv_dim] and values [kv_dim][vstride]
   int32_t pos, hs, kvdim, half, vstride;
+  const int32_t *dpos;  // the position in device memory (a replayed decode step), or null: pos
 };
 
 struct MatArgs {
@@ -92,6 +93,7 @@ struct QkvPost {
   const float *cos_t, *sin_t;  // [seq_len][hs/2]
   void *kcache, *vcache;       // this layer's keys [seq_len][kv_dim] and values [kv_dim][vstride]
   int32_t nh, nkv, hs, pos0, m, half, vstride;
+  const int32_t *dpos;  // the first position in device memory (a replayed decode step), or null: pos0
 };
 hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s);
 
@@ -105,6 +107,9 @@ struct AttnArgs {
   float *scores;  // [m][nh][seq_len]
   float *tilemax; // [m][nh][seq_len / 64 + 1]
   int32_t nh, nkv, hs, pos0, m, seq_len, half, vstride;
+  // the first position in device memory (a replayed decode step), or null: pos0; with it, pos0 is only the largest
+  // first position the launch may see (grid and LDS sizes)
+  const int32_t *dpos;
   // where attention_quantizes(): quantize_x(bias) of out as well, [m][xq_stride] and [m][xs_stride] (null: not)
   int8_t *xq;
   float *xs;
@@ -120,6 +125,10 @@ bool attention_quantizes(const AttnArgs &a);
 // greedy: the first index of the largest logit into *out (and the value into *value)
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
                          hipStream_t s);
+// the end of a replayed decode step: its token and value into ids / values at state[1], the token as the next step's
+// input (tokens[0]), state[0] (the position) and state[1] (the step) advanced
+hipError_t launch_advance(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
+                          float *values, hipStream_t s);
 
 // device synthesis of a checkpoint (the oracle's or_synth_checkpoint bits)
 hipError_t launch_synth_matrix(uint8_t *values, float *scales, int64_t rows, int32_t k, uint64_t seed, int32_t stream,

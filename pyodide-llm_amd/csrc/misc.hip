@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void embed_kernel(float *x, const int32_t *tok
 // per token: bias (q, k, v), rope on q and k at its position, k and v into the cache
 __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPost a) {
   const int t = blockIdx.y;
-  const int pos = a.pos0 + t;
+  const int pos = (a.dpos ? *a.dpos : a.pos0) + t;
   const int qdim = a.nh * a.hs, kvdim = a.nkv * a.hs, half = a.hs / 2;
   float *q = a.q + (int64_t)t * a.q_stride, *k = a.k + (int64_t)t * a.kv_stride, *v = a.v + (int64_t)t * a.kv_stride;
   const float *cs = a.cos_t + (int64_t)pos * half, *sn = a.sin_t + (int64_t)pos * half;
@@ -336,6 +336,22 @@ hipError_t launch_embed(float *x, const int32_t *tokens, const uint8_t *table, c
 hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s) {
   const int64_t items = (int64_t)(a.nh * a.hs + a.nkv * a.hs) / 2 + a.nkv * a.hs;
   hipLaunchKernelGGL(qkv_post_kernel, dim3(blocks_for(items, 256, 64), a.m), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+__global__ void advance_kernel(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
+                               float *values) {
+  const int32_t step = state[1], b = *best;
+  ids[step] = b;
+  values[step] = *value;
+  tokens[0] = b;
+  state[0] = state[0] + 1;
+  state[1] = step + 1;
+}
+
+hipError_t launch_advance(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
+                          float *values, hipStream_t s) {
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, tokens, state, best, value, ids, values);
   return hipGetLastError();
 }
 

@@ -174,3 +174,44 @@ def test_prompt_in_small_pieces_equals_one_at_a_time(piece):
     assert same_bits(one.logits(), many.logits())
     a, b = one.keysAndValues(0, len(tokens)), many.keysAndValues(0, len(tokens))
     assert same_bits(a["keys"], b["keys"]) and same_bits(a["values"], b["values"])
+
+
+@pytest.mark.parametrize("name", sorted(MODELS))
+def test_replayed_steps_with_stops_and_eager_steps_between(name):
+    """generateMany's replayed decode steps (one captured step graph): a stop token ends a call at the right step with
+    that step's logits; eager steps between calls; a later call without stops runs its steps back to back. Every token
+    and the logits of every call's last step against the oracle's greedy steps, to the bit."""
+    cfg, tensors, ck, cos, sin, _ = build(name)
+    rng = np.random.default_rng(4)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=20)]
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    ref.run(prompt[:-1], 0, False)
+    want, logits = [], []
+    tok, pos = prompt[-1], len(prompt) - 1
+    for _ in range(26):
+        ref.run([tok], pos, True)
+        lg = ref.logits()
+        tok, pos = int(np.argmax(lg)), pos + 1
+        want.append(tok)
+        logits.append(lg)
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    eng.forwardMany(prompt[:-1], 0)
+    p0 = len(prompt) - 1
+    # a stop token: the first call ends at the step that produced it (want[6] may also appear earlier)
+    stop = want[6]
+    first = want.index(stop)
+    ids = eng.generateMany(prompt[-1], p0, [], 0, 12, 0.0, 0.9, 1.0, [], [stop])
+    assert ids == want[:first + 1]
+    assert same_bits(eng.logits(), logits[first])
+    n = len(ids)
+    # an eager step, then replayed steps without stops, twice
+    eng.forward(ids[-1], p0 + n, True)
+    assert same_bits(eng.logits(), logits[n])
+    done = n + 1
+    for count in (7, 16 - n):
+        got = eng.generateMany(want[done - 1], p0 + done, [], 0, count, 0.0, 0.9, 1.0, [], [])
+        assert got == want[done:done + count]
+        assert same_bits(eng.logits(), logits[done + count - 1])
+        done += count
+    eng.release()
