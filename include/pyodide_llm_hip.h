@@ -106,13 +106,23 @@ int32_t he_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits
  * every token's numbers are those he_forward gives it alone. count <= he_prompt_block(e). */
 int32_t he_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos);
 
-/* engine.generateMany (public/forward.js:1837-1890) for greedy decoding (temperature 0): `count` steps from token at
- * pos, each the forward pass with logits and the first index of the largest logit (kernels/kernel.ts:695-699).
+/* engine.generateMany(token, pos, history, length, count, temperature, topp, penalty, randoms, stops)
+ * (public/forward.js:1831-1890): up to `count` steps from token at pos, each the forward pass with logits, then the
+ * repetition penalty where penalty != 1 (kernels/kernel.ts:705-719, over the distinct tokens of the latest 64 of
+ * history[0..n_history) followed by the tokens this call has chosen; history ends with `token`, as the caller's
+ * history does; `length` is the caller's full history length, kept for the interface), then the next token: with
+ * temperature 0 the first index of the largest logit (public/llama2_numpy.py:1521-1527), else a draw from the
+ * temperature-scaled logits restricted to the nucleus where 0 < topp < 1 (kernels/kernel.ts:803-868) with randoms[i]
+ * for step i (n_randoms >= count; the caller's generator's numbers in [0, 1)).
  * ids receives the tokens chosen, a stop token last where one came; *n_ids their number. The logits of the last step
- * stay readable with he_logits. Returns HE_E_NOTFINITE where a step's largest logit is not finite (nothing of that
- * step is in ids). */
-int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, int32_t count, const int32_t *stops,
-                         int32_t n_stops, int32_t *ids, int32_t *n_ids);
+ * (penalized where the penalty applied) stay readable with he_logits. Returns HE_E_NOTFINITE where a step's largest
+ * logit is not finite (nothing of that step is in ids). *n_ids may be less than count without a stop token where a
+ * step's nucleus holds more tokens than the device sorts (more than 8192): the caller takes that step itself, and
+ * *n_ids = 0 is the reference's "the GPU did not take them" (undefined). */
+int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, const int32_t *history, int32_t n_history,
+                         int32_t length, int32_t count, float temperature, float topp, float penalty,
+                         const double *randoms, int32_t n_randoms, const int32_t *stops, int32_t n_stops, int32_t *ids,
+                         int32_t *n_ids);
 
 /* engine.logits() (public/forward.js:1936): the logits of the last step with logits, vocab_size floats (host). */
 int32_t he_logits(he_engine *e, float *out);
@@ -180,6 +190,16 @@ int32_t hk_matmul(void *y, const void *xq, const void *xs, const void *w, const 
  * gemm = 0 uses the GEMV loader, 1 the MFMA GEMM's. */
 int32_t hk_group_sums(void *s, const void *xq, const void *w, int32_t m, int32_t rows, int32_t k, int32_t bias,
                       int32_t six, int32_t gemm, void *stream);
+
+/* kernels/kernel.ts:705-719 penalize on device logits (n floats): each distinct token of tokens[0..count) (host,
+ * count <= 64, every token in [0, n)) once, value > 0 ? value / penalty : value * penalty. Blocks until done. */
+int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t count, float penalty, void *stream);
+
+/* kernels/kernel.ts:803-868 sample on device logits (n floats): the token drawn for random in [0, 1) into *token
+ * (host): -1 where the largest logit is not finite, -2 where the nucleus holds more than 8192 tokens. temperature
+ * > 0. Blocks until done. */
+int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
+                  void *stream);
 
 #ifdef __cplusplus
 }

@@ -18,7 +18,11 @@
  *       rope_tables() golden vectors;
  *   or_places      : golden plans written by the reference's external_tensors();
  *   or_model_run   : blocks equal one-at-a-time to the bit (tests/forward-check.mjs:438-452), and the reference's
- *       NumPy forward on a tiny model (golden logits) within the int8 line of tests/test_quantize.py:81-90.
+ *       NumPy forward on a tiny model (golden logits) within the int8 line of tests/test_quantize.py:81-90;
+ *   or_penalize, or_sample : the reference's sampler tests restated (tests/test_sample.py: the drawn set is the
+ *       float64 top-p set, a peaked distribution, a low temperature, the penalty's values and window, logits that
+ *       are not finite), and the draws of a float64 restatement of NumPy's Llama.sample
+ *       (public/llama2_numpy.py:1529-1563) away from its boundaries (tests/smoke.mjs:176-272 holds the kernel to it).
  */
 #include "oracle.h"
 
@@ -488,6 +492,100 @@ int32_t or_argmax(const float *x, int32_t n) {
       mi = j;
     }
   return mi;
+}
+
+/* ------------------------------------------------------------------------------------------------ sampling */
+
+/* kernels/kernel.ts:705-719 penalize: each distinct token of tokens[0..count) once (a later repeat is skipped),
+ * value > 0 ? value / penalty : value * penalty */
+void or_penalize(float *logits, const int32_t *tokens, int32_t count, float penalty) {
+  for (int32_t i = 0; i < count; i++) {
+    int32_t seen = 0;
+    for (int32_t j = 0; j < i; j++)
+      if (tokens[j] == tokens[i]) {
+        seen = 1;
+        break;
+      }
+    if (seen) continue;
+    const float v = logits[tokens[i]];
+    logits[tokens[i]] = v > 0 ? v / penalty : v * penalty;
+  }
+}
+
+static const float *sort_probs;  /* the nucleus sort's keys (qsort has no context argument) */
+static const int32_t *sort_index;
+static int nucleus_order(const void *a, const void *b) {
+  const int32_t x = *(const int32_t *)a, y = *(const int32_t *)b;
+  if (sort_probs[x] != sort_probs[y]) return sort_probs[x] > sort_probs[y] ? -1 : 1;
+  return sort_index[x] < sort_index[y] ? -1 : (sort_index[x] > sort_index[y] ? 1 : 0);
+}
+
+/* kernels/kernel.ts:803-868 sample, with largest (:423-445) and the nucleus of sortNucleus/intoNucleus (:729-787):
+ *   best = the largest logit (a NaN anywhere gives NaN); -1 unless it is finite;
+ *   nucleus = 0 < topp < 1; floor = nucleus ? best - temperature * 16.118095 : -FLT_MAX;
+ *   kept, in index order: (v - best, i) for every v >= floor;
+ *   p = vexp((v - best) * f32(1 / temperature)) for the first 4 * floor(count / 4), fexp((v - best) / temperature)
+ *     for the rest; total = the float64 sum in that order, top = the largest p;
+ *   nucleus: cutoff = min((1 - topp) / max(count - 1, 1) * total, top) (float64); the kept p >= cutoff sorted from
+ *     the most probable, their float64 running sum up to the first >= topp * total (the last taken, the mass);
+ *   the first token whose running float64 sum passes random * mass, else the last.
+ * Equal probabilities in the nucleus go in index order: kernel.ts's quicksort takes them in no set order (either is
+ * its distribution, public/shaders.js:3290-3292), and public/shaders.js's sampleLikeCpu takes index order.
+ * probs and index: scratch of n each; order: scratch of n ints. */
+int32_t or_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
+                  int32_t *index, int32_t *order) {
+  float best = logits[0];
+  for (int32_t i = 0; i < n; i++) best = wmax(best, logits[i]);
+  if (!isfinite(best)) return -1;
+  const int nucleus = topp > 0 && topp < 1;
+  const float floor_ = nucleus ? best - temperature * 16.118095f : -3.4028234663852886e38f;
+  int32_t count = 0;
+  for (int32_t i = 0; i < n; i++)
+    if (logits[i] >= floor_) {
+      probs[count] = logits[i] - best;
+      index[count] = i;
+      count++;
+    }
+  const float inverse = 1.0f / temperature;
+  const int32_t simd = count & ~3;
+  for (int32_t k = 0; k < count; k++) probs[k] = k < simd ? vexp1(probs[k] * inverse) : or_fexp(probs[k] / temperature);
+  double total = 0;
+  float top = 0;
+  for (int32_t k = 0; k < count; k++) {
+    total += probs[k];
+    top = fmaxf(top, probs[k]);
+  }
+  int32_t last = count - 1;
+  double mass = total;
+  for (int32_t k = 0; k < count; k++) order[k] = k;
+  if (nucleus) {
+    const double ceiling = (1.0 - (double)topp) / (double)(count > 1 ? count - 1 : 1) * total;
+    const double cutoff = ceiling < (double)top ? ceiling : (double)top;
+    int32_t likely = 0;
+    for (int32_t k = 0; k < count; k++)
+      if ((double)probs[k] >= cutoff) order[likely++] = k;
+    sort_probs = probs;
+    sort_index = index;
+    qsort(order, (size_t)likely, sizeof(int32_t), nucleus_order);
+    const double limit = (double)topp * total;
+    double sum = 0;
+    last = likely - 1;
+    for (int32_t k = 0; k < likely; k++) {
+      sum += probs[order[k]];
+      if (sum >= limit) {
+        last = k;
+        break;
+      }
+    }
+    mass = sum;
+  }
+  const double target = random * mass;
+  double cumulative = 0;
+  for (int32_t k = 0; k <= last; k++) {
+    cumulative += probs[order[k]];
+    if (cumulative > target) return index[order[k]];
+  }
+  return index[order[last]];
 }
 
 /* ------------------------------------------------------------------------------------------------ attention */

@@ -56,6 +56,9 @@ void or_vexp(float *x, int32_t n);
 void or_swiglu(float *out, const float *h1, const float *h3, int32_t n);
 void or_add(float *x, const float *y, int32_t n);
 int32_t or_argmax(const float *x, int32_t n);
+void or_penalize(float *logits, const int32_t *tokens, int32_t count, float penalty);
+int32_t or_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
+                  int32_t *index, int32_t *order);
 
 /* ---- the checkpoint ---- */
 int64_t or_places(const he_config *cfg, he_tensor *tensors);

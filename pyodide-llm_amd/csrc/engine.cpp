@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -128,6 +129,11 @@ struct he_engine {
   float *host_values = nullptr;                       // pinned
   hipGraphExec_t graph = nullptr;
   bool graph_tried = false;
+  // sampled steps: the sampler's scratch, the penalty's window, the token drawn (device); the window (pinned)
+  float *sample_probs = nullptr;
+  int32_t *sample_index = nullptr, *window = nullptr, *sample_token = nullptr;
+  float *sample_best = nullptr;
+  int32_t *host_window = nullptr;
   bool replayable = false;  // run_chunk is building the graph (positions from state, no host copies)
   // he_profile_forward: event pairs around every launch while `profiling` is set
   struct Mark {
@@ -152,17 +158,19 @@ struct he_engine {
 
 namespace {
 
-constexpr int32_t STEPS_A_ROUND = 64;  // replayed steps between two reads of their tokens
+constexpr int32_t STEPS_A_ROUND = 64;      // replayed steps between two reads of their tokens
+constexpr int32_t REPETITION_WINDOW = 64;  // the penalty's latest tokens (public/llama2_numpy.py:545)
 
 void destroy(he_engine *e) {
   if (!e) return;
   if (e->graph) (void)hipGraphExecDestroy(e->graph);
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
-                  e->best_v, e->best_i, e->state, e->step_ids, e->step_values};
+                  e->best_v, e->best_i, e->state, e->step_ids, e->step_values, e->sample_probs, e->sample_index,
+                  e->window, e->sample_token, e->sample_best};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
-  void *pinned[] = {e->host_ids, e->host_state, e->host_values};
+  void *pinned[] = {e->host_ids, e->host_state, e->host_values, e->host_window};
   for (void *p : pinned)
     if (p) (void)hipHostFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -288,10 +296,16 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->state, sizeof(int32_t) * 4);
   ALLOC(e->step_ids, sizeof(int32_t) * STEPS_A_ROUND);
   ALLOC(e->step_values, sizeof(float) * STEPS_A_ROUND);
+  ALLOC(e->sample_probs, sizeof(float) * c.vocab_size);
+  ALLOC(e->sample_index, sizeof(int32_t) * c.vocab_size);
+  ALLOC(e->window, sizeof(int32_t) * REPETITION_WINDOW);
+  ALLOC(e->sample_token, sizeof(int32_t) * 4);
+  ALLOC(e->sample_best, sizeof(float) * 4);
 #undef ALLOC
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_ids), sizeof(int32_t) * STEPS_A_ROUND));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_values), sizeof(float) * STEPS_A_ROUND));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_state), sizeof(int32_t) * 4));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_window), sizeof(int32_t) * REPETITION_WINDOW));
   return HE_OK;
 }
 
@@ -682,20 +696,73 @@ int32_t eager_step(he_engine *e, int32_t token, int32_t pos, int32_t *best, floa
 }
 }  // namespace
 
-int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, int32_t count, const int32_t *stops,
-                         int32_t n_stops, int32_t *ids, int32_t *n_ids) {
+namespace {
+// sampled (or penalized greedy) steps, one at a time: forward, penalty, the draw, the token read back
+int32_t sampled_steps(he_engine *e, int32_t token, int32_t pos, const int32_t *history, int32_t n_history,
+                      int32_t count, float temperature, float topp, float penalty, const double *randoms,
+                      const std::function<bool(int32_t)> &is_stop, int32_t *ids, int32_t *n_ids) {
+  std::vector<int32_t> window(history + std::max(0, n_history - REPETITION_WINDOW), history + n_history);
+  for (int32_t i = 0; i < count; ++i) {
+    int32_t rc = run_tokens(e, &token, 1, pos + i, true);
+    if (rc) return rc;
+    if (penalty != 1.0f && !window.empty()) {
+      const int32_t w = (int32_t)window.size();
+      std::memcpy(e->host_window, window.data(), sizeof(int32_t) * w);
+      HIP_TRY(hipMemcpyAsync(e->window, e->host_window, sizeof(int32_t) * w, hipMemcpyHostToDevice, e->stream));
+      HIP_TRY(launch_penalize(e->logits, e->window, w, penalty, e->stream));
+    }
+    if (temperature == 0.0f) {
+      HIP_TRY(launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream));
+      HIP_TRY(hipMemcpyAsync(e->host_ids, e->best_i, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+      HIP_TRY(hipMemcpyAsync(e->host_values, e->best_v, sizeof(float), hipMemcpyDeviceToHost, e->stream));
+    } else {
+      HIP_TRY(launch_sample(e->logits, e->c.vocab_size, temperature, topp, randoms[i], e->sample_probs,
+                            e->sample_index, e->sample_token, e->sample_best, e->stream));
+      HIP_TRY(hipMemcpyAsync(e->host_ids, e->sample_token, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
+      HIP_TRY(hipMemcpyAsync(e->host_values, e->sample_best, sizeof(float), hipMemcpyDeviceToHost, e->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    const int32_t chosen = e->host_ids[0];
+    if (!std::isfinite(e->host_values[0]) || chosen == SAMPLE_NOT_FINITE)
+      return fail(HE_E_NOTFINITE, "the largest logit is not finite");
+    if (chosen == SAMPLE_DECLINED) return HE_OK;  // the caller takes this step (nothing of it in ids)
+    ids[(*n_ids)++] = chosen;
+    token = chosen;
+    window.push_back(chosen);
+    if ((int32_t)window.size() > REPETITION_WINDOW) window.erase(window.begin());
+    if (is_stop(chosen)) return HE_OK;
+  }
+  return HE_OK;
+}
+}  // namespace
+
+int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, const int32_t *history, int32_t n_history,
+                         int32_t length, int32_t count, float temperature, float topp, float penalty,
+                         const double *randoms, int32_t n_randoms, const int32_t *stops, int32_t n_stops, int32_t *ids,
+                         int32_t *n_ids) {
+  (void)length;
   if (!e || !ids || !n_ids) return fail(HE_E_ARG, "a required pointer is null");
   if (count < 1) return fail(HE_E_ARG, "count must be at least 1");
   if ((int64_t)pos + count > e->c.seq_len) return fail(HE_E_STATE, "the steps run past the context (seq_len)");
   if (token < 0 || token >= e->c.vocab_size) return fail(HE_E_ARG, "a token is outside the vocabulary");
+  if (n_history < 0 || (n_history > 0 && !history)) return fail(HE_E_ARG, "history is null");
+  for (int32_t i = std::max(0, n_history - REPETITION_WINDOW); i < n_history; ++i)
+    if (history[i] < 0 || history[i] >= e->c.vocab_size) return fail(HE_E_ARG, "a history token is outside the vocabulary");
+  if (!(temperature >= 0.0f) || !std::isfinite(temperature)) return fail(HE_E_ARG, "temperature must be finite, >= 0");
+  if (!(penalty > 0.0f) || !std::isfinite(penalty)) return fail(HE_E_ARG, "penalty must be finite, > 0");
+  if (temperature > 0.0f && (!randoms || n_randoms < count)) return fail(HE_E_ARG, "a random number for every step");
+  if (n_stops > 0 && !stops) return fail(HE_E_ARG, "stops is null");
   *n_ids = 0;
   auto is_stop = [&](int32_t id) {
     for (int32_t j = 0; j < n_stops; ++j)
       if (stops[j] == id) return true;
     return false;
   };
+  if (temperature > 0.0f || penalty != 1.0f)
+    return sampled_steps(e, token, pos, history, n_history, count, temperature, topp, penalty, randoms, is_stop, ids,
+                         n_ids);
   int32_t done = 0;
-  // eager steps until the graph exists (the first step of an engine's first call builds it)
+  // greedy: eager steps until the graph exists (the first step of an engine's first call builds it)
   while (done < count && !e->graph) {
     int32_t best = 0;
     float value = 0.0f;
@@ -980,6 +1047,50 @@ int32_t hk_group_sums(void *s, const void *xq, const void *w, int32_t m, int32_t
     a.sums = reinterpret_cast<int32_t *>(s) + t0 * per_token;
     HIP_TRY(launch_gemv(a, six != 0, bias == 64, st));
   }
+  return HE_OK;
+}
+
+
+int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t count, float penalty, void *stream) {
+  if (!logits || n < 1 || count < 0 || count > REPETITION_WINDOW || (count > 0 && !tokens))
+    return fail(HE_E_ARG, "hk_penalize: bad arguments");
+  for (int32_t i = 0; i < count; ++i)
+    if (tokens[i] < 0 || tokens[i] >= n) return fail(HE_E_ARG, "hk_penalize: a token is outside the logits");
+  if (count == 0) return HE_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int32_t *d = nullptr;
+  int32_t rc = dev_alloc(&d, sizeof(int32_t) * count);
+  if (rc) return rc;
+  hipError_t err = hipMemcpyAsync(d, tokens, sizeof(int32_t) * count, hipMemcpyHostToDevice, s);
+  if (err == hipSuccess) err = launch_penalize(reinterpret_cast<float *>(logits), d, count, penalty, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  (void)hipFree(d);
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_penalize: ") + hipGetErrorString(err));
+  return HE_OK;
+}
+
+int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
+                  void *stream) {
+  if (!logits || !token || n < 1 || !(temperature > 0.0f)) return fail(HE_E_ARG, "hk_sample: bad arguments");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  float *probs = nullptr, *best = nullptr;
+  int32_t *index = nullptr, *out = nullptr;
+  int32_t rc = dev_alloc(&probs, sizeof(float) * n);
+  if (!rc) rc = dev_alloc(&index, sizeof(int32_t) * n);
+  if (!rc) rc = dev_alloc(&out, sizeof(int32_t) * 4);
+  if (!rc) rc = dev_alloc(&best, sizeof(float) * 4);
+  hipError_t err = hipSuccess;
+  if (!rc) {
+    err = launch_sample(reinterpret_cast<const float *>(logits), n, temperature, topp, random, probs, index, out, best,
+                        s);
+    if (err == hipSuccess) err = hipMemcpyAsync(token, out, sizeof(int32_t), hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+  }
+  void *ptrs[] = {probs, index, out, best};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  if (rc) return rc;
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_sample: ") + hipGetErrorString(err));
   return HE_OK;
 }
 

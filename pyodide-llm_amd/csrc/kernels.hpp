@@ -125,6 +125,14 @@ bool attention_quantizes(const AttnArgs &a);
 // greedy: the first index of the largest logit into *out (and the value into *value)
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
                          hipStream_t s);
+// the repetition penalty (kernels/kernel.ts:705-719) on the distinct tokens of tokens[0..count), count <= 64
+hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, float penalty, hipStream_t s);
+// one token drawn from softmax(logits / temperature) (kernels/kernel.ts:803-868) for random in [0, 1), restricted to
+// the nucleus where 0 < topp < 1; *out_token is the token, SAMPLE_NOT_FINITE where the largest logit is not finite,
+// or SAMPLE_DECLINED where the nucleus holds more tokens than one block sorts. probs, index: scratch of n each.
+constexpr int32_t SAMPLE_NOT_FINITE = -1, SAMPLE_DECLINED = -2;
+hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
+                         int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
 // the end of a replayed decode step: its token and value into ids / values at state[1], the token as the next step's
 // input (tokens[0]), state[0] (the position) and state[1] (the step) advanced
 hipError_t launch_advance(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,

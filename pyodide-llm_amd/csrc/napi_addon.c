@@ -14,7 +14,7 @@
 
 #include "include/pyodide_llm_hip.h"
 
-#define MAX_ARGS 10
+#define MAX_ARGS 16 /* the most any function here takes (generateMany: 12) */
 
 /* a failed N-API call: throw (if nothing is pending yet) and return NULL from the callback */
 #define NAPI_TRY(env, call)                                                      \
@@ -53,6 +53,10 @@ static napi_value undefined(napi_env env) {
 static int args_of(napi_env env, napi_callback_info info, size_t want, napi_value *argv) {
   size_t argc = MAX_ARGS;
   napi_value all[MAX_ARGS];
+  if (want > MAX_ARGS) {
+    napi_throw_error(env, NULL, "hip_engine: a function takes more arguments than MAX_ARGS");
+    return 0;
+  }
   if (napi_get_cb_info(env, info, &argc, all, NULL, NULL) != napi_ok) return 0;
   if (argc < want) {
     napi_throw_type_error(env, NULL, "hip_engine: too few arguments");
@@ -291,22 +295,37 @@ static napi_value js_forward_many(napi_env env, napi_callback_info info) {
   return undefined(env);
 }
 
-/* generateMany(engine, token, pos, count, stops: Int32Array, ids: Int32Array) -> the number of ids, or -1 where a
- * step's largest logit was not finite */
+static int get_f64(napi_env env, napi_value v, double *out) {
+  if (napi_get_value_double(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, NULL, "hip_engine: an argument is not a number");
+    return 0;
+  }
+  return 1;
+}
+
+/* generateMany(engine, token, pos, history: Int32Array, length, count, temperature, topp, penalty,
+ * randoms: Float64Array, stops: Int32Array, ids: Int32Array) -> the number of ids (0: the engine did not take the
+ * first step), or -1 where a step's largest logit was not finite */
 static napi_value js_generate_many(napi_env env, napi_callback_info info) {
-  napi_value argv[6];
-  if (!args_of(env, info, 6, argv)) return NULL;
+  napi_value argv[12];
+  if (!args_of(env, info, 12, argv)) return NULL;
   he_engine *e = engine_of(env, argv[0]);
-  int32_t token, pos, count;
-  void *stops, *ids;
-  size_t n_stops, n_ids;
-  if (!e || !get_i32(env, argv[1], &token) || !get_i32(env, argv[2], &pos) || !get_i32(env, argv[3], &count) ||
-      !bytes_of(env, argv[4], napi_int32_array, &stops, &n_stops) ||
-      !bytes_of(env, argv[5], napi_int32_array, &ids, &n_ids))
+  int32_t token, pos, length, count;
+  double temperature, topp, penalty;
+  void *history, *randoms, *stops, *ids;
+  size_t n_history, n_randoms, n_stops, n_ids;
+  if (!e || !get_i32(env, argv[1], &token) || !get_i32(env, argv[2], &pos) ||
+      !bytes_of(env, argv[3], napi_int32_array, &history, &n_history) || !get_i32(env, argv[4], &length) ||
+      !get_i32(env, argv[5], &count) || !get_f64(env, argv[6], &temperature) || !get_f64(env, argv[7], &topp) ||
+      !get_f64(env, argv[8], &penalty) || !bytes_of(env, argv[9], napi_float64_array, &randoms, &n_randoms) ||
+      !bytes_of(env, argv[10], napi_int32_array, &stops, &n_stops) ||
+      !bytes_of(env, argv[11], napi_int32_array, &ids, &n_ids))
     return NULL;
   if (count < 1 || (size_t)count > n_ids / 4) return throw_type(env, "hip_engine: ids holds fewer than count ids");
   int32_t got = 0;
-  const int32_t rc = he_generate_many(e, token, pos, count, (const int32_t *)stops, (int32_t)(n_stops / 4),
+  const int32_t rc = he_generate_many(e, token, pos, (const int32_t *)history, (int32_t)(n_history / 4), length, count,
+                                      (float)temperature, (float)topp, (float)penalty, (const double *)randoms,
+                                      (int32_t)(n_randoms / 8), (const int32_t *)stops, (int32_t)(n_stops / 4),
                                       (int32_t *)ids, &got);
   napi_value out;
   if (rc == HE_E_NOTFINITE) got = -1;

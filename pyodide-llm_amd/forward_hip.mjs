@@ -20,7 +20,7 @@ export const BATCH = 16;
 export const GPU_BLOCK = 64;
 // the tokens one forwardMany call takes here: the whole prompt block goes through each matrix at once
 export const PROMPT_BLOCK = 512;
-// the steps one generateMany call takes (greedy decoding on the device, one host sync a step)
+// the steps one generateMany call takes (greedy steps replayed from one captured step; sampled ones a step at a time)
 export const TOKEN_BLOCK = 16;
 // include/pyodide_llm_hip.h HE_T_*: the tensors the forward reads, by their plan names
 const TENSORS = ["token_embedding_table", "rms_att_weight", "wq", "wk", "wv", "wo", "rms_ffn_weight", "w1", "w2", "w3",
@@ -159,16 +159,24 @@ function engineObject(handle, config) {
     },
     get promptBlock() { return promptBlock; },
     get tokenBlock() { return TOKEN_BLOCK; },
-    /** generateMany (public/forward.js:1837-1890): greedy steps on the device (the first index of the largest logit,
-     * kernels/kernel.ts:695-699). undefined where the engine does not take them: a temperature, a repetition penalty,
-     * more steps than tokenBlock, or logits that are not finite (the caller's own step then stops on NOT_FINITE) */
+    /** generateMany (public/forward.js:1837-1890): count steps on the device, each the forward pass, the repetition
+     * penalty over history (the latest 64 of the generation's tokens, then the ids chosen; where penalty != 1) and the
+     * choice of the next token: the first index of the largest logit (temperature 0, kernels/kernel.ts:695-699) or a
+     * draw with randoms[i] (kernels/kernel.ts:803-868). Returns the ids (a stop token last). undefined where the engine
+     * does not take the first step: more steps than tokenBlock, too few random numbers, a nucleus larger than the
+     * device sorts (8192 tokens), or logits that are not finite (the caller's own step then stops on NOT_FINITE) */
     generateMany(token, pos, history, length, count, temperature, topp, penalty, randoms, stops) {
-      if (!(count >= 1 && count <= TOKEN_BLOCK) || temperature !== 0 || (penalty !== undefined && penalty !== 1)) {
-        return undefined;
-      }
+      if (!(count >= 1 && count <= TOKEN_BLOCK)) return undefined;
+      const t = Number(or(temperature, 0)), p = Number(or(penalty, 1));
+      const draws = Float64Array.from(or(fromJs(randoms), []));
+      if (t !== 0 && draws.length < count) return undefined;
+      const past = Int32Array.from(or(fromJs(history), []));
       const stopList = Int32Array.from(or(fromJs(stops), []));
-      const got = addon.generateMany(handle, token, pos, count, stopList, ids);
-      if (got < 0) return undefined;
+      const got = addon.generateMany(handle, token, pos, past, Number(or(length, past.length)), count, t,
+        Number(or(topp, 0.9)), p, draws, stopList, ids);
+      // -1: a largest logit that is not finite; 0: the engine did not take the first step (its nucleus is larger than
+      // the device sorts): the caller takes the step, as the reference's undefined says
+      if (got <= 0) return undefined;
       addon.logits(handle, logits);
       haveLogits = true;
       toBound();

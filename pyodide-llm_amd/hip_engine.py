@@ -74,7 +74,7 @@ def library():
                                         ctypes.POINTER(P)]),
             "he_forward": (I32, [P, I32, I32, I32, P]),
             "he_forward_many": (I32, [P, P, I32, I32]),
-            "he_generate_many": (I32, [P, I32, I32, I32, P, I32, P, P]),
+            "he_generate_many": (I32, [P, I32, I32, P, I32, I32, I32, F, F, F, P, I32, P, I32, P, P]),
             "he_logits": (I32, [P, P]),
             "he_kv_read": (I32, [P, I32, I32, P, P]),
             "he_checkpoint_read": (I32, [P, U64, U64, P]),
@@ -86,11 +86,13 @@ def library():
             "hk_quantize_x": (I32, [P, P, P, I32, I32, I32, P]),
             "hk_matmul": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, P]),
             "hk_group_sums": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, P]),
+            "hk_penalize": (I32, [P, I32, P, I32, F, P]),
+            "hk_sample": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = res, args
-        del I64, F
+        del I64
         _lib = lib
     return _lib
 
@@ -191,18 +193,28 @@ class Engine:
         return 16
 
     def generateMany(self, token, pos, history, length, count, temperature, topp, penalty, randoms, stops):
-        """public/forward.js:1837-1890: None where the engine does not take the steps (sampling with a temperature or a
-        repetition penalty: the caller then takes the step itself), else the ids (a stop token last)"""
-        if temperature != 0.0 or penalty != 1.0 or count < 1:
+        """public/forward.js:1831-1890: the ids of up to count steps (a stop token last), each the forward pass, the
+        repetition penalty over the latest 64 of history and the ids chosen (where penalty != 1), and greedy argmax
+        (temperature 0) or a draw with randoms[i] (kernels/kernel.ts:803-868); None where the engine does not take the
+        first step (its nucleus holds more tokens than the device sorts: the caller takes it) or where a largest logit
+        is not finite (the caller's own step then stops on NOT_FINITE, public/forward.js:1866-1880)"""
+        if count < 1:
+            return None
+        past = np.ascontiguousarray(np.asarray(list(history), dtype=np.int32))
+        draws = np.ascontiguousarray(np.asarray(list(randoms), dtype=np.float64))
+        if temperature != 0.0 and draws.size < count:
             return None
         stop = np.ascontiguousarray(np.asarray(list(stops), dtype=np.int32))
         ids = np.zeros(int(count), dtype=np.int32)
         n = ctypes.c_int32(0)
-        code = library().he_generate_many(self._h, int(token), int(pos), int(count), _ptr(stop), int(stop.size),
-                                          _ptr(ids), ctypes.byref(n))
+        code = library().he_generate_many(self._h, int(token), int(pos), _ptr(past), int(past.size), int(length),
+                                          int(count), float(temperature), float(topp), float(penalty), _ptr(draws),
+                                          int(draws.size), _ptr(stop), int(stop.size), _ptr(ids), ctypes.byref(n))
         if code == HE_E_NOTFINITE:
-            return None  # the caller's own step then stops on NOT_FINITE (public/forward.js:1866-1880)
+            return None
         check(code)
+        if n.value == 0:
+            return None
         if self._bound is not None:
             check(library().he_logits(self._h, _ptr(self._bound)))
         return [int(i) for i in ids[:n.value]]

@@ -98,3 +98,22 @@ def group_sums(xq, w, rows, k, bias, six, gemm=0):
     out = s.numpy()
     del xd, wd
     return out
+
+
+def penalize(logits, tokens, penalty):
+    """hk_penalize on a device copy of the float32 logits"""
+    x = upload(np.ascontiguousarray(logits, dtype=np.float32))
+    t = np.ascontiguousarray(np.asarray(list(tokens), dtype=np.int32))
+    check(package().library().hk_penalize(x.ptr, x.shape[0], ctypes.c_void_p(t.ctypes.data), t.size, float(penalty),
+                                          None))
+    return x.numpy()
+
+
+def sample(logits, temperature, topp, random):
+    """hk_sample: the token drawn for one random number (-1 not finite, -2 a nucleus larger than the device sorts)"""
+    x = upload(np.ascontiguousarray(logits, dtype=np.float32))
+    token = ctypes.c_int32(0)
+    check(package().library().hk_sample(x.ptr, x.shape[0], float(temperature), float(topp), float(random),
+                                        ctypes.byref(token), None))
+    del x
+    return int(token.value)

@@ -1,7 +1,8 @@
 // Runs the JavaScript host (pyodide-llm_amd/forward_hip.mjs) the way Llama.generate() drives forward.js
 // (public/llama2_numpy.py:1586-1612): the checkpoint written into weightsMemory(), external().start(plan), the prompt
-// [BOS] + prompt[:-1] through forwardMany, then greedy steps through generateMany; and a second engine fed one token at a
-// time through forward() with a bound logits array. Writes what it got for the test to compare with the oracle.
+// [BOS] + prompt[:-1] through forwardMany, then greedy steps and two sampled ones through generateMany; and a second
+// engine fed one token at a time through forward() with a bound logits array. Writes what it got for the test to
+// compare with the oracle.
 //
 //     node tests/node/run_engine.mjs job.json
 import fs from "fs";
@@ -39,7 +40,9 @@ write("bound_logits.bin", bound);
 const kv = engine.keysAndValues(0, job.steps);
 write("keys.bin", kv.keys);
 write("values.bin", kv.values);
-const refused = engine.generateMany(token, pos, [], 0, 1, 0.8, 0.9, 1, [0.5], []) === undefined;
+// two sampled steps (temperature 0.8, top-p 0.9, penalty 1.3 over the last 64 of the history), as generate() asks them
+const history = [1, ...prompt, ...ids];
+const sampled = engine.generateMany(token, pos, history.slice(-64), history.length, 2, 0.8, 0.9, 1.3, [0.5, 0.25], []);
 const memoryBytes = engine.memoryBytes();
 
 // one token at a time through forward(), the logits of the last into the bound array
@@ -59,5 +62,5 @@ try {
 
 Promise.all([engine.release(), second.release()]).then((released) => {
   console.log(JSON.stringify({ ids, backend: engine.backend, promptBlock: engine.promptBlock, tokenBlock: engine.tokenBlock,
-    memoryBytes, refused, released, threw, header: Array.from(header) }));
+    memoryBytes, sampled: sampled === undefined ? null : Array.from(sampled), released, threw, header: Array.from(header) }));
 });

@@ -46,6 +46,8 @@ def load():
             "or_swiglu": (None, [P, P, P, I32]),
             "or_add": (None, [P, P, I32]),
             "or_argmax": (I32, [P, I32]),
+            "or_penalize": (None, [P, P, I32, F]),
+            "or_sample": (I32, [P, I32, F, F, ctypes.c_double, P, P, P]),
             "or_places": (I64, [cfgp, tp]),
             "or_synth_checkpoint": (None, [cfgp, tp, P, I64, U64]),
             "or_rope_tables": (None, [P, P, I32, I32, ctypes.c_double]),
@@ -253,3 +255,21 @@ class Model:
 
     def __del__(self):
         self.close()
+
+
+def penalize(logits, tokens, penalty):
+    """kernels/kernel.ts:705-719 on a float32 copy"""
+    out = np.ascontiguousarray(np.asarray(logits, dtype=np.float32)).copy()
+    t = np.ascontiguousarray(np.asarray(list(tokens), dtype=np.int32))
+    load().or_penalize(ptr(out), ptr(t), t.size, float(penalty))
+    return out
+
+
+def sample(logits, temperature, topp, random):
+    """kernels/kernel.ts:803-868: the token drawn for one random number in [0, 1), -1 for logits that are not finite"""
+    x = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+    probs = np.zeros(x.size, dtype=np.float32)
+    index = np.zeros(x.size, dtype=np.int32)
+    order = np.zeros(x.size, dtype=np.int32)
+    return int(load().or_sample(ptr(x), x.size, float(temperature), float(topp), float(random), ptr(probs),
+                                ptr(index), ptr(order)))

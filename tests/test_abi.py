@@ -21,7 +21,7 @@ def declared():
 def test_header_declares_the_engine_and_kernel_entry_points():
     names = declared()
     for name in ("he_open", "he_forward", "he_forward_many", "he_generate_many", "he_logits", "he_kv_read",
-                 "he_close", "hk_matmul", "hk_quantize_x", "hk_group_sums"):
+                 "he_close", "hk_matmul", "hk_quantize_x", "hk_group_sums", "hk_penalize", "hk_sample"):
         assert name in names
 
 

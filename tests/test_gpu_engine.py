@@ -215,3 +215,68 @@ def test_replayed_steps_with_stops_and_eager_steps_between(name):
         assert same_bits(eng.logits(), logits[done + count - 1])
         done += count
     eng.release()
+
+
+def nucleus_size(logits, temperature, topp):
+    """how many tokens the nucleus sort takes (float64 NumPy: the cases here lie far from the device's 8192)"""
+    if not 0 < topp < 1:
+        return 0
+    best = float(logits.max())
+    kept = logits[logits >= best - temperature * 16.118095].astype(np.float64)
+    p = np.exp((kept - best) / temperature)
+    return int((p >= min((1 - topp) / max(p.size - 1, 1) * p.sum(), p.max())).sum())
+
+
+@pytest.mark.parametrize("name", sorted(MODELS))
+@pytest.mark.parametrize("temperature, topp, penalty", [(0.8, 0.9, 1.3), (1.0, 1.0, 1.0), (0.0, 0.9, 1.5),
+                                                        (0.5, 0.6, 0.8)])
+def test_sampled_generation_matches_the_oracle(name, temperature, topp, penalty):
+    """generate() with a temperature, top-p and a repetition penalty (public/llama2_numpy.py:1565-1640): the steps
+    generateMany takes against the oracle's forward pass, or_penalize over the latest 64 of the history and or_sample
+    with the same random numbers, token for token; a step the engine declines (a nucleus larger than it sorts) is the
+    caller's: forward() and the oracle's draw, as the reference's CPU step takes it"""
+    cfg, tensors, ck, cos, sin, _ = build(name)
+    rng = np.random.default_rng(int(10 * temperature + 100 * topp + 1000 * penalty))
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=12)]
+    steps = min(12 + 40, cfg.seq_len)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    ref.run([1] + prompt[:-1], 0, False)
+    eng = package().open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    eng.forwardMany([1] + prompt[:-1], 0)
+    history = [1] + prompt
+    token, pos, declined = prompt[-1], len(prompt), 0
+
+    def oracle_step(u):
+        ref.run([token], pos, True)
+        lg = ref.logits()
+        if penalty != 1.0:
+            lg = ol.penalize(lg, set(history[-64:]), penalty)
+        if temperature == 0.0:
+            return int(np.argmax(lg)), lg
+        return ol.sample(lg, temperature, topp, u), lg
+
+    while pos < steps:
+        count = min(8, steps - pos)
+        randoms = list(rng.random(count)) if temperature != 0.0 else []
+        got = eng.generateMany(token, pos, history[-64:], len(history), count, temperature, topp, penalty, randoms,
+                               [])
+        got = got or []
+        for i, t in enumerate(got):
+            want, _ = oracle_step(randoms[i] if randoms else 0.0)
+            assert t == want, (pos, i)
+            history.append(t)
+            token, pos = t, pos + 1
+        if len(got) < count:
+            # declined: the caller's step, through forward() and the oracle's draw
+            want, lg = oracle_step(randoms[len(got)])
+            assert nucleus_size(lg, temperature, topp) > 8192
+            eng.forward(token, pos, True)
+            assert same_bits(ol.penalize(eng.logits(), set(history[-64:]), penalty) if penalty != 1.0
+                             else eng.logits(), lg)
+            history.append(want)
+            token, pos = want, pos + 1
+            declined += 1
+    assert pos == steps
+    if cfg.vocab_size < 8192:
+        assert declined == 0
+    eng.release()

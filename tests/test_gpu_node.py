@@ -1,6 +1,6 @@
 """The JavaScript host on the GPU: Node drives pyodide-llm_amd/forward_hip.mjs (over hip_engine.node and the C ABI)
 the way Llama.generate() drives forward.js, and everything it gets is the oracle's to the bit: greedy tokens, the logits
-of forward() in the bound array, the last step's logits, the KV cache."""
+of forward() in the bound array, the last step's logits, the KV cache, and two sampled steps."""
 import json
 import os
 import shutil
@@ -25,6 +25,14 @@ CASES = {
     "stories15m_f16": (dict(dim=288, hidden_dim=768, n_layers=6, n_heads=6, n_kv_heads=6, head_size=48,
                             vocab_size=32000, seq_len=256, shared_classifier=1, half_kv=1), 10000.0, 32, 96),
 }
+
+
+def nucleus_size(logits, temperature, topp):
+    """how many tokens the nucleus sort takes (float64 NumPy: the cases here lie far from the device's 8192)"""
+    best = float(logits.max())
+    kept = logits[logits >= best - temperature * 16.118095].astype(np.float64)
+    p = np.exp((kept - best) / temperature)
+    return int((p >= min((1 - topp) / max(p.size - 1, 1) * p.sum(), p.max())).sum())
 
 
 def bits(a):
@@ -69,7 +77,20 @@ def test_node_host_matches_the_oracle(name, tmp_path):
     got = np.fromfile(tmp_path / "forward_logits.bin", dtype=np.float32)
     assert np.array_equal(bits(got), bits(one.logits()))
 
-    assert out["refused"] is True  # a temperature: the caller takes the step (undefined)
+    # the two sampled steps: the oracle's penalty over the last 64 of [BOS, prompt, ids], its draw for 0.5 then 0.25
+    # (undefined where the nucleus is larger than the device sorts: the caller takes the step)
+    history = [1] + prompt + [int(t) for t in want]
+    expect, token = [], int(want[-1])
+    for i, u in enumerate((0.5, 0.25)):
+        ref.run([token], steps + i, True)
+        logits = ol.penalize(ref.logits(), set(history[-64:]), 1.3)
+        if nucleus_size(logits, 0.8, 0.9) > 8192:
+            expect = None if i == 0 else expect
+            break
+        token = ol.sample(logits, 0.8, 0.9, u)
+        expect.append(token)
+        history.append(token)
+    assert out["sampled"] == expect
     assert out["released"] == [True, True]
     assert "context" in out["threw"]  # a position past seq_len throws, as forward.js does
     assert out["header"] == list(ck[:28])
