@@ -1,8 +1,9 @@
 /*
  * pyodide_llm_hip.h — the C ABI of the MI355X forward engine for pyodide-llm's quantized matmul path.
  *
- * The engine replaces the object public/forward.js:createForward returns (public/forward.js:1676-1955) for the
- * int8 / int6 Llama and Qwen2 forms. Every entry point takes plain pointers and sizes; device pointers are `void *`
+ * The engine replaces the object public/forward.js:createForward returns (public/forward.js:1676-1955) for int8 / int6
+ * checkpoints of the Llama form (with Qwen2's q/k/v biases and Qwen3's q/k head norms) and of the GPT-2 and GPT-NeoX
+ * forms (LayerNorm, GELU, a bias after every projection; learned positions or partial RoPE; parallel residual). Every entry point takes plain pointers and sizes; device pointers are `void *`
  * and streams are `void *` (a hipStream_t, NULL = the engine's own stream). Every function returns 0 on success or a
  * negative HE_E* code; he_last_error() then names what failed (a thread-local string).
  *
@@ -14,7 +15,7 @@
  *
  * Arithmetic is the reference's CPU path to the bit: activations quantized per group of 32 (kernels/kernel.ts:129-156),
  * exact int32 group sums, and the float32 order of kernels/kernel_relaxed.ts:34-67 (bias 64) or kernels/kernel.ts:
- * 231-258 (bias 0), rmsnorm/rope/attention/swiglu in the order of kernels/kernel.ts.
+ * 231-258 (bias 0), rmsnorm/layernorm/rope/attention/swiglu/gelu/add_columns in the order of kernels/kernel.ts.
  */
 #ifndef PYODIDE_LLM_HIP_H
 #define PYODIDE_LLM_HIP_H
@@ -32,7 +33,13 @@ extern "C" {
 #define HE_E_STATE -3    /* the call does not fit the engine's state (a position past the context, ...) */
 #define HE_E_NOTFINITE -4 /* greedy decoding met logits whose largest value is not finite (llama2_numpy.NOT_FINITE) */
 
-/* The model: the fields of `plan` (public/llama2_numpy.py:1261-1270) the Llama/Qwen2 forward reads. */
+/* plan.arch (public/forward.js:636) */
+#define HE_ARCH_LLAMA 0 /* "llama": RMSNorm, RoPE, SwiGLU (Qwen2 and Qwen3 are this form with biases / head norms) */
+#define HE_ARCH_GPT2 1  /* "gpt2": LayerNorm, learned positions added to the embedding, GELU, a bias after every matrix */
+#define HE_ARCH_NEOX 2  /* "neox": GPT-2's layer with RoPE over the first `rotary` values of every head */
+#define HE_OUTLIERS_MOST 8 /* OUTLIER_CHANNELS (public/llama2_numpy.py:561) */
+
+/* The model: the fields of `plan` (public/llama2_numpy.py:1261-1270) the forward reads. */
 typedef struct he_config {
   int32_t dim;               /* plan.dim */
   int32_t hidden_dim;        /* plan.hidden_dim */
@@ -47,7 +54,15 @@ typedef struct he_config {
   int32_t qkv_bias;          /* Qwen2: bq, bk, bv are added after the q, k, v matmuls (public/forward.js:1038-1042) */
   int32_t relaxed;           /* 1: activations with bias 64, matmul_q8r order; 0: bias 0, matmul_q8 lane order */
   int32_t half_kv;           /* keys and values kept in float16 (public/forward.js:762, kernels/kernel.ts:570-608) */
-  float rms_norm_eps;        /* plan.rms_norm_eps */
+  float rms_norm_eps;        /* plan.rms_norm_eps (RMSNorm; LayerNorm's is 1e-5, kernels/kernel.ts:627) */
+  int32_t arch;              /* plan.arch: HE_ARCH_* */
+  int32_t rotary;            /* plan.rotary: the values of each head RoPE turns (neox); 0 or head_size: all */
+  int32_t parallel_residual; /* plan.parallel_residual: the FFN's LayerNorm reads the layer's input (GPT-NeoX) */
+  int32_t qk_norm;           /* Qwen3: every head of q and k RMS-normalized by q_norm / k_norm before RoPE
+                                (public/forward.js:1043-1047) */
+  int32_t n_outliers;        /* plan.outliers: channels of the classifier's input multiplied apart in float32
+                                (public/forward.js:801-812,1084-1089), at most HE_OUTLIERS_MOST */
+  int32_t outliers[HE_OUTLIERS_MOST];
 } he_config;
 
 /* Where a tensor is: byte offsets from the start of the checkpoint (Tensor.offset, Tensor.scales). */
@@ -59,20 +74,29 @@ typedef struct he_tensor {
 /* The order of he_tensor arrays: the names of public/llama2_numpy.py TENSOR_NAMES the forward reads. */
 enum {
   HE_T_EMBEDDING = 0, /* token_embedding_table [vocab][dim], int8 or int6 */
-  HE_T_RMS_ATT,       /* rms_att_weight [layers][dim] f32 */
+  HE_T_RMS_ATT,       /* rms_att_weight [layers][dim] f32 (LayerNorm's weight in gpt2 and neox) */
   HE_T_WQ,            /* wq [layers][n_heads*head_size][dim] */
   HE_T_WK,            /* wk [layers][kv_dim][dim] */
   HE_T_WV,            /* wv [layers][kv_dim][dim] */
   HE_T_WO,            /* wo [layers][dim][n_heads*head_size] */
-  HE_T_RMS_FFN,       /* rms_ffn_weight [layers][dim] f32 */
+  HE_T_RMS_FFN,       /* rms_ffn_weight [layers][dim] f32 (the same) */
   HE_T_W1,            /* w1 [layers][hidden][dim] */
   HE_T_W2,            /* w2 [layers][dim][hidden] */
-  HE_T_W3,            /* w3 [layers][hidden][dim] */
-  HE_T_RMS_FINAL,     /* rms_final_weight [dim] f32 */
+  HE_T_W3,            /* w3 [layers][hidden][dim] (llama only) */
+  HE_T_RMS_FINAL,     /* rms_final_weight [dim] f32 (the same) */
   HE_T_WCLS,          /* wcls [vocab][dim] (the embedding's offsets when shared) */
-  HE_T_BQ,            /* bq [layers][q_dim] f32 (qkv_bias) */
+  HE_T_BQ,            /* bq [layers][q_dim] f32 (qkv_bias; always for gpt2 and neox) */
   HE_T_BK,            /* bk [layers][kv_dim] f32 */
   HE_T_BV,            /* bv [layers][kv_dim] f32 */
+  HE_T_Q_NORM,        /* q_norm [layers][head_size] f32 (qk_norm) */
+  HE_T_K_NORM,        /* k_norm [layers][head_size] f32 (qk_norm) */
+  HE_T_POSITIONS,     /* positions [seq_len][dim], int8 or int6 (gpt2: a learned row added to the embedding) */
+  HE_T_LN_ATT_BIAS,   /* ln_att_bias [layers][dim] f32 (gpt2, neox: LayerNorm's bias; its weight is rms_att_weight) */
+  HE_T_LN_FFN_BIAS,   /* ln_ffn_bias [layers][dim] f32 */
+  HE_T_LN_FINAL_BIAS, /* ln_final_bias [dim] f32 */
+  HE_T_BO,            /* bo [layers][dim] f32 (gpt2, neox: the biases after wo, w1, w2) */
+  HE_T_B1,            /* b1 [layers][hidden] f32 */
+  HE_T_B2,            /* b2 [layers][dim] f32 */
   HE_T_COUNT
 };
 

@@ -27,6 +27,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stddef.h>
 #include <omp.h>
 #include <stdlib.h>
 #include <string.h>
@@ -477,6 +478,51 @@ void or_swiglu(float *out, const float *h1, const float *h3, int32_t n) {
   }
 }
 
+/* kernels/kernel.ts:610-634 layernorm: the sum of x in four lanes over n & ~3, hsum ((l0+l1)+l2)+l3, the tail in
+ * order, mean = total / n; the same for (x - mean)^2; s = 1 / sqrt(ss / n + 1e-5); out = w * (s * (x - mean)) + b */
+void or_layernorm(float *out, const float *x, const float *w, const float *b, int32_t n) {
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int32_t n4 = n & ~3;
+  int32_t j = 0;
+  for (; j < n4; j += 4)
+    for (int32_t l = 0; l < 4; l++) acc[l] = acc[l] + x[j + l];
+  float total = acc[0] + acc[1] + acc[2] + acc[3];
+  for (; j < n; j++) total = total + x[j];
+  const float mean = total / (float)n;
+  float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (j = 0; j < n4; j += 4)
+    for (int32_t l = 0; l < 4; l++) {
+      const float d = x[j + l] - mean;
+      sq[l] = sq[l] + d * d;
+    }
+  float ss = sq[0] + sq[1] + sq[2] + sq[3];
+  for (; j < n; j++) {
+    const float d = x[j] - mean;
+    ss = ss + d * d;
+  }
+  const float s = 1.0f / sqrtf(ss / (float)n + 1e-5f);
+  for (j = 0; j < n; j++) out[j] = w[j] * (s * (x[j] - mean)) + b[j];
+}
+
+/* kernels/kernel.ts:636-652 gelu (GPT-2's gelu_new) with the bias first: v = x + b, inner = c * (v + 0.044715 v v v),
+ * out = v / (1 + vexp(-2 inner)) (the scalar tail's fexp gives the same bits, as in or_swiglu) */
+void or_gelu(float *out, const float *x, const float *b, int32_t n) {
+  for (int32_t j = 0; j < n; j++) {
+    const float v = x[j] + b[j];
+    const float inner = 0.7978845608028654f * (v + ((0.044715f * v) * v) * v);
+    out[j] = v / (1.0f + vexp1(-2.0f * inner));
+  }
+}
+
+/* kernels/kernel.ts:671-689 add_columns: y[j] += a[c] * rows[c][j] for c = 0, 1, ... in order, each product rounded */
+void or_add_columns(float *y, const float *rows, const float *a, int32_t count, int32_t n) {
+  for (int32_t j = 0; j < n; j++) {
+    float acc = y[j];
+    for (int32_t c = 0; c < count; c++) acc = acc + a[c] * rows[(int64_t)c * n + j];
+    y[j] = acc;
+  }
+}
+
 /* kernels/kernel.ts:691-693 */
 void or_add(float *x, const float *y, int32_t n) {
   for (int32_t j = 0; j < n; j++) x[j] = x[j] + y[j];
@@ -670,82 +716,113 @@ void or_attention(float *out, const float *q, const void *kc, const void *vc, fl
 
 /* ------------------------------------------------------------------------------------------------ the checkpoint */
 
-/* public/llama2_numpy.py:751-775 Places.take and :1149-1179 llama_tensors: the offset of every tensor of an int8 or
- * int6 Llama/Qwen2 checkpoint (no RoPE tables in such a file), from the 28-byte header on. Returns the file size. */
-int64_t or_places(const he_config *c, he_tensor *t) {
-  int64_t offset = 28;
+static int layer_norm(const he_config *c) { return c->arch == HE_ARCH_GPT2 || c->arch == HE_ARCH_NEOX; }
+
+/* the tensors of the form (public/llama2_convert.py:32-83) */
+static int present(const he_config *c, int32_t id) {
+  switch (id) {
+    case HE_T_WCLS: return !c->shared_classifier;
+    case HE_T_W3: return !layer_norm(c);
+    case HE_T_BQ:
+    case HE_T_BK:
+    case HE_T_BV: return layer_norm(c) || c->qkv_bias;
+    case HE_T_Q_NORM:
+    case HE_T_K_NORM: return !layer_norm(c) && c->qk_norm;
+    case HE_T_POSITIONS: return c->arch == HE_ARCH_GPT2;
+    case HE_T_LN_ATT_BIAS:
+    case HE_T_LN_FFN_BIAS:
+    case HE_T_LN_FINAL_BIAS:
+    case HE_T_BO:
+    case HE_T_B1:
+    case HE_T_B2: return layer_norm(c);
+  }
+  return 1;
+}
+
+/* a tensor's value count and row length (0 for float32 vectors) */
+static void tensor_shape(const he_config *c, int32_t id, int64_t *count, int64_t *last) {
   const int64_t L = c->n_layers, dim = c->dim, hidden = c->hidden_dim, vocab = c->vocab_size;
   const int64_t qdim = (int64_t)c->n_heads * c->head_size, kvdim = (int64_t)c->n_kv_heads * c->head_size;
+  const int64_t counts[HE_T_COUNT] = {vocab * dim, L * dim, L * qdim * dim, L * kvdim * dim, L * kvdim * dim,
+                                      L * dim * qdim, L * dim, L * hidden * dim, L * dim * hidden, L * hidden * dim,
+                                      dim, vocab * dim, L * qdim, L * kvdim, L * kvdim,
+                                      L * c->head_size, L * c->head_size, (int64_t)c->seq_len * dim, L * dim, L * dim,
+                                      dim, L * dim, L * hidden, L * dim};
+  const int64_t lasts[HE_T_COUNT] = {dim, 0, dim, dim, dim, qdim, 0, dim, hidden, dim, 0, dim, 0, 0, 0,
+                                     0, 0, dim, 0, 0, 0, 0, 0, 0};
+  *count = counts[id];
+  *last = lasts[id];
+}
+
+/* public/llama2_numpy.py:751-775 Places.take over the tensor order of the form: llama_tensors (:1149-1179, Qwen2's
+ * biases and Qwen3's head norms last) or gpt2_tensors (:1203-1240), as public/llama2_convert.py:32-83 writes them, of
+ * an int8 or int6 checkpoint (no RoPE tables in such a file), from the 28-byte header on. Returns the file size. */
+int64_t or_places(const he_config *c, he_tensor *t) {
+  int64_t offset = 28;
   memset(t, 0, sizeof(he_tensor) * HE_T_COUNT);
-#define MATRIX(id, count, last)                                                   \
-  do {                                                                            \
-    int64_t n_ = (count), grp_ = or_group_size((int32_t)(last));                  \
-    int64_t stored_ = c->six ? n_ * 3 / 4 : n_;                                   \
-    t[id].offset = offset;                                                        \
-    t[id].scales = offset + stored_;                                              \
-    offset += stored_ + 4 * (n_ / grp_);                                          \
+#define TAKE(id)                                                              \
+  do {                                                                        \
+    int64_t n_, last_;                                                        \
+    tensor_shape(c, (id), &n_, &last_);                                       \
+    t[id].offset = offset;                                                    \
+    if (last_) {                                                              \
+      const int64_t grp_ = or_group_size((int32_t)last_);                     \
+      const int64_t stored_ = c->six ? n_ * 3 / 4 : n_;                       \
+      t[id].scales = offset + stored_;                                        \
+      offset += stored_ + 4 * (n_ / grp_);                                    \
+    } else {                                                                  \
+      offset += 4 * n_;                                                       \
+    }                                                                         \
   } while (0)
-#define VECTOR(id, count)      \
-  do {                         \
-    t[id].offset = offset;     \
-    t[id].scales = 0;          \
-    offset += 4 * (count);     \
-  } while (0)
-  MATRIX(HE_T_EMBEDDING, vocab * dim, dim);
-  VECTOR(HE_T_RMS_ATT, L * dim);
-  MATRIX(HE_T_WQ, L * qdim * dim, dim);
-  MATRIX(HE_T_WK, L * kvdim * dim, dim);
-  MATRIX(HE_T_WV, L * kvdim * dim, dim);
-  MATRIX(HE_T_WO, L * dim * qdim, qdim);
-  VECTOR(HE_T_RMS_FFN, L * dim);
-  MATRIX(HE_T_W1, L * hidden * dim, dim);
-  MATRIX(HE_T_W2, L * dim * hidden, hidden);
-  MATRIX(HE_T_W3, L * hidden * dim, dim);
-  VECTOR(HE_T_RMS_FINAL, dim);
-  if (c->shared_classifier) t[HE_T_WCLS] = t[HE_T_EMBEDDING];
-  else MATRIX(HE_T_WCLS, vocab * dim, dim);
-  if (c->qkv_bias) {
-    VECTOR(HE_T_BQ, L * qdim);
-    VECTOR(HE_T_BK, L * kvdim);
-    VECTOR(HE_T_BV, L * kvdim);
+  if (layer_norm(c)) {
+    static const int32_t order[] = {HE_T_EMBEDDING, HE_T_POSITIONS, HE_T_RMS_ATT, HE_T_LN_ATT_BIAS, HE_T_WQ, HE_T_WK,
+                                    HE_T_WV, HE_T_BQ, HE_T_BK, HE_T_BV, HE_T_WO, HE_T_BO, HE_T_RMS_FFN,
+                                    HE_T_LN_FFN_BIAS, HE_T_W1, HE_T_B1, HE_T_W2, HE_T_B2, HE_T_RMS_FINAL,
+                                    HE_T_LN_FINAL_BIAS, HE_T_WCLS};
+    for (size_t i = 0; i < sizeof order / sizeof order[0]; i++)
+      if (present(c, order[i])) TAKE(order[i]);
+  } else {
+    static const int32_t order[] = {HE_T_EMBEDDING, HE_T_RMS_ATT, HE_T_WQ, HE_T_WK, HE_T_WV, HE_T_WO, HE_T_RMS_FFN,
+                                    HE_T_W1, HE_T_W2, HE_T_W3, HE_T_RMS_FINAL, HE_T_WCLS, HE_T_BQ, HE_T_BK, HE_T_BV,
+                                    HE_T_Q_NORM, HE_T_K_NORM};
+    for (size_t i = 0; i < sizeof order / sizeof order[0]; i++)
+      if (present(c, order[i])) TAKE(order[i]);
   }
-#undef MATRIX
-#undef VECTOR
+  if (c->shared_classifier) t[HE_T_WCLS] = t[HE_T_EMBEDDING];
+#undef TAKE
   return offset;
+}
+
+static int norm_weight(int32_t id) {
+  return id == HE_T_RMS_ATT || id == HE_T_RMS_FFN || id == HE_T_RMS_FINAL || id == HE_T_Q_NORM || id == HE_T_K_NORM;
 }
 
 /* quantize.py:22-40 on a synthetic float32 model: matrices N(0, 0.02) by or_synth_value (stream = the tensor's
  * HE_T_* index, index = the value's place in the tensor), quantize() or quantize6()+pack6(); norm weights 1.0;
- * Qwen2 biases N(0, 0.02). The 28-byte header is the llama2.c one (vocab negative where the classifier is its own). */
+ * biases N(0, 0.02). The 28-byte header is the llama2.c one (vocab negative where the classifier is its own). */
 void or_synth_checkpoint(const he_config *c, const he_tensor *t, uint8_t *out, int64_t size, uint64_t seed) {
   (void)size;
   int32_t header[7] = {c->dim, c->hidden_dim, c->n_layers, c->n_heads, c->n_kv_heads,
                        c->shared_classifier ? c->vocab_size : -c->vocab_size, c->seq_len};
   memcpy(out, header, 28);
-  const int64_t L = c->n_layers, dim = c->dim, hidden = c->hidden_dim, vocab = c->vocab_size;
-  const int64_t qdim = (int64_t)c->n_heads * c->head_size, kvdim = (int64_t)c->n_kv_heads * c->head_size;
-  const int64_t counts[HE_T_COUNT] = {vocab * dim, L * dim, L * qdim * dim, L * kvdim * dim, L * kvdim * dim,
-                                      L * dim * qdim, L * dim, L * hidden * dim, L * dim * hidden, L * hidden * dim,
-                                      dim, vocab * dim, L * qdim, L * kvdim, L * kvdim};
-  const int64_t lasts[HE_T_COUNT] = {dim, 0, dim, dim, dim, qdim, 0, dim, hidden, dim, 0, dim, 0, 0, 0};
   for (int32_t id = 0; id < HE_T_COUNT; id++) {
-    const int64_t n = counts[id];
-    if (id == HE_T_WCLS && c->shared_classifier) continue;
-    if (id >= HE_T_BQ && !c->qkv_bias) continue;
-    if (lasts[id] == 0 && id < HE_T_BQ) {
+    if (!present(c, id)) continue;
+    int64_t n, last;
+    tensor_shape(c, id, &n, &last);
+    if (!last && norm_weight(id)) {
       float *v = (float *)(out + t[id].offset);
       for (int64_t i = 0; i < n; i++) v[i] = 1.0f;
       continue;
     }
-    /* one piece of rows at a time */
-    const int64_t K = id < HE_T_BQ ? lasts[id] : n;
+    /* one piece of rows at a time (a vector: one row) */
+    const int64_t K = last ? last : n;
     const int64_t piece_rows = (1 << 22) / K + 1;
     float *vals = (float *)malloc(sizeof(float) * (size_t)(piece_rows * K));
     int8_t *q = (int8_t *)malloc((size_t)(piece_rows * K));
     for (int64_t r0 = 0; r0 < n / K; r0 += piece_rows) {
       const int64_t rows = (n / K - r0) < piece_rows ? (n / K - r0) : piece_rows;
       or_synth_fill(vals, (uint64_t)(rows * K), seed, id, (uint64_t)(r0 * K), 0.02);
-      if (id >= HE_T_BQ) {
+      if (!last) {
         memcpy(out + t[id].offset + 4 * r0 * K, vals, sizeof(float) * (size_t)(rows * K));
         continue;
       }
@@ -792,6 +869,8 @@ struct or_model {
   float *x, *xb, *xb2, *q, *k, *v, *hb, *hb2, *att, *logits;
   int8_t *xq;
   float *xs;
+  float *before;          /* the layer's input (parallel residual) */
+  float *columns, picked[HE_OUTLIERS_MOST]; /* the outlier channels' float32 classifier columns [n][vocab] */
 };
 
 static const int8_t *mat_values(const or_model *m, int32_t id, int32_t l, int64_t rows, int64_t K) {
@@ -839,6 +918,24 @@ or_model *or_model_open(const he_config *c, const he_tensor *t, const uint8_t *c
   m->logits = (float *)calloc((size_t)c->vocab_size, 4);
   m->xq = (int8_t *)calloc((size_t)(B * wq), 1);
   m->xs = (float *)calloc((size_t)(B * wq / GS + 1), 4);
+  m->before = (float *)calloc((size_t)(B * c->dim), 4);
+  /* public/forward.js:801-812: columns[i][v] = f32(weight(v, c_i) * the scale of its group) */
+  m->columns = (float *)calloc((size_t)c->n_outliers * (size_t)c->vocab_size + 1, 4);
+  if (c->n_outliers) {
+    const int32_t dim = c->dim, grp = c->six ? 32 : or_group_size(dim);
+    const float *scales = (const float *)(checkpoint + t[HE_T_WCLS].scales);
+    int8_t *wide = (int8_t *)malloc((size_t)dim);
+    for (int32_t v = 0; v < c->vocab_size; v++) {
+      const int64_t row = (int64_t)v * dim;
+      if (c->six) or_unpack6(wide, checkpoint + t[HE_T_WCLS].offset + row / GS * 24, dim / GS);
+      else memcpy(wide, checkpoint + t[HE_T_WCLS].offset + row, (size_t)dim);
+      for (int32_t i = 0; i < c->n_outliers; i++) {
+        const int32_t ch = c->outliers[i];
+        m->columns[(int64_t)i * c->vocab_size + v] = (float)wide[ch] * scales[(row + ch) / grp];
+      }
+    }
+    free(wide);
+  }
   return m;
 }
 
@@ -847,6 +944,7 @@ void or_model_close(or_model *m) {
   free(m->cosT); free(m->sinT); free(m->keys); free(m->values);
   free(m->x); free(m->xb); free(m->xb2); free(m->q); free(m->k); free(m->v);
   free(m->hb); free(m->hb2); free(m->att); free(m->logits); free(m->xq); free(m->xs);
+  free(m->before); free(m->columns);
   free(m);
 }
 
@@ -870,19 +968,30 @@ static void matmuls(or_model *m, const float *input, int64_t in_stride, int32_t 
   }
 }
 
-/* public/forward.js:962-973 embed() with valueAt (:692-696): f32(int8 * scale of its group) */
-static void embed(or_model *m, int32_t token, float *x) {
+/* valueAt (public/forward.js:672-696) over a row of an int8 / int6 table: f32(value * scale of its group) */
+static void widen_row(const or_model *m, int32_t id, int64_t r, float *x) {
   const int32_t dim = m->c.dim, grp = m->c.six ? 32 : or_group_size(dim);
-  const float *scales = (const float *)(m->ck + m->t[HE_T_EMBEDDING].scales);
-  const int64_t row = (int64_t)token * dim;
+  const float *scales = (const float *)(m->ck + m->t[id].scales);
+  const int64_t row = r * dim;
   if (m->c.six) {
     int8_t *wide = (int8_t *)malloc((size_t)dim);
-    or_unpack6(wide, m->ck + m->t[HE_T_EMBEDDING].offset + row / GS * 24, dim / GS);
+    or_unpack6(wide, m->ck + m->t[id].offset + row / GS * 24, dim / GS);
     for (int32_t i = 0; i < dim; i++) x[i] = (float)wide[i] * scales[(row + i) / grp];
     free(wide);
   } else {
-    const int8_t *v = (const int8_t *)(m->ck + m->t[HE_T_EMBEDDING].offset) + row;
+    const int8_t *v = (const int8_t *)(m->ck + m->t[id].offset) + row;
     for (int32_t i = 0; i < dim; i++) x[i] = (float)v[i] * scales[(row + i) / grp];
+  }
+}
+
+/* public/forward.js:962-973 embed(): the token's row widened; GPT-2's row of positions (widened too, floats()) added */
+static void embed(or_model *m, int32_t token, int32_t pos, float *x) {
+  widen_row(m, HE_T_EMBEDDING, token, x);
+  if (m->c.arch == HE_ARCH_GPT2) {
+    float *p = (float *)malloc(sizeof(float) * (size_t)m->c.dim);
+    widen_row(m, HE_T_POSITIONS, pos, p);
+    or_add(x, p, m->c.dim);
+    free(p);
   }
 }
 
@@ -892,32 +1001,49 @@ static void write_cache(or_model *m, void *cache, int32_t l, int32_t pos, const 
   else memcpy((float *)cache + at, src, sizeof(float) * (size_t)m->kvdim);
 }
 
-/* public/forward.js:1011-1090 run(): count tokens at pos0.. (the Llama/Qwen2 path: RMSNorm, RoPE, SwiGLU, optional
- * q/k/v biases), every token computed as it would be alone; the logits, if asked for, the last token's */
+/* public/forward.js:1011-1090 run(): count tokens at pos0.., every token computed as it would be alone; the logits,
+ * if asked for, the last token's. The llama form (RMSNorm, RoPE, SwiGLU; Qwen2's q/k/v biases, Qwen3's head norms)
+ * and GPT-2 / GPT-NeoX (LayerNorm, learned positions or RoPE over the first `rotary` values, GELU, a bias after every
+ * matrix, the parallel residual); the outlier channels multiplied apart at the classifier. */
 int32_t or_model_run(or_model *m, const int32_t *tokens, int32_t count, int32_t pos0, int32_t need_logits) {
   const he_config *c = &m->c;
   if (count < 1 || count > m->max_block || pos0 < 0 || pos0 + count > c->seq_len) return -1;
   const int32_t dim = c->dim, hidden = c->hidden_dim, qdim = m->qdim, kvdim = m->kvdim, hs = c->head_size, xw = m->xw;
   const float eps = c->rms_norm_eps;
   const size_t e = c->half_kv ? 2 : 4;
-  for (int32_t t = 0; t < count; t++) embed(m, tokens[t], m->x + (int64_t)t * dim);
+  const int ln = layer_norm(c), biases = ln || c->qkv_bias;
+  for (int32_t t = 0; t < count; t++) embed(m, tokens[t], pos0 + t, m->x + (int64_t)t * dim);
   for (int32_t l = 0; l < c->n_layers; l++) {
-    for (int32_t t = 0; t < count; t++)
-      or_rmsnorm(m->xb + (int64_t)t * xw, m->x + (int64_t)t * dim, vec(m, HE_T_RMS_ATT, (int64_t)l * dim), dim, eps);
+    for (int32_t t = 0; t < count; t++) {
+      float *xbt = m->xb + (int64_t)t * xw, *xt = m->x + (int64_t)t * dim;
+      if (ln) or_layernorm(xbt, xt, vec(m, HE_T_RMS_ATT, (int64_t)l * dim), vec(m, HE_T_LN_ATT_BIAS, (int64_t)l * dim),
+                           dim);
+      else or_rmsnorm(xbt, xt, vec(m, HE_T_RMS_ATT, (int64_t)l * dim), dim, eps);
+      if (c->parallel_residual) memcpy(m->before + (int64_t)t * dim, xt, sizeof(float) * (size_t)dim);
+    }
     matmuls(m, m->xb, xw, count, dim, HE_T_WQ, l, qdim, m->q, qdim);
     matmuls(m, m->xb, xw, count, dim, HE_T_WK, l, kvdim, m->k, kvdim);
     matmuls(m, m->xb, xw, count, dim, HE_T_WV, l, kvdim, m->v, kvdim);
     for (int32_t t = 0; t < count; t++) {
       float *qt = m->q + (int64_t)t * qdim, *kt = m->k + (int64_t)t * kvdim, *vt = m->v + (int64_t)t * kvdim;
       const int32_t pos = pos0 + t;
-      if (c->qkv_bias) {
+      if (biases) {
         or_add(qt, vec(m, HE_T_BQ, (int64_t)l * qdim), qdim);
         or_add(kt, vec(m, HE_T_BK, (int64_t)l * kvdim), kvdim);
         or_add(vt, vec(m, HE_T_BV, (int64_t)l * kvdim), kvdim);
       }
-      const float *cs = m->cosT + (int64_t)pos * (hs / 2), *sn = m->sinT + (int64_t)pos * (hs / 2);
-      or_rope(qt, cs, sn, c->n_heads, hs, 0);
-      or_rope(kt, cs, sn, c->n_kv_heads, hs, 0);
+      if (c->qk_norm) {
+        for (int32_t h = 0; h < c->n_heads; h++)
+          or_rmsnorm(qt + h * hs, qt + h * hs, vec(m, HE_T_Q_NORM, (int64_t)l * hs), hs, eps);
+        for (int32_t h = 0; h < c->n_kv_heads; h++)
+          or_rmsnorm(kt + h * hs, kt + h * hs, vec(m, HE_T_K_NORM, (int64_t)l * hs), hs, eps);
+      }
+      if (c->arch != HE_ARCH_GPT2) {
+        const float *cs = m->cosT + (int64_t)pos * (hs / 2), *sn = m->sinT + (int64_t)pos * (hs / 2);
+        const int32_t rot = c->arch == HE_ARCH_NEOX ? c->rotary : 0;
+        or_rope(qt, cs, sn, c->n_heads, hs, rot);
+        or_rope(kt, cs, sn, c->n_kv_heads, hs, rot);
+      }
       write_cache(m, m->keys, l, pos, kt);
       write_cache(m, m->values, l, pos, vt);
     }
@@ -931,6 +1057,22 @@ int32_t or_model_run(or_model *m, const int32_t *tokens, int32_t count, int32_t 
                      c->half_kv);
     matmuls(m, m->xb, xw, count, qdim, HE_T_WO, l, dim, m->xb2, dim);
     for (int32_t t = 0; t < count; t++) or_add(m->x + (int64_t)t * dim, m->xb2 + (int64_t)t * dim, dim);
+    if (ln) {
+      for (int32_t t = 0; t < count; t++) {
+        or_add(m->x + (int64_t)t * dim, vec(m, HE_T_BO, (int64_t)l * dim), dim);
+        or_layernorm(m->xb + (int64_t)t * xw, (c->parallel_residual ? m->before : m->x) + (int64_t)t * dim,
+                     vec(m, HE_T_RMS_FFN, (int64_t)l * dim), vec(m, HE_T_LN_FFN_BIAS, (int64_t)l * dim), dim);
+      }
+      matmuls(m, m->xb, xw, count, dim, HE_T_W1, l, hidden, m->hb, hidden);
+      for (int32_t t = 0; t < count; t++)
+        or_gelu(m->hb + (int64_t)t * hidden, m->hb + (int64_t)t * hidden, vec(m, HE_T_B1, (int64_t)l * hidden), hidden);
+      matmuls(m, m->hb, hidden, count, hidden, HE_T_W2, l, dim, m->xb2, dim);
+      for (int32_t t = 0; t < count; t++) {
+        or_add(m->x + (int64_t)t * dim, m->xb2 + (int64_t)t * dim, dim);
+        or_add(m->x + (int64_t)t * dim, vec(m, HE_T_B2, (int64_t)l * dim), dim);
+      }
+      continue;
+    }
     for (int32_t t = 0; t < count; t++)
       or_rmsnorm(m->xb + (int64_t)t * xw, m->x + (int64_t)t * dim, vec(m, HE_T_RMS_FFN, (int64_t)l * dim), dim, eps);
     matmuls(m, m->xb, xw, count, dim, HE_T_W1, l, hidden, m->hb, hidden);
@@ -942,8 +1084,14 @@ int32_t or_model_run(or_model *m, const int32_t *tokens, int32_t count, int32_t 
   }
   if (!need_logits) return 0;
   const float *last = m->x + (int64_t)(count - 1) * dim;
-  or_rmsnorm(m->xb, last, vec(m, HE_T_RMS_FINAL, 0), dim, eps);
+  if (ln) or_layernorm(m->xb, last, vec(m, HE_T_RMS_FINAL, 0), vec(m, HE_T_LN_FINAL_BIAS, 0), dim);
+  else or_rmsnorm(m->xb, last, vec(m, HE_T_RMS_FINAL, 0), dim, eps);
+  for (int32_t i = 0; i < c->n_outliers; i++) { /* public/forward.js:1084-1087 */
+    m->picked[i] = m->xb[c->outliers[i]];
+    m->xb[c->outliers[i]] = 0.0f;
+  }
   matmuls(m, m->xb, xw, 1, dim, HE_T_WCLS, 0, c->vocab_size, m->logits, 0);
+  if (c->n_outliers) or_add_columns(m->logits, m->columns, m->picked, c->n_outliers, c->vocab_size);
   return 0;
 }
 
@@ -993,6 +1141,17 @@ int32_t or_generate(or_model *m, const int32_t *prompt, int32_t n_prompt, int32_
   }
   if (last_logits) memcpy(last_logits, m->logits, sizeof(float) * (size_t)m->c.vocab_size);
   return n;
+}
+
+/* the C layout of include/pyodide_llm_hip.h's structs, for the hosts' ctypes mirrors: sizeof(he_config), the offsets
+ * of rms_norm_eps, arch and outliers in it, sizeof(he_tensor), HE_T_COUNT */
+void or_abi_layout(int64_t *out) {
+  out[0] = (int64_t)sizeof(he_config);
+  out[1] = (int64_t)offsetof(he_config, rms_norm_eps);
+  out[2] = (int64_t)offsetof(he_config, arch);
+  out[3] = (int64_t)offsetof(he_config, outliers);
+  out[4] = (int64_t)sizeof(he_tensor);
+  out[5] = HE_T_COUNT;
 }
 
 void or_set_threads(int32_t n) { omp_set_num_threads(n > 0 ? n : 1); }

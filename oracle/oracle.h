@@ -54,6 +54,9 @@ void or_from_f16(float *out, const uint16_t *x, int32_t n);
 float or_fexp(float x);
 void or_vexp(float *x, int32_t n);
 void or_swiglu(float *out, const float *h1, const float *h3, int32_t n);
+void or_layernorm(float *out, const float *x, const float *w, const float *b, int32_t n);
+void or_gelu(float *out, const float *x, const float *b, int32_t n);
+void or_add_columns(float *y, const float *rows, const float *a, int32_t count, int32_t n);
 void or_add(float *x, const float *y, int32_t n);
 int32_t or_argmax(const float *x, int32_t n);
 void or_penalize(float *logits, const int32_t *tokens, int32_t count, float penalty);
@@ -75,6 +78,7 @@ void or_model_kv(const or_model *m, int32_t from, int32_t count, float *keys, fl
 void or_model_close(or_model *m);
 int32_t or_generate(or_model *m, const int32_t *prompt, int32_t n_prompt, int32_t steps, int32_t block,
                     int32_t *out_tokens, float *last_logits);
+void or_abi_layout(int64_t *out);
 void or_set_threads(int32_t n);
 int32_t or_get_threads(void);
 

@@ -202,4 +202,15 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// quantize_x of one group of 32, a half-wave (all 32 lanes present): amax (order-free), scale = f32(amax / qmax),
+// inv = scale > 0 ? f32(1 / scale) : 0 (kernels/kernel.ts:129-156)
+__device__ __forceinline__ void quantize_group(float v, int8_t *xq, float *xs, int j, int g, int32_t bias) {
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  const float amax = wave_max32(__builtin_fabsf(v));
+  const float scale = amax / qmax;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  xq[j] = quant_value(v, inv, bias);
+  if ((threadIdx.x & 31) == 0) xs[g] = scale;
+}
+
 }  // namespace ple

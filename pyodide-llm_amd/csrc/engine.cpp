@@ -70,15 +70,49 @@ Shape shape_of(const he_config &c, int id) {
     case HE_T_BQ: return {L * qdim, 0, 0, c.n_layers};
     case HE_T_BK: return {L * kvdim, 0, 0, c.n_layers};
     case HE_T_BV: return {L * kvdim, 0, 0, c.n_layers};
+    case HE_T_Q_NORM: return {L * c.head_size, 0, 0, c.n_layers};
+    case HE_T_K_NORM: return {L * c.head_size, 0, 0, c.n_layers};
+    case HE_T_POSITIONS: return {(int64_t)c.seq_len * dim, c.dim, c.seq_len, 1};
+    case HE_T_LN_ATT_BIAS: return {L * dim, 0, 0, c.n_layers};
+    case HE_T_LN_FFN_BIAS: return {L * dim, 0, 0, c.n_layers};
+    case HE_T_LN_FINAL_BIAS: return {dim, 0, 0, 1};
+    case HE_T_BO: return {L * dim, 0, 0, c.n_layers};
+    case HE_T_B1: return {L * hidden, 0, 0, c.n_layers};
+    case HE_T_B2: return {L * dim, 0, 0, c.n_layers};
   }
   return {0, 0, 0, 0};
 }
 
+bool layer_norm(const he_config &c) { return c.arch == HE_ARCH_GPT2 || c.arch == HE_ARCH_NEOX; }
+
+// the tensors of the form (public/llama2_convert.py:32-83): Llama's with Qwen2's biases and Qwen3's head norms where
+// the form has them; GPT-2's and GPT-NeoX's LayerNorm biases, biases after every matrix, no w3, GPT-2's positions
 bool present(const he_config &c, int id) {
-  if (id == HE_T_WCLS && c.shared_classifier) return false;  // the embedding's
-  if (id >= HE_T_BQ && !c.qkv_bias) return false;
+  switch (id) {
+    case HE_T_WCLS: return !c.shared_classifier;  // else the embedding's
+    case HE_T_W3: return !layer_norm(c);
+    case HE_T_BQ:
+    case HE_T_BK:
+    case HE_T_BV: return layer_norm(c) || c.qkv_bias;
+    case HE_T_Q_NORM:
+    case HE_T_K_NORM: return !layer_norm(c) && c.qk_norm;
+    case HE_T_POSITIONS: return c.arch == HE_ARCH_GPT2;
+    case HE_T_LN_ATT_BIAS:
+    case HE_T_LN_FFN_BIAS:
+    case HE_T_LN_FINAL_BIAS:
+    case HE_T_BO:
+    case HE_T_B1:
+    case HE_T_B2: return layer_norm(c);
+  }
   return true;
 }
+
+// the float32 vectors a synthetic checkpoint fills with 1.0 (norm weights); the others are biases, N(0, 0.02)
+bool norm_weight(int id) {
+  return id == HE_T_RMS_ATT || id == HE_T_RMS_FFN || id == HE_T_RMS_FINAL || id == HE_T_Q_NORM || id == HE_T_K_NORM;
+}
+
+static_assert(HE_OUTLIERS_MOST == 8, "OutlierSet holds 8 channels");
 
 struct Region {
   uint64_t file, bytes, dev;
@@ -134,6 +168,10 @@ struct he_engine {
   int32_t *sample_index = nullptr, *window = nullptr, *sample_token = nullptr;
   float *sample_best = nullptr;
   int32_t *host_window = nullptr;
+  // the other forms: the layer's input a parallel residual's FFN normalizes (GPT-NeoX); the outlier channels' float32
+  // columns of the classifier [n][vocab] and the values taken out of the classifier's input
+  float *before = nullptr, *columns = nullptr, *picked = nullptr;
+  OutlierSet outliers{};
   bool replayable = false;  // run_chunk is building the graph (positions from state, no host copies)
   // he_profile_forward: event pairs around every launch while `profiling` is set
   struct Mark {
@@ -167,7 +205,7 @@ void destroy(he_engine *e) {
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
                   e->best_v, e->best_i, e->state, e->step_ids, e->step_values, e->sample_probs, e->sample_index,
-                  e->window, e->sample_token, e->sample_best};
+                  e->window, e->sample_token, e->sample_best, e->before, e->columns, e->picked};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   void *pinned[] = {e->host_ids, e->host_state, e->host_values, e->host_window};
@@ -189,6 +227,25 @@ int32_t check_config(const he_config &c) {
   if (!attention_supported(c.head_size, c.n_heads, c.n_kv_heads))
     return fail(HE_E_ARG, "attention takes head sizes 16, 32, 48, 64, 96, 128, 256 and at most 8 query heads a kv head");
   if (c.seq_len % 4) return fail(HE_E_ARG, "seq_len must be a multiple of 4");
+  if (c.arch != HE_ARCH_LLAMA && c.arch != HE_ARCH_GPT2 && c.arch != HE_ARCH_NEOX)
+    return fail(HE_E_ARG, "arch is not one of llama, gpt2, neox");
+  if (layer_norm(c)) {
+    if (qdim != c.dim) return fail(HE_E_ARG, "a GPT-2 / GPT-NeoX form has heads of dim / n_heads");
+    if (c.qk_norm) return fail(HE_E_ARG, "q/k head norms belong to the llama form (Qwen3)");
+    if (c.dim > 16384) return fail(HE_E_ARG, "LayerNorm takes rows of at most 16384");
+  } else if (c.parallel_residual) {
+    return fail(HE_E_ARG, "a parallel residual belongs to the GPT-NeoX form");
+  }
+  if (c.arch == HE_ARCH_NEOX && (c.rotary < 0 || c.rotary % 2 || c.rotary > c.head_size))
+    return fail(HE_E_ARG, "rotary must be even and at most head_size");
+  if (c.arch == HE_ARCH_LLAMA && c.rotary && c.rotary != c.head_size)
+    return fail(HE_E_ARG, "the llama form turns every value of a head (rotary 0 or head_size)");
+  if (c.qk_norm && c.head_size > 256) return fail(HE_E_ARG, "q/k head norms take heads of at most 256");
+  if (c.n_outliers < 0 || c.n_outliers > HE_OUTLIERS_MOST)
+    return fail(HE_E_ARG, "at most 8 outlier channels (OUTLIER_CHANNELS)");
+  for (int32_t i = 0; i < c.n_outliers; ++i)
+    if (c.outliers[i] < 0 || c.outliers[i] >= c.dim || (i > 0 && c.outliers[i] <= c.outliers[i - 1]))
+      return fail(HE_E_ARG, "outlier channels must be distinct channels below dim, in increasing order");
   return HE_OK;
 }
 
@@ -301,11 +358,28 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->window, sizeof(int32_t) * REPETITION_WINDOW);
   ALLOC(e->sample_token, sizeof(int32_t) * 4);
   ALLOC(e->sample_best, sizeof(float) * 4);
+  if (c.parallel_residual) ALLOC(e->before, sizeof(float) * T * c.dim);
+  e->outliers.n = c.n_outliers;
+  for (int32_t i = 0; i < c.n_outliers; ++i) e->outliers.c[i] = c.outliers[i];
+  if (c.n_outliers) {
+    ALLOC(e->columns, sizeof(float) * c.n_outliers * (size_t)c.vocab_size);
+    ALLOC(e->picked, sizeof(float) * HE_OUTLIERS_MOST);
+  }
 #undef ALLOC
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_ids), sizeof(int32_t) * STEPS_A_ROUND));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_values), sizeof(float) * STEPS_A_ROUND));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_state), sizeof(int32_t) * 4));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_window), sizeof(int32_t) * REPETITION_WINDOW));
+  return HE_OK;
+}
+
+// the outlier channels' columns of the classifier (public/forward.js:801-812), once its bytes are on the device
+int32_t prepare_outliers(he_engine *e) {
+  const he_config &c = e->c;
+  if (!c.n_outliers) return HE_OK;
+  HIP_TRY(launch_outlier_columns(e->columns, e->values[HE_T_WCLS], e->scales[HE_T_WCLS], c.vocab_size, c.dim,
+                                 c.six ? 32 : group_size(c.dim), c.six, e->outliers, e->stream));
+  HIP_TRY(hipStreamSynchronize(e->stream));
   return HE_OK;
 }
 
@@ -445,9 +519,13 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
   const size_t esz = c.half_kv ? 2 : 4;
   const int32_t *dpos = e->replayable ? e->state : nullptr;  // a replayed step: the position in device memory
   if (!e->replayable) HIP_TRY(hipMemcpyAsync(e->tokens, tokens, sizeof(int32_t) * m, hipMemcpyHostToDevice, s));
+  const bool ln = layer_norm(c);  // GPT-2 / GPT-NeoX: LayerNorm, GELU, biases after every matrix
+  Positions positions{};
+  if (c.arch == HE_ARCH_GPT2)
+    positions = {e->values[HE_T_POSITIONS], e->scales[HE_T_POSITIONS], c.six ? 32 : group_size(dim), pos0, dpos};
   HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * dim * (c.six ? 0.75 + 0.125 + 4 : 1 + 0.125 + 4), [&] {
     return launch_embed(e->x, e->tokens, e->values[HE_T_EMBEDDING], e->scales[HE_T_EMBEDDING], m, dim, dim,
-                        c.six ? 32 : group_size(dim), c.six, s);
+                        c.six ? 32 : group_size(dim), c.six, positions, s);
   }));
   for (int32_t l = 0; l < c.n_layers; ++l) {
     const MatSeg qkv[3] = {
@@ -460,9 +538,10 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     qp.v = e->v;
     qp.q_stride = qdim;
     qp.kv_stride = kvdim;
-    qp.bq = c.qkv_bias ? e->vec(HE_T_BQ, (int64_t)l * qdim) : nullptr;
-    qp.bk = c.qkv_bias ? e->vec(HE_T_BK, (int64_t)l * kvdim) : nullptr;
-    qp.bv = c.qkv_bias ? e->vec(HE_T_BV, (int64_t)l * kvdim) : nullptr;
+    const bool biases = c.qkv_bias || ln;
+    qp.bq = biases ? e->vec(HE_T_BQ, (int64_t)l * qdim) : nullptr;
+    qp.bk = biases ? e->vec(HE_T_BK, (int64_t)l * kvdim) : nullptr;
+    qp.bv = biases ? e->vec(HE_T_BV, (int64_t)l * kvdim) : nullptr;
     qp.cos_t = e->cos_t;
     qp.sin_t = e->sin_t;
     qp.kcache = reinterpret_cast<uint8_t *>(e->keys) + (size_t)l * c.seq_len * kvdim * esz;
@@ -475,17 +554,35 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     qp.half = c.half_kv;
     qp.vstride = value_stride(c.seq_len);
     qp.dpos = dpos;
-    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
-                                  W, W / 32, 0, c.rms_norm_eps, e->bias, s);
-    }));
-    if (m == 1 && decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0)) {
+    qp.rot = c.arch == HE_ARCH_GPT2 ? 0 : (c.rotary > 0 && c.rotary < hs ? c.rotary : hs);
+    if (ln) {
+      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 8.0, [&] {
+        return launch_layernorm_quant(e->xq, e->xs, nullptr, c.parallel_residual ? e->before : nullptr, e->x,
+                                      e->vec(HE_T_RMS_ATT, (int64_t)l * dim), e->vec(HE_T_LN_ATT_BIAS, (int64_t)l * dim),
+                                      m, dim, dim, W, W / 32, 0, e->bias, s);
+      }));
+    } else {
+      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
+                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+      }));
+    }
+    if (c.arch == HE_ARCH_LLAMA && !c.qk_norm && m == 1 && decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0)) {
       // one token: the q/k/v GEMV adds the biases, rotates q and k and writes k and v into the cache itself
       const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv,
                          qp.vstride, dpos};
       HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, nullptr, &fuse));
     } else {
       HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
+      if (c.qk_norm) {
+        // Qwen3: the q/k biases, then every head normalized, before RoPE
+        HIP_TRY(timed(e, HE_K_NORM, (double)m * (qdim + kvdim) * 8, [&] {
+          return launch_head_norm(e->q, e->k, qp.bq, qp.bk, e->vec(HE_T_Q_NORM, (int64_t)l * hs),
+                                  e->vec(HE_T_K_NORM, (int64_t)l * hs), m, c.n_heads, c.n_kv_heads, hs, qdim, kvdim,
+                                  c.rms_norm_eps, s);
+        }));
+        qp.bq = qp.bk = nullptr;
+      }
       HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * (qdim + 2 * kvdim) * 8 + (double)m * 2 * kvdim * esz,
                     [&] { return launch_qkv_post(qp, s); }));
     }
@@ -529,6 +626,27 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
                     [&] { return launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s); }));
       HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
     }
+    if (ln) {
+      // x += bo; LayerNorm of x (or of the layer's input: parallel residual); w1; gelu(+ b1); w2; x += b2
+      HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * dim * 12,
+                    [&] { return launch_add_rows(e->x, e->vec(HE_T_BO, (int64_t)l * dim), m, dim, dim, s); }));
+      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 8.0, [&] {
+        return launch_layernorm_quant(e->xq, e->xs, nullptr, nullptr, c.parallel_residual ? e->before : e->x,
+                                      e->vec(HE_T_RMS_FFN, (int64_t)l * dim), e->vec(HE_T_LN_FFN_BIAS, (int64_t)l * dim),
+                                      m, dim, dim, W, W / 32, 0, e->bias, s);
+      }));
+      const MatSeg w1[1] = {{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), e->hb, hidden, hidden, 0}};
+      HIP_TRY(matmul(e, w1, 1, dim, m, e->xq, e->xs));
+      HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * hidden * (8 + 1 + 0.125), [&] {
+        return launch_gelu_quant(e->xq, e->xs, nullptr, e->hb, e->vec(HE_T_B1, (int64_t)l * hidden), m, hidden,
+                                 hidden, W, W / 32, e->bias, s);
+      }));
+      const MatSeg w2g[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
+      HIP_TRY(matmul(e, w2g, 1, hidden, m, e->xq, e->xs));
+      HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * dim * 12,
+                    [&] { return launch_add_rows(e->x, e->vec(HE_T_B2, (int64_t)l * dim), m, dim, dim, s); }));
+      continue;
+    }
     HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
       return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
                                   W / 32, 0, c.rms_norm_eps, e->bias, s);
@@ -543,12 +661,29 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs));
   }
   if (need_logits) {
+    // the final norm; with outlier channels its float32 output too, whose channels are taken out and the rest
+    // quantized again (public/forward.js:1082-1089)
+    const bool apart = c.n_outliers > 0;
+    const float *last = e->x + (int64_t)(m - 1) * dim;
     HIP_TRY(timed(e, HE_K_NORM, (double)dim * (8 + 1 + 0.125), [&] {
-      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x + (int64_t)(m - 1) * dim, e->vec(HE_T_RMS_FINAL, 0), 1,
-                                  dim, dim, W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+      return ln ? launch_layernorm_quant(e->xq, e->xs, apart ? e->xb : nullptr, nullptr, last,
+                                         e->vec(HE_T_RMS_FINAL, 0), e->vec(HE_T_LN_FINAL_BIAS, 0), 1, dim, dim, W,
+                                         W / 32, e->xw, e->bias, s)
+                : launch_rmsnorm_quant(e->xq, e->xs, apart ? e->xb : nullptr, last, e->vec(HE_T_RMS_FINAL, 0), 1,
+                                       dim, dim, W, W / 32, e->xw, c.rms_norm_eps, e->bias, s);
     }));
+    if (apart) {
+      HIP_TRY(timed(e, HE_K_ELEMENTWISE, 64.0, [&] { return launch_pick(e->xb, e->picked, e->outliers, s); }));
+      HIP_TRY(timed(e, HE_K_NORM, (double)dim * (4 + 1 + 0.125), [&] {
+        return launch_quantize(e->xq, e->xs, e->xb, 1, dim, e->xw, W, W / 32, e->bias, s);
+      }));
+    }
     const MatSeg cls[1] = {{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), e->logits, c.vocab_size, 0, 0}};
     HIP_TRY(matmul(e, cls, 1, dim, 1, e->xq, e->xs));
+    if (apart)
+      HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)c.vocab_size * (8 + 4 * c.n_outliers), [&] {
+        return launch_add_columns(e->logits, e->columns, e->picked, c.n_outliers, c.vocab_size, s);
+      }));
     e->have_logits = true;
   }
   return HE_OK;
@@ -589,6 +724,7 @@ int32_t he_open(const he_config *cfg, const he_tensor *tensors, const void *chec
       }
     }
   }
+  if (rc == HE_OK) rc = prepare_outliers(e);
   if (rc != HE_OK) {
     destroy(e);
     return rc;
@@ -619,11 +755,13 @@ int32_t he_open_synthetic(const he_config *cfg, const he_tensor *tensors, uint64
         err = launch_synth_matrix(vals, const_cast<float *>(e->scales[id]), s.count / s.k, s.k, seed, id, factor,
                                   c.six, e->stream);
       } else {
-        err = launch_synth_vector(reinterpret_cast<float *>(vals), s.count, seed, id, factor, id < HE_T_BQ, e->stream);
+        err = launch_synth_vector(reinterpret_cast<float *>(vals), s.count, seed, id, factor, norm_weight(id),
+                                e->stream);
       }
     }
     if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
     if (err != hipSuccess && rc == HE_OK) rc = fail(HE_E_HIP, std::string("synthesis: ") + hipGetErrorString(err));
+    if (rc == HE_OK) rc = prepare_outliers(e);
   }
   if (rc != HE_OK) {
     destroy(e);
@@ -862,10 +1000,12 @@ int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *m
                      3, dim});
     if (which == -1 || which == 1)
       seq.push_back({{{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), out, dim, dim, 1}}, 1, qdim});
-    if (which == -1 || which == 2)
+    if ((which == -1 || which == 2) && present(c, HE_T_W3))
       seq.push_back({{{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), out, hidden, hidden, 0},
                       {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), out + hidden, hidden, hidden, 0}},
                      2, dim});
+    else if (which == -1 || which == 2)
+      seq.push_back({{{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), out, hidden, hidden, 0}}, 1, dim});
     if (which == -1 || which == 3)
       seq.push_back({{{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), out, dim, dim, 1}}, 1, hidden});
   }

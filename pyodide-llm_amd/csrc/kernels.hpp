@@ -80,9 +80,17 @@ hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *
 hipError_t launch_swiglu_quant(int8_t *xq, float *xs, float *out, const float *h1, const float *h3, int32_t m,
                                int32_t n, int32_t h_stride, int32_t xq_stride, int32_t xs_stride, int32_t bias,
                                hipStream_t s);
-// embedding rows of m tokens (int8 or int6 table) into x (x_stride apart)
+// embedding rows of m tokens (int8 or int6 table) into x (x_stride apart); with a positions table (GPT-2's, the same
+// kind, its group pgroup), the row of position (dpos ? *dpos : pos0) + t widened and added to each
+struct Positions {
+  const uint8_t *table;  // null: none
+  const float *scales;
+  int32_t group, pos0;
+  const int32_t *dpos;
+};
 hipError_t launch_embed(float *x, const int32_t *tokens, const uint8_t *table, const float *scales, int32_t m,
-                        int32_t dim, int32_t x_stride, int32_t group, bool six, hipStream_t s);
+                        int32_t dim, int32_t x_stride, int32_t group, bool six, const Positions &positions,
+                        hipStream_t s);
 // per token: + bias (optional), RoPE on q and k at pos0 + t, k and v into the cache (f32 or f16)
 struct QkvPost {
   float *q;
@@ -94,6 +102,7 @@ struct QkvPost {
   void *kcache, *vcache;       // this layer's keys [seq_len][kv_dim] and values [kv_dim][vstride]
   int32_t nh, nkv, hs, pos0, m, half, vstride;
   const int32_t *dpos;  // the first position in device memory (a replayed decode step), or null: pos0
+  int32_t rot;          // the values of each head RoPE turns (kernels/kernel.ts:344-357): hs all, 0 none (GPT-2)
 };
 hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s);
 
@@ -137,6 +146,30 @@ hipError_t launch_sample(const float *logits, int32_t n, float temperature, floa
 // input (tokens[0]), state[0] (the position) and state[1] (the step) advanced
 hipError_t launch_advance(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
                           float *values, hipStream_t s);
+
+// ---- the other forms (forms.hip) ----
+// layernorm (eps 1e-5) then quantize_x, m tokens; out (optional) the float32 rows; copy (optional, x_stride) x itself
+hipError_t launch_layernorm_quant(int8_t *xq, float *xs, float *out, float *copy, const float *x, const float *w,
+                                  const float *b, int32_t m, int32_t n, int32_t x_stride, int32_t xq_stride,
+                                  int32_t xs_stride, int32_t out_stride, int32_t bias, hipStream_t s);
+// gelu(h + b) then quantize_x, m tokens (n a multiple of 32)
+hipError_t launch_gelu_quant(int8_t *xq, float *xs, float *out, const float *h, const float *b, int32_t m, int32_t n,
+                             int32_t h_stride, int32_t xq_stride, int32_t xs_stride, int32_t bias, hipStream_t s);
+// x[t][j] += b[j] for m rows of n, stride apart
+hipError_t launch_add_rows(float *x, const float *b, int32_t m, int32_t n, int32_t stride, hipStream_t s);
+// Qwen3: q and k heads + bias (optional), then RMS-normalized in place by qw / kw (hs values each)
+hipError_t launch_head_norm(float *q, float *k, const float *bq, const float *bk, const float *qw, const float *kw,
+                            int32_t m, int32_t nh, int32_t nkv, int32_t hs, int32_t q_stride, int32_t kv_stride,
+                            float eps, hipStream_t s);
+// the outlier channels of the classifier's input
+struct OutlierSet {
+  int32_t n;
+  int32_t c[8];
+};
+hipError_t launch_outlier_columns(float *columns, const uint8_t *table, const float *scales, int32_t vocab,
+                                  int32_t dim, int32_t group, bool six, const OutlierSet &set, hipStream_t s);
+hipError_t launch_pick(float *x, float *picked, const OutlierSet &set, hipStream_t s);
+hipError_t launch_add_columns(float *y, const float *columns, const float *a, int32_t n, int32_t vocab, hipStream_t s);
 
 // device synthesis of a checkpoint (the oracle's or_synth_checkpoint bits)
 hipError_t launch_synth_matrix(uint8_t *values, float *scales, int64_t rows, int32_t k, uint64_t seed, int32_t stream,

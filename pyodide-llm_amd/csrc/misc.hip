@@ -1,7 +1,7 @@
 // misc.hip — the per-token elementwise work around the matmuls, each in the reference's float32 order:
 //   quantize_x (kernels/kernel.ts:129-156), rmsnorm (:330-342) then quantize_x, swiglu (:654-667) then quantize_x,
-//   embed (public/forward.js:962-973 with valueAt :692-696), the q/k/v bias add (:691-693, public/forward.js:1038-1042),
-//   rope (:344-357) and the KV-cache write (to_f16 :570-599 or a copy, public/forward.js:998-1006), argmax (:695-699),
+//   embed (public/forward.js:962-973 with valueAt :692-696; GPT-2's positions added), the q/k/v bias add (:691-693,
+//   public/forward.js:1038-1042), rope (:344-357, over the first `rot` values of each head) and the KV-cache write (to_f16 :570-599 or a copy, public/forward.js:998-1006), argmax (:695-699),
 //   and the device twin of the oracle's synthetic checkpoint.
 #pragma clang fp contract(off)
 
@@ -11,16 +11,6 @@
 namespace ple {
 
 namespace {
-
-// one group of 32 a half-wave: amax (order-free), scale = f32(amax / qmax), inv = scale > 0 ? f32(1 / scale) : 0
-__device__ __forceinline__ void quantize_group(float v, int8_t *xq, float *xs, int j, int g, int32_t bias) {
-  const float qmax = bias == 0 ? 127.0f : 63.0f;
-  const float amax = wave_max32(__builtin_fabsf(v));
-  const float scale = amax / qmax;
-  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
-  xq[j] = quant_value(v, inv, bias);
-  if ((threadIdx.x & 31) == 0) xs[g] = scale;
-}
 
 __global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n,
                                                        int32_t x_stride, int32_t xq_stride, int32_t xs_stride,
@@ -114,25 +104,33 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(int8_t *xq, float *xs
   quantize_group(o, xq + (int64_t)t * xq_stride, xs + (int64_t)t * xs_stride, j, g, bias);
 }
 
-// embed: x_i = f32(int8 * scale of its group) for the token's row
+// valueAt (public/forward.js:672-696): f32(int8 or unpacked int6 value * the scale of its group)
+__device__ __forceinline__ float value_at(const uint8_t *table, const float *scales, int64_t at, int32_t group,
+                                          int32_t six) {
+  int32_t v;
+  if (six) {
+    const uint8_t *b = table + (at >> 5) * 24;
+    const int j = (int)(at & 31);
+    const int low = j < 16 ? (b[j] & 15) : (b[j - 16] >> 4);
+    const int top = (b[16 + (j & 7)] >> (2 * (j >> 3))) & 3;
+    v = (int8_t)(uint8_t)((low | (top << 4)) << 2);
+  } else {
+    v = (int8_t)table[at];
+  }
+  return (float)v * scales[at / group];
+}
+
+// embed: x_i = f32(int8 * scale of its group) for the token's row; GPT-2's position row (widened the same way) added
 __global__ __launch_bounds__(256) void embed_kernel(float *x, const int32_t *tokens, const uint8_t *table,
                                                     const float *scales, int32_t dim, int32_t x_stride, int32_t group,
-                                                    int32_t six) {
+                                                    int32_t six, const Positions p) {
   const int t = blockIdx.y;
   const int64_t row = (int64_t)tokens[t] * dim;
+  const int64_t prow = p.table ? (int64_t)((p.dpos ? *p.dpos : p.pos0) + t) * dim : 0;
   for (int i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256) {
-    const int64_t at = row + i;
-    int32_t v;
-    if (six) {
-      const uint8_t *b = table + (at >> 5) * 24;
-      const int j = (int)(at & 31);
-      const int low = j < 16 ? (b[j] & 15) : (b[j - 16] >> 4);
-      const int top = (b[16 + (j & 7)] >> (2 * (j >> 3))) & 3;
-      v = (int8_t)(uint8_t)((low | (top << 4)) << 2);
-    } else {
-      v = (int8_t)table[at];
-    }
-    x[(int64_t)t * x_stride + i] = (float)v * scales[at / group];
+    float v = value_at(table, scales, row + i, group, six);
+    if (p.table) v = v + value_at(p.table, p.scales, prow + i, p.group, six);
+    x[(int64_t)t * x_stride + i] = v;
   }
 }
 
@@ -155,9 +153,13 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const QkvPost a) {
         v0 = v0 + bias[i];
         v1 = v1 + bias[i + 1];
       }
-      const int ci = (i % a.hs) >> 1;
-      const float c = cs[ci], s = sn[ci];
-      const float o0 = v0 * c - v1 * s, o1 = v0 * s + v1 * c;
+      float o0 = v0, o1 = v1;
+      if (i % a.hs < a.rot) {
+        const int ci = (i % a.hs) >> 1;
+        const float c = cs[ci], s = sn[ci];
+        o0 = v0 * c - v1 * s;
+        o1 = v0 * s + v1 * c;
+      }
       base[i] = o0;
       base[i + 1] = o1;
       if (!isq) {
@@ -327,9 +329,10 @@ hipError_t launch_swiglu_quant(int8_t *xq, float *xs, float *out, const float *h
 }
 
 hipError_t launch_embed(float *x, const int32_t *tokens, const uint8_t *table, const float *scales, int32_t m,
-                        int32_t dim, int32_t x_stride, int32_t group, bool six, hipStream_t s) {
+                        int32_t dim, int32_t x_stride, int32_t group, bool six, const Positions &positions,
+                        hipStream_t s) {
   hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(dim, 256, 64), m), dim3(256), 0, s, x, tokens, table, scales, dim,
-                     x_stride, group, (int32_t)six);
+                     x_stride, group, (int32_t)six, positions);
   return hipGetLastError();
 }
 

@@ -142,7 +142,8 @@ static int field_i32(napi_env env, napi_value obj, const char *name, int32_t *ou
   return 1;
 }
 
-/* he_config from {dim, hidden_dim, ..., rms_norm_eps} (the names of include/pyodide_llm_hip.h) */
+/* he_config from {dim, hidden_dim, ..., rms_norm_eps, arch, rotary, parallel_residual, qk_norm, outliers: [...]} (the
+ * names of include/pyodide_llm_hip.h) */
 static int config_of(napi_env env, napi_value obj, he_config *c) {
   memset(c, 0, sizeof *c);
   static const char *names[] = {"dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "head_size", "vocab_size",
@@ -159,6 +160,22 @@ static int config_of(napi_env env, napi_value obj, he_config *c) {
     return 0;
   }
   c->rms_norm_eps = (float)eps;
+  static const char *forms[] = {"arch", "rotary", "parallel_residual", "qk_norm"};
+  int32_t *form_fields[] = {&c->arch, &c->rotary, &c->parallel_residual, &c->qk_norm};
+  for (size_t i = 0; i < sizeof forms / sizeof forms[0]; ++i)
+    if (!field_i32(env, obj, forms[i], form_fields[i])) return 0;
+  /* outliers: an array of at most HE_OUTLIERS_MOST channels */
+  uint32_t n = 0;
+  if (napi_get_named_property(env, obj, "outliers", &v) != napi_ok || napi_get_array_length(env, v, &n) != napi_ok ||
+      n > HE_OUTLIERS_MOST) {
+    napi_throw_type_error(env, NULL, "hip_engine: config.outliers is not an array of at most 8 channels");
+    return 0;
+  }
+  c->n_outliers = (int32_t)n;
+  for (uint32_t i = 0; i < n; ++i) {
+    napi_value e;
+    if (napi_get_element(env, v, i, &e) != napi_ok || !get_i32(env, e, &c->outliers[i])) return 0;
+  }
   return 1;
 }
 
@@ -166,7 +183,7 @@ static int config_of(napi_env env, napi_value obj, he_config *c) {
 static int tensors_of(napi_env env, napi_value arr, he_tensor *t) {
   uint32_t n = 0;
   if (napi_get_array_length(env, arr, &n) != napi_ok || n != HE_T_COUNT) {
-    napi_throw_type_error(env, NULL, "hip_engine: tensors must be an array of 15 [offset, scales] pairs");
+    napi_throw_type_error(env, NULL, "hip_engine: tensors must be an array of HE_T_COUNT (24) [offset, scales] pairs");
     return 0;
   }
   for (uint32_t i = 0; i < n; ++i) {

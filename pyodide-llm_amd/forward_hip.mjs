@@ -24,7 +24,11 @@ export const PROMPT_BLOCK = 512;
 export const TOKEN_BLOCK = 16;
 // include/pyodide_llm_hip.h HE_T_*: the tensors the forward reads, by their plan names
 const TENSORS = ["token_embedding_table", "rms_att_weight", "wq", "wk", "wv", "wo", "rms_ffn_weight", "w1", "w2", "w3",
-  "rms_final_weight", "wcls", "bq", "bk", "bv"];
+  "rms_final_weight", "wcls", "bq", "bk", "bv", "q_norm", "k_norm", "positions", "ln_att_bias", "ln_ffn_bias",
+  "ln_final_bias", "bo", "b1", "b2"];
+// include/pyodide_llm_hip.h HE_ARCH_*, HE_OUTLIERS_MOST
+const ARCHS = { llama: 0, gpt2: 1, neox: 2 };
+const OUTLIERS_MOST = 8;
 // include/pyodide_llm_hip.h HE_K_*
 const KINDS = ["gemv", "gemm", "attention", "norm", "elementwise", "argmax"];
 
@@ -81,21 +85,26 @@ function floats(bytes, count, name) {
   return new Float32Array(copy.buffer);
 }
 
-/** The engine's config and tensor places from a plan (public/llama2_numpy.py:1261-1270). The forms the engine does not
- * run are refused by name, as public/forward.js refuses what its kernels cannot take. */
+/** The engine's config and tensor places from a plan (public/llama2_numpy.py:1261-1270): the llama form (Qwen2's
+ * biases and Qwen3's head norms where the plan has those tensors), gpt2 and neox (public/forward.js:636). The forms the
+ * engine does not run are refused by name, as public/forward.js refuses what its kernels cannot take. */
 export function planToConfig(plan, { relaxedKernels = true, halfKeys } = {}) {
-  if (or(plan.arch, "llama") !== "llama") throw new Error(`the HIP engine runs the Llama/Qwen2 form, not ${plan.arch}`);
-  if (plan.parallel_residual) throw new Error("the HIP engine has no parallel residual (GPT-NeoX)");
-  if (plan.outliers && plan.outliers.length) throw new Error("outlier channels are not supported by the HIP engine");
+  const arch = or(plan.arch, "llama");
+  if (!(arch in ARCHS)) throw new Error(`the HIP engine runs the llama, gpt2 and neox forms, not ${arch}`);
   if (!plan.int8) throw new Error("the HIP engine multiplies int8/int6 matrices only (plan.int8)");
-  const T = plan.tensors;
-  if (T.q_norm || T.k_norm) throw new Error("Qwen3 q/k norms are not supported by the HIP engine");
-  const kinds = new Set(["wq", "wk", "wv", "wo", "w1", "w2", "w3", "token_embedding_table"].map((n) => T[n] && T[n].kind));
+  const T = plan.tensors, layerNorm = arch !== "llama";
+  const names = ["wq", "wk", "wv", "wo", "w1", "w2", "token_embedding_table", ...(layerNorm ? [] : ["w3"]),
+    ...(arch === "gpt2" ? ["positions"] : [])];
+  const kinds = new Set(names.map((n) => T[n] && T[n].kind));
   if (kinds.size !== 1 || !(kinds.has("int8") || kinds.has("int6"))) {
     throw new Error(`the HIP engine takes int8 or int6 matrices, not ${[...kinds].join(", ")}`);
   }
   const rotary = Number(plan.rotary || 0);
-  if (rotary && rotary !== plan.head_size) throw new Error("partial rotary embeddings are not supported by the HIP engine");
+  if (arch === "llama" && rotary && rotary !== plan.head_size) {
+    throw new Error("partial rotary embeddings belong to the neox form");
+  }
+  const outliers = [...or(fromJs(plan.outliers), [])].map(Number).sort((a, b) => a - b);
+  if (outliers.length > OUTLIERS_MOST) throw new Error(`at most ${OUTLIERS_MOST} outlier channels`);
   const heads = plan.n_heads, kvHeads = plan.n_kv_heads;
   const config = {
     dim: plan.dim, hidden_dim: plan.hidden_dim, n_layers: plan.n_layers, n_heads: heads, n_kv_heads: kvHeads,
@@ -106,6 +115,9 @@ export function planToConfig(plan, { relaxedKernels = true, halfKeys } = {}) {
     // public/forward.js:762
     half_kv: plan.half_kv && or(halfKeys, kvHeads >= heads) ? 1 : 0,
     rms_norm_eps: or(plan.rms_norm_eps, 1e-5),
+    arch: ARCHS[arch], rotary: arch === "neox" ? rotary : 0,
+    parallel_residual: layerNorm && plan.parallel_residual ? 1 : 0,
+    qk_norm: T.q_norm && T.k_norm ? 1 : 0, outliers,
   };
   const tensors = TENSORS.map((name) => {
     const t = name === "wcls" && config.shared_classifier ? T.token_embedding_table : T[name];

@@ -18,7 +18,10 @@ LIBRARY = os.path.join(HERE, "libpyodide_llm_hip.so")
 # include/pyodide_llm_hip.h HE_T_*: the tensors the forward reads, by their plan names (public/llama2_numpy.py
 # TENSOR_NAMES)
 TENSORS = ("token_embedding_table", "rms_att_weight", "wq", "wk", "wv", "wo", "rms_ffn_weight", "w1", "w2", "w3",
-           "rms_final_weight", "wcls", "bq", "bk", "bv")
+           "rms_final_weight", "wcls", "bq", "bk", "bv", "q_norm", "k_norm", "positions", "ln_att_bias", "ln_ffn_bias",
+           "ln_final_bias", "bo", "b1", "b2")
+ARCHS = {"llama": 0, "gpt2": 1, "neox": 2}  # include/pyodide_llm_hip.h HE_ARCH_*
+OUTLIERS_MOST = 8  # HE_OUTLIERS_MOST (public/llama2_numpy.py:561 OUTLIER_CHANNELS)
 T = {name: i for i, name in enumerate(TENSORS)}
 HE_OK, HE_E_ARG, HE_E_HIP, HE_E_STATE, HE_E_NOTFINITE = 0, -1, -2, -3, -4
 KINDS = ("gemv", "gemm", "attention", "norm", "elementwise", "argmax")  # include/pyodide_llm_hip.h HE_K_*
@@ -29,7 +32,9 @@ NOT_FINITE = ("The model computed logits that are not finite numbers (NaN or inf
 class HeConfig(ctypes.Structure):
     _fields_ = [(name, ctypes.c_int32) for name in (
         "dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "head_size", "vocab_size", "seq_len",
-        "shared_classifier", "six", "qkv_bias", "relaxed", "half_kv")] + [("rms_norm_eps", ctypes.c_float)]
+        "shared_classifier", "six", "qkv_bias", "relaxed", "half_kv")] + [("rms_norm_eps", ctypes.c_float)] + [
+        (name, ctypes.c_int32) for name in ("arch", "rotary", "parallel_residual", "qk_norm", "n_outliers")] + [
+        ("outliers", ctypes.c_int32 * OUTLIERS_MOST)]
 
 
 class HeTensor(ctypes.Structure):
@@ -40,12 +45,20 @@ TensorArray = HeTensor * len(TENSORS)
 
 
 def config(**fields):
-    """an HeConfig from keyword fields; relaxed defaults to 1 (bias 64, the reference's default path), eps 1e-5"""
+    """an HeConfig from keyword fields; relaxed defaults to 1 (bias 64, the reference's default path), eps 1e-5;
+    outliers takes a list of channels"""
     c = HeConfig()
     c.relaxed = 1
     c.rms_norm_eps = 1e-5
     for key, value in fields.items():
-        setattr(c, key, value)
+        if key == "outliers":
+            c.n_outliers = len(value)
+            for i, channel in enumerate(value):
+                c.outliers[i] = int(channel)
+        elif key == "arch" and isinstance(value, str):
+            c.arch = ARCHS[value]
+        else:
+            setattr(c, key, value)
     if c.head_size == 0 and c.n_heads:
         c.head_size = c.dim // c.n_heads
     return c
@@ -111,34 +124,39 @@ def _ptr(a):
 
 
 def plan_to_config(plan, half_keys=None):
-    """he_config and he_tensor[] from a plan dict (public/llama2_numpy.py:1261-1270); forms the engine does not take
-    are refused by name, as public/forward.js refuses what its kernels cannot run. Keys and values are float16 where
-    the plan allows it and every head has its own (or half_keys says so): public/forward.js:762"""
-    if plan.get("arch", "llama") != "llama":
-        raise HipError(f"the engine runs the Llama/Qwen2 form, not {plan['arch']}")
-    if plan.get("parallel_residual"):
-        raise HipError("the engine has no parallel residual (GPT-NeoX)")
-    if plan.get("outliers"):
-        raise HipError("outlier channels are not supported by the engine")
+    """he_config and he_tensor[] from a plan dict (public/llama2_numpy.py:1261-1270): the llama form (with Qwen2's
+    biases and Qwen3's head norms where the tensors are there), gpt2 and neox (public/forward.js:636); forms the engine
+    does not take are refused by name, as public/forward.js refuses what its kernels cannot run. Keys and values are
+    float16 where the plan allows it and every head has its own (or half_keys says so): public/forward.js:762"""
+    arch = plan.get("arch", "llama")
+    if arch not in ARCHS:
+        raise HipError(f"the engine runs the llama, gpt2 and neox forms, not {arch}")
     if not plan.get("int8"):
         raise HipError("the engine multiplies int8/int6 matrices only (plan.int8)")
     tensors = plan["tensors"]
-    if "q_norm" in tensors or "k_norm" in tensors:
-        raise HipError("Qwen3 q/k norms are not supported by the engine")
-    kinds = {tensors[name]["kind"] for name in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "token_embedding_table")}
+    layer_norm = arch != "llama"
+    names = ("wq", "wk", "wv", "wo", "w1", "w2", "token_embedding_table") + (() if layer_norm else ("w3",)) + (
+        ("positions",) if arch == "gpt2" else ())
+    kinds = {tensors[name]["kind"] for name in names}
     if not kinds <= {"int8", "int6"} or len(kinds) != 1:
         raise HipError(f"the engine takes int8 or int6 matrices, not {sorted(kinds)}")
     six = kinds == {"int6"}
     rotary = int(plan.get("rotary") or 0)
-    if rotary and rotary != plan["head_size"]:
-        raise HipError("partial rotary embeddings are not supported by the engine")
+    if arch == "llama" and rotary and rotary != plan["head_size"]:
+        raise HipError("partial rotary embeddings belong to the neox form")
+    outliers = sorted(int(channel) for channel in (plan.get("outliers") or []))
+    if len(outliers) > OUTLIERS_MOST:
+        raise HipError(f"at most {OUTLIERS_MOST} outlier channels")
     c = config(dim=plan["dim"], hidden_dim=plan["hidden_dim"], n_layers=plan["n_layers"], n_heads=plan["n_heads"],
                n_kv_heads=plan["n_kv_heads"], head_size=plan["head_size"], vocab_size=plan["vocab_size"],
                seq_len=plan["seq_len"], shared_classifier=int(bool(plan["shared_classifier"])), six=int(six),
                qkv_bias=int("bq" in tensors), relaxed=int(bool(plan.get("relaxed", True))),
                half_kv=int(bool(plan.get("half_kv", False)) and (
                    bool(half_keys) if half_keys is not None else plan["n_kv_heads"] >= plan["n_heads"])),
-               rms_norm_eps=float(plan.get("rms_norm_eps", 1e-5)))
+               rms_norm_eps=float(plan.get("rms_norm_eps", 1e-5)), arch=ARCHS[arch],
+               rotary=rotary if arch == "neox" else 0,
+               parallel_residual=int(layer_norm and bool(plan.get("parallel_residual"))),
+               qk_norm=int("q_norm" in tensors and "k_norm" in tensors), outliers=outliers)
     t = TensorArray()
     for name, i in T.items():
         if name == "wcls" and c.shared_classifier:
@@ -152,7 +170,8 @@ def plan_to_config(plan, half_keys=None):
 
 
 class Engine:
-    """the object public/forward.js createForward returns, for the int8/int6 Llama and Qwen2 forms"""
+    """the object public/forward.js createForward returns, for int8/int6 checkpoints of the llama (Qwen2, Qwen3), gpt2
+    and neox forms"""
 
     backend = "MI355X HIP kernels (gfx950)"
 
@@ -290,7 +309,8 @@ def group_size(row_length):
 
 
 def places(cfg):
-    """public/llama2_numpy.py:751-775 Places.take over the Llama/Qwen2 tensor order (:1149-1179) of an int8 or int6
+    """public/llama2_numpy.py:751-775 Places.take over the tensor order of the form (public/llama2_convert.py:32-83:
+    Llama's, then Qwen2's biases and Qwen3's head norms; GPT-2's and GPT-NeoX's own order) of an int8 or int6
     checkpoint (which leaves the RoPE tables out): (HeTensor array, file size)"""
     t = TensorArray()
     offset = 28
@@ -308,6 +328,36 @@ def places(cfg):
         t[T[name]].offset, t[T[name]].scales = offset, 0
         offset += 4 * count
 
+    def classifier():
+        if cfg.shared_classifier:
+            t[T["wcls"]].offset, t[T["wcls"]].scales = t[0].offset, t[0].scales
+        else:
+            matrix("wcls", vocab * dim, dim)
+
+    if cfg.arch in (ARCHS["gpt2"], ARCHS["neox"]):  # llama2_numpy.py:1203-1240 gpt2_tensors
+        matrix("token_embedding_table", vocab * dim, dim)
+        if cfg.arch == ARCHS["gpt2"]:
+            matrix("positions", cfg.seq_len * dim, dim)
+        vector("rms_att_weight", L * dim)
+        vector("ln_att_bias", L * dim)
+        matrix("wq", L * dim * dim, dim)
+        matrix("wk", L * kvdim * dim, dim)
+        matrix("wv", L * kvdim * dim, dim)
+        vector("bq", L * dim)
+        vector("bk", L * kvdim)
+        vector("bv", L * kvdim)
+        matrix("wo", L * dim * dim, dim)
+        vector("bo", L * dim)
+        vector("rms_ffn_weight", L * dim)
+        vector("ln_ffn_bias", L * dim)
+        matrix("w1", L * hidden * dim, dim)
+        vector("b1", L * hidden)
+        matrix("w2", L * dim * hidden, hidden)
+        vector("b2", L * dim)
+        vector("rms_final_weight", dim)
+        vector("ln_final_bias", dim)
+        classifier()
+        return t, offset
     matrix("token_embedding_table", vocab * dim, dim)
     vector("rms_att_weight", L * dim)
     matrix("wq", L * qdim * dim, dim)
@@ -319,23 +369,28 @@ def places(cfg):
     matrix("w2", L * dim * hidden, hidden)
     matrix("w3", L * hidden * dim, dim)
     vector("rms_final_weight", dim)
-    if cfg.shared_classifier:
-        t[T["wcls"]].offset, t[T["wcls"]].scales = t[0].offset, t[0].scales
-    else:
-        matrix("wcls", vocab * dim, dim)
+    classifier()
     if cfg.qkv_bias:
         vector("bq", L * qdim)
         vector("bk", L * kvdim)
         vector("bv", L * kvdim)
+    if cfg.qk_norm:
+        vector("q_norm", L * cfg.head_size)
+        vector("k_norm", L * cfg.head_size)
     return t, offset
 
 
-def rope_tables(seq_len, head_size, theta):
+def rope_tables(seq_len, head_size, theta, rotary=0):
     """public/llama2_numpy.py:484-542 rope_tables() without scaling, as float32 (:1177-1179): what a caller hands the
-    engine as plan.derived"""
-    freq = 1.0 / theta ** (np.arange(0, head_size, 2, dtype=np.float64) / head_size)
+    engine as plan.derived. rotary (GPT-NeoX): the tables of the first `rotary` values of a head in the first
+    rotary / 2 columns, zeros past them (:1235-1240)"""
+    width = rotary if 0 < rotary < head_size else head_size
+    freq = 1.0 / theta ** (np.arange(0, width, 2, dtype=np.float64) / width)
     angles = np.arange(seq_len, dtype=np.float64)[:, None] * freq
-    return np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
+    cos = np.zeros((seq_len, head_size // 2), dtype=np.float32)
+    sin = np.zeros_like(cos)
+    cos[:, :width // 2], sin[:, :width // 2] = np.cos(angles), np.sin(angles)
+    return cos, sin
 
 
 def start(plan, checkpoint, max_block=2048):

@@ -3,9 +3,10 @@
 The fixtures pin the functions of the path that no closed form or known-answer test of the reference pins on its
 own: the bits of quantize() (public/llama2_convert.py:125-130), quantize6()/pack6()/unpack6()
 (public/llama2_numpy.py:678-702), rope_tables() (public/llama2_numpy.py:484-542, the float32 tables a caller hands the
-engine), external_tensors() (public/llama2_numpy.py:778-795, where every tensor of a checkpoint is) and the NumPy
-forward's logits on tiny int8/int6 models (public/llama2_numpy.py:1310-1383; the float reference the int8 path is held
-to within a line, tests/test_quantize.py:81-90). Inputs are seeded; outputs are stored as NumPy arrays (no pickles)
+engine), external_tensors() (public/llama2_numpy.py:778-795, where every tensor of a checkpoint is), layout() and
+tensor_bytes() of the GPT-2, GPT-NeoX and Qwen3 forms (public/llama2_convert.py:32-83,105-118), and the NumPy
+forward's logits on tiny int8/int6 models of every form (public/llama2_numpy.py:1310-1383; the float reference the
+int8 path is held to within a line, tests/test_quantize.py:81-90). Inputs are seeded; outputs are stored as NumPy arrays (no pickles)
 and JSON. The reference is read from /root/reference/public; it does not travel with the fixtures.
 
     python tests/golden/make_golden.py
@@ -28,6 +29,7 @@ import llama2_numpy  # noqa: E402
 
 sys.path.insert(0, os.path.join(REPO, "tests"))
 import oracle_lib  # noqa: E402
+from forms import FORM_TINY, form_checkpoint  # noqa: E402
 
 
 def save(name, **arrays):
@@ -82,6 +84,32 @@ def plans():
         json.dump(out, f, indent=1, sort_keys=True)
 
 
+FORMS = {
+    # name: (header, dtype, form) of the other forms (public/llama2_convert.py:32-83)
+    "gpt2_int8": ((64, 128, 2, 4, 4, 320, 32), "int8", {"arch": "gpt2"}),
+    "gpt2_int6_own_cls": ((64, 96, 2, 2, 2, -256, 32), "int6", {"arch": "gpt2"}),
+    "neox_int8": ((64, 128, 2, 4, 4, -320, 32), "int8", {"arch": "neox"}),
+    "qwen3_int8": ((64, 96, 2, 4, 2, -288, 32), "int8", {"qk_norm": True, "head_dim": 32}),
+    "qwen3_bias_int6": ((64, 96, 2, 4, 1, 288, 32), "int6", {"bias": True, "qk_norm": True}),
+}
+
+
+def layouts():
+    """llama2_convert.layout() of every form: shape, whether a matrix, and the offset and bytes tensor_bytes() gives
+    each tensor in file order (the RoPE tables of an int8 file take none)"""
+    out = {}
+    for name, (header, dtype, form) in FORMS.items():
+        offset, entries = 28, []
+        for shape, is_matrix in llama2_convert.layout(*header, **form):
+            size = llama2_convert.tensor_bytes(shape, is_matrix, dtype)
+            entries.append({"shape": list(shape), "matrix": is_matrix, "offset": offset, "bytes": int(size)})
+            offset += size
+        out[name] = {"header": list(header), "dtype": dtype, "form": form, "layout": entries,
+                     "size": int(llama2_convert.checkpoint_size(header, dtype, form))}
+    with open(os.path.join(HERE, "layouts.json"), "w") as f:
+        json.dump(out, f, indent=1, sort_keys=True)
+
+
 def tokenizer_bytes(vocab):
     """llama2.c's tokenizer.bin (tests/conftest.py:172-176): the pieces are placeholders, never decoded here."""
     pieces = [(0.0, b"<unk>"), (0.0, b"<s>"), (0.0, b"</s>")] + [(0.0, b"<p%d>" % i) for i in range(3, vocab)]
@@ -118,10 +146,26 @@ def forwards():
     save("numpy_forward.npz", **out)
 
 
+def form_forwards():
+    out = {}
+    for name, (fields, theta, keywords) in FORM_TINY.items():
+        cfg, _, ck = form_checkpoint(name)
+        dtype = "int6" if fields["six"] else "int8"
+        model = llama2_numpy.Llama(bytes(ck), tokenizer_bytes(fields["vocab_size"]), dtype=dtype, rope_theta=theta,
+                                   **keywords)
+        logits = np.stack([model.forward(tok, pos).astype(np.float32) for pos, tok in enumerate(TOKENS)])
+        out[f"logits_{name}"] = logits
+        out[f"sha256_{name}"] = np.frombuffer(hashlib.sha256(bytes(ck)).digest(), dtype=np.uint8)
+    out["tokens"] = np.array(TOKENS, dtype=np.int32)
+    save("numpy_forms.npz", **out)
+
+
 if __name__ == "__main__":
     oracle_lib.load()
     quantizers()
     ropes()
     plans()
     forwards()
+    layouts()
+    form_forwards()
     print("golden fixtures written to", HERE)

@@ -44,6 +44,9 @@ def load():
             "or_fexp": (F, [F]),
             "or_vexp": (None, [P, I32]),
             "or_swiglu": (None, [P, P, P, I32]),
+            "or_layernorm": (None, [P, P, P, P, I32]),
+            "or_gelu": (None, [P, P, P, I32]),
+            "or_add_columns": (None, [P, P, P, I32, I32]),
             "or_add": (None, [P, P, I32]),
             "or_argmax": (I32, [P, I32]),
             "or_penalize": (None, [P, P, I32, F]),
@@ -57,6 +60,7 @@ def load():
             "or_model_kv": (None, [P, I32, I32, P, P]),
             "or_model_close": (None, [P]),
             "or_generate": (I32, [P, P, I32, I32, I32, P, P]),
+            "or_abi_layout": (None, [P]),
             "or_set_threads": (None, [I32]),
             "or_get_threads": (I32, []),
         }
@@ -273,3 +277,40 @@ def sample(logits, temperature, topp, random):
     order = np.zeros(x.size, dtype=np.int32)
     return int(load().or_sample(ptr(x), x.size, float(temperature), float(topp), float(random), ptr(probs),
                                 ptr(index), ptr(order)))
+
+
+NORM_WEIGHTS = ("rms_att_weight", "rms_ffn_weight", "rms_final_weight", "q_norm", "k_norm")
+BIASES = ("bq", "bk", "bv", "ln_att_bias", "ln_ffn_bias", "ln_final_bias", "bo", "b1", "b2")
+
+
+def vector_length(cfg, name):
+    """the float32 count of a vector tensor of the checkpoint"""
+    L, dim, hidden, hs = cfg.n_layers, cfg.dim, cfg.hidden_dim, cfg.head_size
+    qdim, kvdim = cfg.n_heads * hs, cfg.n_kv_heads * hs
+    return {"rms_att_weight": L * dim, "rms_ffn_weight": L * dim, "rms_final_weight": dim, "q_norm": L * hs,
+            "k_norm": L * hs, "bq": L * qdim, "bk": L * kvdim, "bv": L * kvdim, "ln_att_bias": L * dim,
+            "ln_ffn_bias": L * dim, "ln_final_bias": dim, "bo": L * dim, "b1": L * hidden, "b2": L * dim}[name]
+
+
+def vary_vectors(cfg, tensors, ck, seed):
+    """in place: the checkpoint's norm weights 1 + 0.25 N(0, 1) and its biases 0.2 N(0, 1) (NumPy's default_rng(seed)),
+    so that a dropped or misplaced weight or bias shows in the logits"""
+    rng = np.random.default_rng(seed)
+    T = package().T
+    for name in NORM_WEIGHTS + BIASES:
+        t = tensors[T[name]]
+        if t.offset == 0:
+            continue  # not in this form
+        n = vector_length(cfg, name)
+        values = (1.0 + 0.25 * rng.standard_normal(n)) if name in NORM_WEIGHTS else 0.2 * rng.standard_normal(n)
+        ck[t.offset:t.offset + 4 * n] = np.frombuffer(values.astype(np.float32).tobytes(), dtype=np.uint8)
+    return ck
+
+
+def outlier_channels(weight, count=8, ratio=4.0):
+    """public/llama2_numpy.py:807-813: the count channels with the largest |final-norm weight|, in order, or none where
+    the largest is below ratio times the median"""
+    size = np.abs(np.asarray(weight, dtype=np.float32))
+    if size.max() < ratio * np.median(size):
+        return []
+    return sorted(int(c) for c in np.argsort(-size, kind="stable")[:count])

@@ -47,6 +47,20 @@ def test_plan_conversion_takes_the_reference_plan_and_refuses_other_forms():
     assert pk.plan_to_config(plan, half_keys=True)[0].half_kv == 1
     assert pk.plan_to_config({**plan, "n_kv_heads": 4})[0].half_kv == 1
     assert t[pk.T["wcls"]].offset == tensors["token_embedding_table"]["offset"]
-    for change in ({"arch": "gpt2"}, {"outliers": [3]}, {"int8": False}, {"parallel_residual": True}):
+    for change in ({"arch": "qwen35"}, {"int8": False}, {"rotary": 8}, {"outliers": list(range(9))}):
         with pytest.raises(pk.HipError):
             pk.plan_to_config({**plan, **change})
+    # the other forms: outliers, Qwen3's head norms, GPT-2 (its positions), GPT-NeoX (partial rotary, parallel)
+    c, _ = pk.plan_to_config({**plan, "outliers": [40, 3]})
+    assert (c.n_outliers, list(c.outliers)[:2]) == (2, [3, 40])
+    norms = {name: {"kind": "f32", "offset": 60000 + i * 100, "shape": [2, 16], "group": 0, "scales": 0}
+             for i, name in enumerate(("q_norm", "k_norm"))}
+    assert pk.plan_to_config({**plan, "tensors": {**tensors, **norms}})[0].qk_norm == 1
+    assert pk.plan_to_config({**plan, "parallel_residual": True})[0].parallel_residual == 0  # llama: not read
+    with pytest.raises(KeyError):
+        pk.plan_to_config({**plan, "arch": "gpt2"})  # a GPT-2 plan places its positions
+    gpt2 = {**tensors, "positions": dict(tensors["wq"], offset=70000, scales=70500)}
+    c, t = pk.plan_to_config({**plan, "arch": "gpt2", "tensors": gpt2, "rotary": 8})
+    assert (c.arch, c.rotary, t[pk.T["positions"]].offset) == (1, 0, 70000)
+    c, _ = pk.plan_to_config({**plan, "arch": "neox", "rotary": 8, "parallel_residual": True})
+    assert (c.arch, c.rotary, c.parallel_residual) == (2, 8, 1)

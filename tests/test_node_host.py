@@ -46,9 +46,14 @@ def test_module_exports_and_plan_conversion_match_the_python_host(tmp_path):
     tensors, _ = ol.places(cfg)
     take.append(plan_of(cfg, tensors))
     base = take[-1]
-    refuse = [{**base, "arch": "gpt2"}, {**base, "outliers": [3]}, {**base, "int8": False},
-              {**base, "parallel_residual": True}, {**base, "rotary": 8},
-              {**base, "tensors": {**base["tensors"], "q_norm": {"kind": "f32", "offset": 0}}}]
+    norms = {name: {"kind": "f32", "offset": 1000 + i, "shape": [2, 16], "group": 0, "scales": 0}
+             for i, name in enumerate(("q_norm", "k_norm"))}
+    positions = dict(base["tensors"]["wq"], offset=7000, scales=7500)
+    take += [{**base, "outliers": [40, 3, 17]}, {**base, "tensors": {**base["tensors"], **norms}},
+             {**base, "arch": "gpt2", "tensors": {**base["tensors"], "positions": positions}},
+             {**base, "arch": "neox", "rotary": 8, "parallel_residual": True}]
+    refuse = [{**base, "arch": "qwen35"}, {**base, "outliers": list(range(9))}, {**base, "int8": False},
+              {**base, "rotary": 8}]
     job = tmp_path / "plans.json"
     job.write_text(json.dumps({"take": take, "refuse": refuse}))
     out = run_node("plan_config.mjs", str(job))
@@ -59,7 +64,12 @@ def test_module_exports_and_plan_conversion_match_the_python_host(tmp_path):
         c, t = pk.plan_to_config(plan)
         for field, _ in c._fields_:
             want = getattr(c, field)
-            assert js["config"][field] == pytest.approx(want, rel=1e-7), (field, plan["dim"])
+            if field == "n_outliers":
+                assert len(js["config"]["outliers"]) == want
+            elif field == "outliers":
+                assert js["config"]["outliers"] == list(want)[:c.n_outliers]
+            else:
+                assert js["config"][field] == pytest.approx(want, rel=1e-7), (field, plan["dim"])
         assert [list(p) for p in js["tensors"]] == [[t[i].offset, t[i].scales] for i in range(len(t))]
     assert all(message for message in out["refused"]), out["refused"]
     assert out["kernels"] == [None, True]

@@ -120,9 +120,12 @@ def test_package_config_structs_match_the_header():
     """the ctypes structs of the package are the layout of include/pyodide_llm_hip.h"""
     import ctypes
     pk = package()
-    assert ctypes.sizeof(pk.HeConfig) == 14 * 4
-    assert ctypes.sizeof(pk.HeTensor) == 16
-    assert len(pk.TENSORS) == 15
+    layout = np.zeros(6, dtype=np.int64)
+    ol.load().or_abi_layout(ol.ptr(layout))
+    assert ctypes.sizeof(pk.HeConfig) == layout[0]
+    assert (pk.HeConfig.rms_norm_eps.offset, pk.HeConfig.arch.offset, pk.HeConfig.outliers.offset) == tuple(layout[1:4])
+    assert ctypes.sizeof(pk.HeTensor) == layout[4]
+    assert len(pk.TENSORS) == layout[5]
 
 
 @pytest.mark.parametrize("name", sorted(PLANS))
