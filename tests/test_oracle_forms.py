@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as ol
-from forms import FORM_TINY, form_checkpoint
+from forms import FORM_TINY, form_checkpoint, form_model
 from paths import GOLDEN_DIR, package
 
 NF = np.load(os.path.join(GOLDEN_DIR, "numpy_forms.npz"))
@@ -56,17 +56,6 @@ def test_places_follow_the_reference_layout(name, places):
 def test_checkpoint_is_the_golden_one(name):
     _, _, ck = form_checkpoint(name)
     assert np.array_equal(np.frombuffer(hashlib.sha256(ck.tobytes()).digest(), dtype=np.uint8), NF[f"sha256_{name}"])
-
-
-def form_model(name, max_block=8, outliers=True, **extra):
-    cfg, tensors, ck = form_checkpoint(name)
-    fields, theta, _ = FORM_TINY[name]
-    final = np.frombuffer(ck.tobytes(), dtype=np.float32, count=cfg.dim,
-                          offset=tensors[package().T["rms_final_weight"]].offset)
-    channels = ol.outlier_channels(final) if outliers else []
-    cfg = ol.config(**{**fields, **extra, "outliers": channels})
-    cos, sin = package().rope_tables(cfg.seq_len, cfg.head_size, theta, cfg.rotary if cfg.arch == 2 else 0)
-    return cfg, tensors, ck, cos, sin, channels
 
 
 def max_error(model):
