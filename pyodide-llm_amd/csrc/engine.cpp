@@ -173,6 +173,10 @@ struct he_engine {
   float *before = nullptr, *columns = nullptr, *picked = nullptr;
   OutlierSet outliers{};
   bool replayable = false;  // run_chunk is building the graph (positions from state, no host copies)
+  // one-token GEMVs whose first rows extra blocks of the launch before them bring into L2 (L2Fetch); sink: their
+  // 64 words
+  int64_t fetch_xcd_bytes = 3 << 20;
+  uint32_t *sink = nullptr;
   // he_profile_forward: event pairs around every launch while `profiling` is set
   struct Mark {
     int kind;
@@ -205,7 +209,7 @@ void destroy(he_engine *e) {
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
                   e->best_v, e->best_i, e->state, e->step_ids, e->step_values, e->sample_probs, e->sample_index,
-                  e->window, e->sample_token, e->sample_best, e->before, e->columns, e->picked};
+                  e->window, e->sample_token, e->sample_best, e->before, e->columns, e->picked, e->sink};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   void *pinned[] = {e->host_ids, e->host_state, e->host_values, e->host_window};
@@ -358,6 +362,12 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->window, sizeof(int32_t) * REPETITION_WINDOW);
   ALLOC(e->sample_token, sizeof(int32_t) * 4);
   ALLOC(e->sample_best, sizeof(float) * 4);
+  ALLOC(e->sink, sizeof(uint32_t) * 64);
+  {
+    // PYODIDE_LLM_HIP_L2FETCH: KiB an XCD of the L2 fills ahead of the one-token GEMVs (0: none)
+    const char *env = std::getenv("PYODIDE_LLM_HIP_L2FETCH");
+    if (env && *env) e->fetch_xcd_bytes = std::max(0L, std::atol(env)) << 10;
+  }
   if (c.parallel_residual) ALLOC(e->before, sizeof(float) * T * c.dim);
   e->outliers.n = c.n_outliers;
   for (int32_t i = 0; i < c.n_outliers; ++i) e->outliers.c[i] = c.outliers[i];
@@ -511,6 +521,39 @@ bool quantizes_itself(const he_engine *e, int32_t k, int32_t m, int32_t rows) {
   return m == 1 && rows <= 8192 && decode_takes_f32(k, e->c.six != 0, e->c.relaxed != 0);
 }
 
+// The L2Fetch of a one-token GEMV over segs (rows of k): the rows of its first blocks, at most fetch_xcd_bytes an XCD
+// (of its 4 MiB L2), fetched by `blocks` extra blocks of the launch before it. None (blocks = 0) for more tokens, where
+// the GEMV is not the one-token path, or where a segment's rows are not whole GEMV blocks.
+L2Fetch fetch_for(const he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, int32_t blocks,
+                  bool qkv_on = false) {
+  L2Fetch f{};
+  if (e->fetch_xcd_bytes <= 0 || m != 1 || blocks < 8 || blocks % 8) return f;
+  int32_t total = 0;
+  for (int i = 0; i < nseg; ++i) total += segs[i].rows;
+  const int32_t br = decode_block_rows(k, total, e->c.six != 0, e->c.relaxed != 0, false, qkv_on);
+  if (br <= 0) return f;
+  const int32_t row_bytes = e->c.six ? k / 32 * 24 : k, scale_bytes = k / 32 * 4;
+  for (int i = 0; i < nseg; ++i) {
+    // whole GEMV blocks a segment, and every block's values and scales on 16-byte boundaries
+    if (segs[i].rows % br || (br * row_bytes) % 16 || (br * scale_bytes) % 16 ||
+        reinterpret_cast<uintptr_t>(segs[i].w) % 16 || reinterpret_cast<uintptr_t>(segs[i].ws) % 16)
+      return L2Fetch{};
+    f.w[i] = segs[i].w;
+    f.ws[i] = reinterpret_cast<const uint8_t *>(segs[i].ws);
+    f.rows[i] = segs[i].rows;
+  }
+  f.nseg = nseg;
+  f.row_bytes = row_bytes;
+  f.scale_bytes = scale_bytes;
+  f.block_rows = br;
+  const int64_t per_block = (int64_t)br * (f.row_bytes + f.scale_bytes);
+  f.gemv_blocks = (int32_t)std::min<int64_t>(total / br, 8 * (e->fetch_xcd_bytes / per_block));
+  if (f.gemv_blocks < 1) return L2Fetch{};
+  f.blocks = blocks;
+  f.sink = e->sink;
+  return f;
+}
+
 int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, bool need_logits) {
   const he_config &c = e->c;
   hipStream_t s = e->stream;
@@ -561,13 +604,17 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
                                       e->vec(HE_T_RMS_ATT, (int64_t)l * dim), e->vec(HE_T_LN_ATT_BIAS, (int64_t)l * dim),
                                       m, dim, dim, W, W / 32, 0, e->bias, s);
       }));
-    } else {
+    }
+    const bool fuse_qkv = c.arch == HE_ARCH_LLAMA && !c.qk_norm && m == 1 &&
+                          decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0);
+    if (!ln) {
+      const L2Fetch fq = fetch_for(e, qkv, 3, dim, m, 256, fuse_qkv);
       HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
         return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
-                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s);
+                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s, &fq);
       }));
     }
-    if (c.arch == HE_ARCH_LLAMA && !c.qk_norm && m == 1 && decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0)) {
+    if (fuse_qkv) {
       // one token: the q/k/v GEMV adds the biases, rotates q and k and writes k and v into the cache itself
       const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv,
                          qp.vstride, dpos};
@@ -613,9 +660,9 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     if (!quantized) at.xq = nullptr;
     double kv_rows = 0;
     for (int32_t t = 0; t < m; ++t) kv_rows += pos0 + t + 1;
+    const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
     HIP_TRY(timed(e, HE_K_ATTENTION, kv_rows * 2 * kvdim * esz + (double)m * qdim * 8,
                   [&] { return launch_attention(at, s); }));
-    const MatSeg wo[1] = {{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), e->x, dim, dim, 1}};
     if (quantized) {
       HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
     } else if (quantizes_itself(e, qdim, m, dim)) {
@@ -647,17 +694,18 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
                     [&] { return launch_add_rows(e->x, e->vec(HE_T_B2, (int64_t)l * dim), m, dim, dim, s); }));
       continue;
     }
-    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
-                                  W / 32, 0, c.rms_norm_eps, e->bias, s);
-    }));
     const MatSeg w13[2] = {{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), e->hb, hidden, hidden, 0},
                            {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), e->hb2, hidden, hidden, 0}};
+    const L2Fetch f13 = fetch_for(e, w13, 2, dim, m, 256);
+    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
+                                  W / 32, 0, c.rms_norm_eps, e->bias, s, &f13);
+    }));
     HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs));
+    const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
     HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * hidden * (8 + 1 + 0.125), [&] {
       return launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s);
     }));
-    const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
     HIP_TRY(matmul(e, w2, 1, hidden, m, e->xq, e->xs));
   }
   if (need_logits) {
@@ -665,12 +713,14 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     // quantized again (public/forward.js:1082-1089)
     const bool apart = c.n_outliers > 0;
     const float *last = e->x + (int64_t)(m - 1) * dim;
+    const MatSeg cls[1] = {{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), e->logits, c.vocab_size, 0, 0}};
+    const L2Fetch fc = fetch_for(e, cls, 1, dim, 1, apart ? 0 : 256);
     HIP_TRY(timed(e, HE_K_NORM, (double)dim * (8 + 1 + 0.125), [&] {
       return ln ? launch_layernorm_quant(e->xq, e->xs, apart ? e->xb : nullptr, nullptr, last,
                                          e->vec(HE_T_RMS_FINAL, 0), e->vec(HE_T_LN_FINAL_BIAS, 0), 1, dim, dim, W,
                                          W / 32, e->xw, e->bias, s)
                 : launch_rmsnorm_quant(e->xq, e->xs, apart ? e->xb : nullptr, last, e->vec(HE_T_RMS_FINAL, 0), 1,
-                                       dim, dim, W, W / 32, e->xw, c.rms_norm_eps, e->bias, s);
+                                       dim, dim, W, W / 32, e->xw, c.rms_norm_eps, e->bias, s, &fc);
     }));
     if (apart) {
       HIP_TRY(timed(e, HE_K_ELEMENTWISE, 64.0, [&] { return launch_pick(e->xb, e->picked, e->outliers, s); }));
@@ -678,7 +728,6 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
         return launch_quantize(e->xq, e->xs, e->xb, 1, dim, e->xw, W, W / 32, e->bias, s);
       }));
     }
-    const MatSeg cls[1] = {{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), e->logits, c.vocab_size, 0, 0}};
     HIP_TRY(matmul(e, cls, 1, dim, 1, e->xq, e->xs));
     if (apart)
       HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)c.vocab_size * (8 + 4 * c.n_outliers), [&] {

@@ -648,6 +648,25 @@ bool decode_fuses_qkv(int32_t k, bool six, bool relaxed) {
   return six ? (k / GS) % 2 == 0 && k <= 256 * GS : k <= 8 * 1024;
 }
 
+int32_t decode_block_rows(int32_t k, int32_t total_rows, bool six, bool relaxed, bool xf, bool qkv_on) {
+  // launch_decode's and launch_decode6's choices of rows a wave (launch_gemv's one-token paths)
+  if (!relaxed) return 0;
+  if (!six) {
+    if (k > 20 * 1024) return 0;
+    const int steps = (k / GS + 31) / 32;
+    if (steps <= 2) return 4 * WAVES;
+    if (steps <= 4) return (xf ? 4 : (total_rows > 4096 || qkv_on ? 2 : 1)) * WAVES;
+    if (steps <= 8) return 2 * WAVES;
+    return WAVES;
+  }
+  if (k > 24 * 1024 || (k / GS) % 2) return 0;
+  const int steps = (k / GS + 127) / 128;
+  if (steps <= 1) return 4 * WAVES;
+  if (steps <= 2) return 2 * WAVES;
+  if (steps <= 6) return WAVES;
+  return 0;
+}
+
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   const bool sums = a.sums != nullptr;
   if (a.xf && (sums || a.m != 1 || !decode_takes_f32(a.k, six, relaxed))) return hipErrorInvalidValue;

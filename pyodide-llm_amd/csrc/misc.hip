@@ -7,6 +7,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "l2fetch.hpp"
 
 namespace ple {
 
@@ -28,7 +29,13 @@ __global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, co
 __global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *xs, float *out, const float *x,
                                                             const float *w, int32_t n, int32_t x_stride,
                                                             int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
-                                                            float eps, int32_t bias) {
+                                                            float eps, int32_t bias, const L2Fetch f) {
+  // the last f.blocks rows of blocks (one token) fill the next GEMV's L2 lines instead
+  const int split = gridDim.y - f.blocks;
+  if ((int)blockIdx.y >= split) {
+    l2_fetch(f, blockIdx.y - split, blockIdx.y);
+    return;
+  }
   extern __shared__ float sm[];
   const int n4 = n & ~3, q4 = n4 >> 2, qs = chain_rowstride(q4);
   float *xv = sm;            // n
@@ -82,7 +89,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *
   float *sc = xs + (int64_t)t * xs_stride;
   // this block's share of the groups: gridDim.y blocks of a token each run the (short) sums themselves and quantize
   // every gridDim.y-th group, so that no one CU does all the divisions
-  for (int g = (tid >> 5) * gridDim.y + blockIdx.y; g < n / GS; g += 32 * gridDim.y) {
+  for (int g = (tid >> 5) * split + blockIdx.y; g < n / GS; g += 32 * split) {
     const int j = g * GS + (tid & 31);
     const float o = wv[j] * (s * xv[j]);
     if (out) out[(int64_t)t * out_stride + j] = o;
@@ -310,12 +317,13 @@ hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int
 
 hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
-                                float eps, int32_t bias, hipStream_t s) {
+                                float eps, int32_t bias, hipStream_t s, const L2Fetch *fetch) {
   const size_t lds = sizeof(float) * (size_t)(2 * n + 4 * chain_rowstride((n & ~3) >> 2) + 16);
   // one token: 4 blocks share its groups (more tokens fill the chip by themselves)
   const int split = m < 64 ? 4 : 1;
-  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m, split), dim3(1024), lds, s, xq, xs, out, x, w, n, x_stride,
-                     xq_stride, xs_stride, out_stride, eps, bias);
+  const L2Fetch f = fetch && m == 1 ? *fetch : L2Fetch{};
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(m, split + f.blocks), dim3(1024), lds, s, xq, xs, out, x, w, n,
+                     x_stride, xq_stride, xs_stride, out_stride, eps, bias, f);
   return hipGetLastError();
 }
 

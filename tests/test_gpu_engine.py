@@ -100,6 +100,29 @@ def test_greedy_generation_matches_the_oracle():
     assert same_bits(eng.logits(), want_logits)
 
 
+@pytest.mark.parametrize("fill_kib", ["0", "16", "3072"])
+def test_l2_fills_change_no_bits(fill_kib, monkeypatch):
+    """the rmsnorm launches' L2 fills ahead of the q/k/v, w1/w3 and classifier GEMVs only read: none, a part of the
+    first GEMV blocks (16 KiB an XCD) or all of them give the oracle's tokens and logits, replayed steps included"""
+    monkeypatch.setenv("PYODIDE_LLM_HIP_L2FETCH", fill_kib)
+    cfg, tensors, ck, cos, sin, _ = build("stories15m", half_kv=1)
+    rng = np.random.default_rng(3)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=8)]
+    steps = 8 + 24
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    want, want_logits = ref.generate(prompt, steps)
+    eng = package().open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    eng.forwardMany([1] + prompt[:-1], 0)
+    got, token, pos = [], prompt[-1], len(prompt)
+    while pos < steps:
+        ids = eng.generateMany(token, pos, [], 0, min(16, steps - pos), 0.0, 0.9, 1.0, [], [])
+        got += ids
+        token, pos = ids[-1], pos + len(ids)
+    assert got == [int(t) for t in want]
+    assert same_bits(eng.logits(), want_logits)
+    eng.release()
+
+
 @pytest.mark.parametrize("half_kv", [0, 1])
 def test_long_context_crosses_attention_chunks(half_kv):
     """positions past 512 and 1024 (the value kernel's chunks) and every count % 4, against the oracle to the bit"""
