@@ -34,6 +34,22 @@ struct QkvFuse {
   const int32_t *dpos;  // the position in device memory (a replayed decode step), or null: pos
 };
 
+// An L2 fill ahead of a one-token GEMV, run by extra blocks of the rmsnorm launch before it, which leaves most CUs and
+// the HBM idle. A launch's block b runs on XCD b % 8 (the 8 XCDs take blocks in
+// turn, every launch from XCD 0), and each XCD has its own 4 MiB L2 that keeps its lines across launches: so the
+// extra block whose launch-wide index is L touches every 64-byte line of the rows (values and scales) of the GEMV's
+// blocks b = L (mod 8), and the GEMV's block b finds them in its own XCD's L2. Only reads; the results never change.
+struct L2Fetch {
+  const uint8_t *w[3];   // each segment's values [rows][row_bytes]
+  const uint8_t *ws[3];  // and scales [rows][scale_bytes]
+  int32_t rows[3];       // each a multiple of block_rows
+  int32_t nseg;
+  int32_t row_bytes, scale_bytes;
+  int32_t block_rows;   // rows a GEMV block takes
+  int32_t gemv_blocks;  // the GEMV blocks fetched: the first ones (those of its first round on the CUs)
+  int32_t blocks;       // the extra blocks (a multiple of 8; 0: none)
+  uint32_t *sink;       // 64 words, written only where the touched words' xor hits a constant (keeps the loads)
+};
 struct MatArgs {
   MatSeg seg[3];
   int32_t nseg;
@@ -53,22 +69,6 @@ struct MatArgs {
   QkvFuse qkv;  // decode_fuses_qkv()
 };
 
-// An L2 fill ahead of a one-token GEMV, run by extra blocks of the rmsnorm launch before it, which leaves most CUs and
-// the HBM idle. A launch's block b runs on XCD b % 8 (the 8 XCDs take blocks in
-// turn, every launch from XCD 0), and each XCD has its own 4 MiB L2 that keeps its lines across launches: so the
-// extra block whose launch-wide index is L touches every 64-byte line of the rows (values and scales) of the GEMV's
-// blocks b = L (mod 8), and the GEMV's block b finds them in its own XCD's L2. Only reads; the results never change.
-struct L2Fetch {
-  const uint8_t *w[3];   // each segment's values [rows][row_bytes]
-  const uint8_t *ws[3];  // and scales [rows][scale_bytes]
-  int32_t rows[3];       // each a multiple of block_rows
-  int32_t nseg;
-  int32_t row_bytes, scale_bytes;
-  int32_t block_rows;   // rows a GEMV block takes
-  int32_t gemv_blocks;  // the GEMV blocks fetched: the first ones (those of its first round on the CUs)
-  int32_t blocks;       // the extra blocks (a multiple of 8; 0: none)
-  uint32_t *sink;       // 64 words, written only where the touched words' xor hits a constant (keeps the loads)
-};
 // rows a block of the one-token decode GEMV takes (launch_gemv with m = 1, bias 64, no sums) for rows of k, 0 where
 // the launch goes another way
 int32_t decode_block_rows(int32_t k, int32_t total_rows, bool six, bool relaxed, bool xf, bool qkv_on);

@@ -12,7 +12,7 @@ namespace ple {
 // block_rows), so its values and its scales are two contiguous ranges, both whole 16-byte pieces on 16-byte
 // boundaries (checked by the host). Each thread reads 16-byte pieces, 8 in flight, their indices clamped into the
 // block's pieces (every load unconditional and in bounds).
-__device__ __forceinline__ void l2_fetch(const L2Fetch &f, int j, int linear) {
+__device__ __forceinline__ void l2_fetch(const L2Fetch f, int j, int linear) {
   const int nt = blockDim.x;
   const int xcd = linear & 7, q = j >> 3, Q = f.blocks >> 3;
   const int first = xcd + 8 * q;
@@ -28,10 +28,21 @@ __device__ __forceinline__ void l2_fetch(const L2Fetch &f, int j, int linear) {
       const int64_t idx = min(base + (int64_t)u * nt, total - 1);
       const int i = (int)(idx / per), l = (int)(idx % per);
       const int b = first + 8 * Q * i;
-      int r = b * f.block_rows, s = 0;
-      while (s + 1 < f.nseg && r >= f.rows[s]) r -= f.rows[s++];
-      const uint8_t *p = l < cv ? f.w[s] + (int64_t)r * f.row_bytes + ((int64_t)l << 4)
-                                : f.ws[s] + (int64_t)r * f.scale_bytes + ((int64_t)(l - cv) << 4);
+      // the block's segment by selects (a segment index into the arrays would put the struct in scratch memory)
+      int r = b * f.block_rows;
+      const uint8_t *w = f.w[0], *ws = f.ws[0];
+      if (f.nseg > 1 && r >= f.rows[0]) {
+        r -= f.rows[0];
+        w = f.w[1];
+        ws = f.ws[1];
+        if (f.nseg > 2 && r >= f.rows[1]) {
+          r -= f.rows[1];
+          w = f.w[2];
+          ws = f.ws[2];
+        }
+      }
+      const uint8_t *p = l < cv ? w + (int64_t)r * f.row_bytes + ((int64_t)l << 4)
+                                : ws + (int64_t)r * f.scale_bytes + ((int64_t)(l - cv) << 4);
       v[u] = *reinterpret_cast<const uint4 *>(p);
     }
 #pragma unroll

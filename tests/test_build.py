@@ -1,0 +1,54 @@
+"""The built library's gfx950 code objects: every kernel without scratch (private) memory. A kernel that indexes an
+argument struct's array at run time, or spills, gets a private segment; the decode kernels are written so that none
+does (a struct in scratch made the GEMVs three times slower). Runs on the CPU over the library build() made."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from paths import package
+
+LLVM = "/opt/rocm/llvm/bin"
+MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+
+def code_objects(tmp_path):
+    lib = package().hip_engine.LIBRARY
+    fat = tmp_path / "fatbin.bin"
+    # the section copied out into a file of its own (objcopy given no output file would rewrite the library in place)
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", lib, str(fat)], check=True)
+    data = fat.read_bytes()
+    starts = [m.start() for m in re.finditer(re.escape(MAGIC), data)]
+    assert starts, "no offload bundle in the library"
+    out = []
+    for i, at in enumerate(starts):
+        piece = tmp_path / f"bundle{i}.bin"
+        piece.write_bytes(data[at:starts[i + 1] if i + 1 < len(starts) else len(data)])
+        co = tmp_path / f"dev{i}.co"
+        subprocess.run([f"{LLVM}/clang-offload-bundler", "--type=o", "--unbundle", f"--input={piece}",
+                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True)
+        out.append(co)
+    return out
+
+
+@pytest.mark.skipif(not (os.path.exists(f"{LLVM}/clang-offload-bundler") and shutil.which("objcopy")),
+                    reason="ROCm's clang-offload-bundler or objcopy missing")
+def test_no_kernel_uses_scratch(tmp_path):
+    kernels, scratch = 0, []
+    for co in code_objects(tmp_path):
+        notes = subprocess.run([f"{LLVM}/llvm-readelf", "--notes", str(co)], check=True, stdout=subprocess.PIPE,
+                               text=True).stdout
+        name = None
+        for line in notes.splitlines():
+            m = re.match(r"\s+\.name:\s+(\S+)", line)
+            if m:
+                name = m.group(1)
+            m = re.match(r"\s+\.private_segment_fixed_size:\s+(\d+)", line)
+            if m:
+                kernels += 1
+                if int(m.group(1)):
+                    scratch.append((name, int(m.group(1))))
+    assert kernels > 100
+    assert not scratch, scratch
