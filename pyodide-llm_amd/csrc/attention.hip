@@ -410,11 +410,15 @@ __global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a
     }
 #pragma unroll
     for (int u = 0; u < ASV; ++u) {
-      const int i = base + tid + NT * u;
-      if (i < count) {
-        const float d = sv[u] - mx;
-        if (i < count4) e4[(i & 3) * rs + (i >> 2)] = vexp(d);
-        else tail[i - count4] = fexp(d);
+      // the block's test first (the same for every thread: a scalar branch), so that no wave runs the exponentials
+      // of positions past the count with its lanes switched off
+      if (base + NT * u < count) {
+        const int i = base + tid + NT * u;
+        if (i < count) {
+          const float d = sv[u] - mx;
+          if (i < count4) e4[(i & 3) * rs + (i >> 2)] = vexp(d);
+          else tail[i - count4] = fexp(d);
+        }
       }
     }
   }
@@ -450,26 +454,56 @@ __global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a
       if (it + 2 * NP < items) ATT_FETCH(it + 2 * NP, vn);  // in flight while the wave waits
     }
   } else {
-    float acc = 0.0f;  // lane j < AC: column j0 + j
-    for (int c = 0; c < chunks; ++c) {
+    // lane j < AC: column j0 + j (lanes past AC repeat column AC - 1 and store nothing). Chunks in pairs, two
+    // register sets: chunk c + 1 is requested (after its flags) before chunk c's adds, which hide its latency. The
+    // slot of c + 1 is free once c - 1 is released, so waiting for c + 1 before releasing c needs nslot >= 2.
+    float acc = 0.0f;
+    const int lr = min(lane, AC - 1);
+    float4 xa[RB / 4], xb[RB / 4];
+    auto ready = [&](int c) {  // every half of chunk c filled: the flags requested together, then one wait
+      const int *f = filled[c % nslot];
+      for (;;) {
+        int least = lds_load(f);
 #pragma unroll
-      for (int hh = 0; hh < H; ++hh) wait_at_least(&filled[c % nslot][hh], c + 1);
-      if (lane < AC) {
-        const int nb = min(RP, count4 - c * RP) >> 2;
-        const float *row = ring + (c % nslot) * (AC * RR) + lane * RR;
-        if (nb == RB) {  // a whole chunk: its 16 reads requested together (the scheduling barrier keeps them so)
-          float4 x[RB / 4];
+        for (int hh = 1; hh < H; ++hh) least = min(least, lds_load(f + hh));
+        if (least >= c + 1) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
+    auto fetch = [&](int c, float4 (&x)[RB / 4]) {
+      const float4 *row = reinterpret_cast<const float4 *>(ring + (c % nslot) * (AC * RR) + lr * RR);
 #pragma unroll
-          for (int u = 0; u < RB / 4; ++u) x[u] = reinterpret_cast<const float4 *>(row)[u];
-          __builtin_amdgcn_sched_barrier(0);
-          acc = add32(acc, x);
-          acc = add32(acc, x + 8);
-        } else {
-          acc = lds_chain(row, nb, acc);
-        }
+      for (int u = 0; u < RB / 4; ++u) x[u] = row[u];
+    };
+    auto consume = [&](int c, const float4 (&x)[RB / 4]) {
+      const int nb = min(RP, count4 - c * RP) >> 2;
+      if (nb == RB) {
+        acc = add32(acc, x);
+        acc = add32(acc, x + 8);
+      } else {  // the last chunk, part full: from LDS
+        acc = lds_chain(ring + (c % nslot) * (AC * RR) + lr * RR, nb, acc);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0) lds_store(&used, c + 1);
+    };
+    if (chunks > 0) {
+      ready(0);
+      fetch(0, xa);
+    }
+    for (int c = 0; c < chunks; c += 2) {
+      if (c + 1 < chunks) {
+        ready(c + 1);
+        fetch(c + 1, xb);
+      }
+      consume(c, xa);
+      if (c + 1 < chunks) {
+        if (c + 2 < chunks) {
+          ready(c + 2);
+          fetch(c + 2, xa);
+        }
+        consume(c + 1, xb);
+      }
     }
 #pragma unroll
     for (int r = 0; r < 3; ++r)
