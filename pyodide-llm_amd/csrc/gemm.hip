@@ -127,6 +127,14 @@ __device__ __forceinline__ void products(const v16i &S, const float *ws_rows, fl
   }
 }
 
+// the 16 values live in registers here: an empty asm that takes and gives them keeps the compiler from moving their
+// computation below this point (asm volatile statements keep their order; the last one's memory clobber keeps the
+// stores that follow below it)
+__device__ __forceinline__ void pin16(float (&x)[16]) {
+  asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]),
+               "+v"(x[8]), "+v"(x[9]), "+v"(x[10]), "+v"(x[11]), "+v"(x[12]), "+v"(x[13]), "+v"(x[14]), "+v"(x[15]));
+}
+
 // the 16 group sums of a lane's tile outputs (rows row0 + (v / 4) * 8 + (lane / 32) * 4 + v % 4, token tok0 + lane % 32)
 __device__ __forceinline__ void write_sums(const MatArgs &a, const v16i &S, int row0, int tok0, int g, int G, int lane) {
   const int t = tok0 + (lane & 31);
@@ -170,7 +178,10 @@ __global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
   __syncthreads();
   for (int s = 0; s < steps; ++s) {
     const Stage &st = stage[s & 1];
-    if (s + 1 < total) fetch<SIX, SUMS>(f, a, r0, t0, (s + 1) * KS, G, tid);
+    // the next stage fetched and stored unconditionally (no branch that would let the compiler move the products
+    // below the stores): its groups are clamped into the row, and past the last stage what it stores goes to the
+    // buffer no later read takes (the tail's stage is a real one: total > steps)
+    fetch<SIX, SUMS>(f, a, r0, t0, (s + 1) * KS, G, tid);
 #pragma unroll
     for (int gi = 0; gi < KS; ++gi) {
       const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
@@ -185,7 +196,15 @@ __global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
         for (int v = 0; v < 16; ++v) acc[gi][v] = acc[gi][v] + p[v];
       }
     }
-    if (s + 1 < total) store<SIX>(stage[(s + 1) & 1], f, tid);
+    // the next stage's stores wait for its global loads: kept after the products (the compiler would move them,
+    // and their waits, above the float32 work that hides the loads' latency)
+    if constexpr (!SUMS) {
+#pragma unroll
+      for (int c = 0; c < KS; ++c) pin16(acc[c]);
+      asm volatile("" ::: "memory");
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store<SIX>(stage[(s + 1) & 1], f, tid);
     __syncthreads();
   }
 
