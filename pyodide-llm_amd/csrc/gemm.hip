@@ -182,16 +182,23 @@ __global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
     // below the stores): its groups are clamped into the row, and past the last stage what it stores goes to the
     // buffer no later read takes (the tail's stage is a real one: total > steps)
     fetch<SIX, SUMS>(f, a, r0, t0, (s + 1) * KS, G, tid);
+    // the step's four MFMAs issued together, then the float32 work: each group's products start as its MFMA ends
+    // while the later ones still run
+    v16i S[KS];
 #pragma unroll
     for (int gi = 0; gi < KS; ++gi) {
       const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
       const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
-      const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+      S[gi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int gi = 0; gi < KS; ++gi) {
       if constexpr (SUMS) {
-        write_sums(a, S, r0 + wr * 32, t0 + wt * 32, s * KS + gi, G, lane);
+        write_sums(a, S[gi], r0 + wr * 32, t0 + wt * 32, s * KS + gi, G, lane);
       } else {
         float p[16];
-        products(S, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
+        products(S[gi], st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[gi][v] = acc[gi][v] + p[v];
       }
