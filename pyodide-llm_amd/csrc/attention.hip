@@ -232,29 +232,35 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
 }
 
 // (C) for many tokens (a prompt block): one block of 256 threads a (kv head, 32 of its columns (16 where hs is not a
-// multiple of 32), 256 / (columns * mul) tokens), a thread a (token, head, column) whose ordered sum over the
-// four-position blocks it runs itself: out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) from LDS, where 128-position
-// chunks of the values (a column's positions side by side, as the cache holds them) and of the weights are staged, the next
-// chunk's loads in flight meanwhile. The block's tokens share every value they read; each stops at its own last four.
+// multiple of 32), 2 * 256 / (columns * mul) tokens), a thread two (token, head, column) ordered sums over the
+// four-position blocks, run side by side (tokens tt and tt + 256 / (columns * mul) of the block, one value read for
+// both): out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) from LDS, where 128-position chunks of the values (a column's
+// positions side by side, as the cache holds them) and of the weights are staged, the next chunk's loads in flight
+// meanwhile. The block's tokens share every value they read; each stops at its own last four.
 constexpr int TPC = 128;  // positions a chunk
 
 template <int HS, bool HALF>
 __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
   constexpr int COLS = HS % 32 == 0 ? 32 : 16;   // columns a block
-  constexpr int ROWS = 256 / COLS;               // (token, head) weight rows a block at most
+  constexpr int TROWS = 256 / COLS;              // (token, head) rows of one pass over the block's threads
+  constexpr int ROWS = 2 * TROWS;                // weight rows a block at most: a thread runs two rows' sums
   constexpr int TVS = TPC + 4;                   // LDS row of a column's values (16 lanes' float4 on distinct banks)
   constexpr int VPT = TPC * (COLS / 4) / 256;    // float4 of values a thread a chunk
   constexpr int WPT = ROWS * (TPC / 4) / 256;    // float4 of weights a thread a chunk
   __shared__ float vs[2][COLS * TVS];  // [column][position]
   __shared__ float ps[2][ROWS * TPC];  // [token * mul + head][position]
   const int tid = threadIdx.x, kh = blockIdx.y;
-  const int mul = a.nh / a.nkv, tt_n = max(1, ROWS / mul);
-  const int j0 = blockIdx.x * COLS, t0 = blockIdx.z * tt_n;
+  const int mul = a.nh / a.nkv, tt_n = max(1, TROWS / mul);  // tokens of one pass; the block takes two passes' worth
+  const int j0 = blockIdx.x * COLS, t0 = blockIdx.z * 2 * tt_n;
   const int j = tid % COLS, hl = (tid / COLS) % mul, tt = tid / (COLS * mul);
-  const bool chain = tt < tt_n && t0 + tt < a.m;
-  const int t = min(t0 + tt, a.m - 1);
-  const int pos0 = first_position(a), count = pos0 + t + 1, count4 = count & ~3;
-  const int last = min(t0 + tt_n, a.m) - 1;  // the block's last token reads the most positions
+  // the thread's two sums, tokens t0 + tt and t0 + tt + tt_n of the same head and column: two independent chains,
+  // every value read serves both
+  const bool in = tt < tt_n;
+  const bool chain0 = in && t0 + tt < a.m, chain1 = in && t0 + tt + tt_n < a.m;
+  const int ta = min(t0 + tt, a.m - 1), tb = min(t0 + tt + tt_n, a.m - 1);
+  const int pos0 = first_position(a);
+  const int count_a = pos0 + ta + 1, count4_a = count_a & ~3, count_b = pos0 + tb + 1, count4_b = count_b & ~3;
+  const int last = min(t0 + 2 * tt_n, a.m) - 1;  // the block's last token reads the most positions
   const int most4 = (pos0 + last + 1) & ~3;
   const int chunks = (most4 + TPC - 1) / TPC;
   const int rows = (last - t0 + 1) * mul;  // weight rows of the block
@@ -289,26 +295,48 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
     PVT_STAGE(0);
   }
   __syncthreads();
-  float acc = 0.0f;
+  float acc0 = 0.0f, acc1 = 0.0f;
   for (int c = 0; c < chunks; ++c) {
     PVT_FETCH(c + 1);  // the next chunk's loads fly while this one is added (after the last: clamped, unused)
     const float *vc = vs[c & 1] + j * TVS;
-    const float *prow = ps[c & 1] + (tt * mul + hl) * TPC;
-    const int nb = chain ? max(0, min(TPC, count4 - c * TPC)) >> 2 : 0;
-    for (int b = 0; b < nb; ++b) {
-      const float4 pw = *reinterpret_cast<const float4 *>(prow + 4 * b);
+    const float *pa = ps[c & 1] + (tt * mul + hl) * TPC;
+    const float *pb = ps[c & 1] + ((tt + tt_n) * mul + hl) * TPC;
+    const int na = chain0 ? max(0, min(TPC, count4_a - c * TPC)) >> 2 : 0;
+    const int nb = chain1 ? max(0, min(TPC, count4_b - c * TPC)) >> 2 : 0;
+    const int both = min(na, nb);
+    int b = 0;
+    for (; b < both; ++b) {
       const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * b);
-      acc = acc + ((pw.x * vv.x + pw.y * vv.y) + (pw.z * vv.z + pw.w * vv.w));
+      const float4 wa = *reinterpret_cast<const float4 *>(pa + 4 * b);
+      const float4 wb = *reinterpret_cast<const float4 *>(pb + 4 * b);
+      acc0 = acc0 + ((wa.x * vv.x + wa.y * vv.y) + (wa.z * vv.z + wa.w * vv.w));
+      acc1 = acc1 + ((wb.x * vv.x + wb.y * vv.y) + (wb.z * vv.z + wb.w * vv.w));
+    }
+    for (int e = b; e < na; ++e) {  // the earlier token's own positions (only where the later one has no sum)
+      const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * e);
+      const float4 wa = *reinterpret_cast<const float4 *>(pa + 4 * e);
+      acc0 = acc0 + ((wa.x * vv.x + wa.y * vv.y) + (wa.z * vv.z + wa.w * vv.w));
+    }
+    for (int e = b; e < nb; ++e) {  // the later token's positions past the earlier one's
+      const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * e);
+      const float4 wb = *reinterpret_cast<const float4 *>(pb + 4 * e);
+      acc1 = acc1 + ((wb.x * vv.x + wb.y * vv.y) + (wb.z * vv.z + wb.w * vv.w));
     }
     PVT_STAGE((c + 1) & 1);  // the other buffer: its last readers passed the previous barrier
     __syncthreads();
   }
 #undef PVT_FETCH
 #undef PVT_STAGE
-  if (chain) {
-    const float *pt = a.scores + ((int64_t)t * a.nh + kh * mul + hl) * a.seq_len;
-    for (int p = count4; p < count; ++p) acc = acc + pt[p] * cache1<HALF>(a.vcache, (int64_t)(kh * HS + j0 + j) * a.vstride + p);
-    a.out[(int64_t)t * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc;
+  const int64_t vcol = (int64_t)(kh * HS + j0 + j) * a.vstride;
+  if (chain0) {
+    const float *pt = a.scores + ((int64_t)ta * a.nh + kh * mul + hl) * a.seq_len;
+    for (int p = count4_a; p < count_a; ++p) acc0 = acc0 + pt[p] * cache1<HALF>(a.vcache, vcol + p);
+    a.out[(int64_t)ta * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc0;
+  }
+  if (chain1) {
+    const float *pt = a.scores + ((int64_t)tb * a.nh + kh * mul + hl) * a.seq_len;
+    for (int p = count4_b; p < count_b; ++p) acc1 = acc1 + pt[p] * cache1<HALF>(a.vcache, vcol + p);
+    a.out[(int64_t)tb * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc1;
   }
 }
 
@@ -562,7 +590,7 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const size_t lds_b = sizeof(float) * (size_t)(4 * chain_rowstride(most4 / 4) + 4);
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
   constexpr int COLS = HS % 32 == 0 ? 32 : 16;
-  const int tt = std::max(1, 256 / COLS / (a.nh / a.nkv));
+  const int tt = 2 * std::max(1, 256 / COLS / (a.nh / a.nkv));  // tokens a block: two sums a thread
   hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / COLS, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   return hipGetLastError();
 }
