@@ -207,11 +207,13 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int i = base + tid + 256 * u;
-      if (i < count) {
-        const float d = sv[u] - mx;
-        if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
-        else tail[i - count4] = fexp(d);
+      if (base + 256 * u < count) {  // the block's test first (a scalar branch): no exponentials past the count
+        const int i = base + tid + 256 * u;
+        if (i < count) {
+          const float d = sv[u] - mx;
+          if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
+          else tail[i - count4] = fexp(d);
+        }
       }
     }
   }
