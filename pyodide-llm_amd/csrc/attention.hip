@@ -101,26 +101,28 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   }
 }
 
-// (A) for many tokens (a prompt block): one block a (64-position tile, kv head, 32 / mul tokens): the tile's keys
-// staged once in LDS for every (token, head) row of the block, 32 rows; wave w takes rows w, w + 4, ..., a lane one
-// position, and runs the 8 rows' four lane sums side by side over the head (the keys read once for the 8). The
-// rows' tile maxima by wave reductions.
-constexpr int SROWS = 32;  // (token, head) rows a block
+// (A) for many tokens (a prompt block): one block a (64-position tile, kv head, SR / mul tokens): the tile's keys
+// staged once in LDS for every (token, head) row of the block, SR rows (64; 32 for head size 256). A lane takes two
+// positions (2 pl, 2 pl + 1 of the tile) and the rows of its half-wave: wave w's half h takes rows
+// w + 4 (u + RW h), u < RW = SR / 8, and runs their four lane sums for both positions side by side over the head
+// (a query read serves two positions, a key read RW rows). The rows' tile maxima by half-wave reductions.
+template <int HS> constexpr int scores_rows() { return HS <= 128 ? 64 : 32; }
 
 template <int HS, bool HALF>
 __global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
-  constexpr int LD = HS + 4, C4 = HS / 4;
+  constexpr int LD = HS + 4, C4 = HS / 4, SR = scores_rows<HS>(), RW = SR / 8;
   __shared__ float ks[TILE * LD];
-  __shared__ float qs[SROWS * HS];
+  __shared__ float qs[SR * HS];
   const int tile = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int mul = a.nh / a.nkv, tt_n = max(1, SROWS / mul);
+  const int half = lane >> 5, pl = lane & 31;
+  const int mul = a.nh / a.nkv, tt_n = max(1, SR / mul);
   const int t0 = blockIdx.z * tt_n, last = min(t0 + tt_n, a.m) - 1;
   const int p0 = tile * TILE, pos0 = first_position(a);
   if (p0 >= pos0 + last + 1) return;  // past every token of the block (uniform: before any barrier)
   const int kvdim = a.nkv * HS;
   const int np = min(TILE, pos0 + last + 1 - p0);  // positions any token of the block reaches
-  // keys: TILE * C4 float4, and the rows' queries: SROWS * C4 float4, requested together (clamped, unconditional)
-  constexpr int NK = TILE * C4 / 256, NQ = (SROWS * C4 + 255) / 256;
+  // keys: TILE * C4 float4, and the rows' queries: SR * C4 float4, requested together (clamped, unconditional)
+  constexpr int NK = TILE * C4 / 256, NQ = (SR * C4 + 255) / 256;
   float4 kr[NK], qr[NQ];
 #pragma unroll
   for (int u = 0; u < NK; ++u) {
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
   }
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
-    const int i = min(tid + u * 256, SROWS * C4 - 1), r = i / C4, c = i % C4;
+    const int i = min(tid + u * 256, SR * C4 - 1), r = i / C4, c = i % C4;
     const int t = min(t0 + r / mul, last), h = kh * mul + r % mul;
     qr[u] = *reinterpret_cast<const float4 *>(a.q + (int64_t)t * a.q_stride + (int64_t)h * HS + 4 * c);
   }
@@ -141,39 +143,53 @@ __global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
     const int i = tid + u * 256;
-    if (i < SROWS * C4) *reinterpret_cast<float4 *>(qs + 4 * i) = qr[u];
+    if (i < SR * C4) *reinterpret_cast<float4 *>(qs + 4 * i) = qr[u];
   }
   __syncthreads();
   const float isq = 1.0f / __builtin_sqrtf((float)HS);
-  float l[8][4];
+  float l[2][RW][4];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) l[u][0] = l[u][1] = l[u][2] = l[u][3] = 0.0f;
-  const float *kp = ks + lane * LD;
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int u = 0; u < RW; ++u) l[e][u][0] = l[e][u][1] = l[e][u][2] = l[e][u][3] = 0.0f;
+  const float *kp0 = ks + (2 * pl) * LD, *kp1 = kp0 + LD;
+  const float *qb = qs + (wave + 4 * RW * half) * HS;  // row u of the half-wave at qb + 4 u HS
 #pragma unroll 4
   for (int j = 0; j < HS; j += 4) {
-    const float4 kv = *reinterpret_cast<const float4 *>(kp + j);
+    const float4 k0 = *reinterpret_cast<const float4 *>(kp0 + j);
+    const float4 k1 = *reinterpret_cast<const float4 *>(kp1 + j);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float4 qv = *reinterpret_cast<const float4 *>(qs + (wave + 4 * u) * HS + j);
-      l[u][0] = l[u][0] + qv.x * kv.x;
-      l[u][1] = l[u][1] + qv.y * kv.y;
-      l[u][2] = l[u][2] + qv.z * kv.z;
-      l[u][3] = l[u][3] + qv.w * kv.w;
+    for (int u = 0; u < RW; ++u) {
+      const float4 qv = *reinterpret_cast<const float4 *>(qb + 4 * u * HS + j);
+      l[0][u][0] = l[0][u][0] + qv.x * k0.x;
+      l[0][u][1] = l[0][u][1] + qv.y * k0.y;
+      l[0][u][2] = l[0][u][2] + qv.z * k0.z;
+      l[0][u][3] = l[0][u][3] + qv.w * k0.w;
+      l[1][u][0] = l[1][u][0] + qv.x * k1.x;
+      l[1][u][1] = l[1][u][1] + qv.y * k1.y;
+      l[1][u][2] = l[1][u][2] + qv.z * k1.z;
+      l[1][u][3] = l[1][u][3] + qv.w * k1.w;
     }
   }
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int r = wave + 4 * u, tt = r / mul, hl = r % mul, t = t0 + tt;
-    const bool row = tt < tt_n && t < a.m;  // uniform over the wave
+  for (int u = 0; u < RW; ++u) {
+    const int r = wave + 4 * (u + RW * half), tt = r / mul, hl = r % mul, t = t0 + tt;
+    const bool row = tt < tt_n && t < a.m;  // uniform over the half-wave
     const int count = first_position(a) + min(t, a.m - 1) + 1;
-    float sc = -__builtin_inff();
-    if (row && p0 + lane < count) {
-      sc = ((l[u][0] + l[u][2]) + (l[u][1] + l[u][3])) * isq;
-      a.scores[((int64_t)t * a.nh + kh * mul + hl) * a.seq_len + p0 + lane] = sc;
+    float *srow = a.scores + ((int64_t)t * a.nh + kh * mul + hl) * a.seq_len;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int p = p0 + 2 * pl + e;
+      if (row && p < count) {
+        const float sc = ((l[e][u][0] + l[e][u][2]) + (l[e][u][1] + l[e][u][3])) * isq;
+        srow[p] = sc;
+        mx = wmax(mx, sc);
+      }
     }
-    float mx = sc;  // the tile's largest of this (token, head)
-    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-    if (row && lane == 0 && p0 < count) a.tilemax[((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1) + tile] = mx;
+    // the tile's largest of this (token, head): the 32 lanes of the half-wave (xor offsets below 32 stay in it)
+    for (int o = 16; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+    if (row && pl == 0 && p0 < count) a.tilemax[((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1) + tile] = mx;
   }
 }
 
@@ -570,7 +586,7 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   if (a.m <= DECODE_TOKENS) {
     hipLaunchKernelGGL((scores_kernel<HS, HALF>), dim3(tiles, a.nkv, a.m), dim3(256), 0, s, a);
   } else {
-    const int tt = std::max(1, SROWS / (a.nh / a.nkv));
+    const int tt = std::max(1, scores_rows<HS>() / (a.nh / a.nkv));
     hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   }
   int nslot = 0;
