@@ -82,6 +82,20 @@ def copy_calibration(nbytes=1 << 30, reps=4):
     print(json.dumps({"copy_bytes": nbytes, "copies": reps}))
 
 
+def host_cpu():
+    """the host's CPU model and the logical CPUs this process may run on"""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus_available": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline(pk, spec, seconds=20.0):
     """the oracle (oracle/liboracle.so, the reference's arithmetic restated in C) on the host's cores, on a bounded
     sample of the same workload: the model's widths with 2 of its layers and its classifier, a few decode tokens,
@@ -114,6 +128,7 @@ def cpu_baseline(pk, spec, seconds=20.0):
     per_token = tl * layers / sample_layers + (tf - tl)
     model.close()
     return {"value": 1.0 / per_token, "unit": "tok/s", "cores": int(ol.load().or_get_threads()), "kind": "port",
+            "host": host_cpu(),
             "sample": (f"oracle decode (C restatement of the reference's WASM path, OpenMP) at the model's widths with "
                        f"{sample_layers} of {layers} layers and the classifier, {len(t_layers) * 2} tokens at positions "
                        f"0-{pos - 1}; per-layer time scaled to {layers} layers; short context (the measured 8B run is "
