@@ -82,6 +82,27 @@ def copy_calibration(nbytes=1 << 30, reps=4):
     print(json.dumps({"copy_bytes": nbytes, "copies": reps}))
 
 
+def read_ceiling(pk, nbytes=4 << 30, passes=4):
+    """the HBM read bandwidth a plain streaming kernel reaches on this GPU (hk_read_ceiling, the device form of the
+    reference's kernels/ceilings.ts read()): 4 GiB (more than the 256 MB MALL holds) read 4 times after a memset,
+    GB/s of one pass. A practical figure, not a bound: the decode GEMV's access pattern reads its largest matrices a
+    little faster."""
+    lib = ctypes.CDLL("libamdhip64.so")
+    buf = ctypes.c_void_p()
+    if lib.hipMalloc(ctypes.byref(buf), ctypes.c_size_t(nbytes)) != 0:
+        raise RuntimeError("hipMalloc failed")
+    try:
+        if lib.hipMemset(buf, 1, ctypes.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMemset failed")
+        checksum, ms = ctypes.c_int32(0), ctypes.c_double(0.0)
+        pk.hip_engine.check(pk.library().hk_read_ceiling(buf, nbytes, passes, ctypes.byref(checksum), ctypes.byref(ms),
+                                                         None))
+    finally:
+        hip_sync()
+        lib.hipFree(buf)
+    return nbytes / (ms.value * 1e-3) / 1e9
+
+
 def host_cpu():
     """the host's CPU model and the logical CPUs this process may run on"""
     model = "unknown"
@@ -215,6 +236,7 @@ def main():
                             "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     traffic = TRAFFIC.get(args.model)
     eng.release()
+    ceiling_gbs = read_ceiling(pk)
 
     cpu = None if args.no_cpu else cpu_baseline(pk, spec)
     out = {
@@ -243,7 +265,9 @@ def main():
                      "launches_per_pass": int(gemv_launches),
                      "algorithmic_bytes_per_launch": round(gemv_bytes / gemv_launches),
                      "us_per_launch": round(1e3 * gemv_ms / gemv_launches, 3),
-                     "traffic_source": traffic["source"] if traffic else None},
+                     "traffic_source": traffic["source"] if traffic else None,
+                     "read_ceiling_gb_s": round(ceiling_gbs, 1),
+                     "frac_of_read_ceiling": round(gemv_gbs / ceiling_gbs, 4)},
         "gemv_by_matrix": by_matrix,
         "profile_ms": {k: round(v[0], 4) for k, v in prof.items()},
         "profiled_step_ms": round(step_ms, 4),

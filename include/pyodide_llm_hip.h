@@ -225,6 +225,12 @@ int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t coun
 int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
                   void *stream);
 
+/* The memory's read ceiling, kernels/ceilings.ts:9-25 read(p, bytes, passes) on the device: bytes (a multiple of 64)
+ * at the device pointer p read passes times by a streaming kernel (one launch a pass). *checksum is read()'s: the
+ * xor of the four lanes j of passes times the sum (mod 2^32) of the 32-bit words at p + 16k + 4j. *ms is the mean
+ * time of a pass (HIP events on the stream). Blocks until done. */
+int32_t hk_read_ceiling(const void *p, int64_t bytes, int32_t passes, int32_t *checksum, double *ms, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1283,4 +1283,37 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
   return HE_OK;
 }
 
+int32_t hk_read_ceiling(const void *p, int64_t bytes, int32_t passes, int32_t *checksum, double *ms, void *stream) {
+  if (!p || !checksum || !ms || bytes < 64 || bytes % 64 || passes < 1)
+    return fail(HE_E_ARG, "hk_read_ceiling: bad arguments");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int32_t blocks = read_ceiling_blocks(bytes);
+  uint32_t *partial = nullptr;
+  int32_t rc = dev_alloc(&partial, sizeof(uint32_t) * 4 * blocks);
+  if (rc) return rc;
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t err = hipEventCreate(&a);
+  if (err == hipSuccess) err = hipEventCreate(&b);
+  if (err == hipSuccess) err = hipEventRecord(a, s);
+  for (int32_t r = 0; r < passes && err == hipSuccess; ++r) err = launch_read_ceiling(p, bytes, partial, s);
+  if (err == hipSuccess) err = hipEventRecord(b, s);
+  if (err == hipSuccess) err = hipEventSynchronize(b);
+  float t = 0;
+  if (err == hipSuccess) err = hipEventElapsedTime(&t, a, b);
+  std::vector<uint32_t> h(4 * (size_t)blocks);
+  if (err == hipSuccess) err = hipMemcpy(h.data(), partial, sizeof(uint32_t) * h.size(), hipMemcpyDeviceToHost);
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  (void)hipFree(partial);
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_read_ceiling: ") + hipGetErrorString(err));
+  // every pass reads the same words: passes times one pass's lane sums (mod 2^32)
+  uint32_t lane[4] = {0, 0, 0, 0};
+  for (int32_t i = 0; i < blocks; ++i)
+    for (int j = 0; j < 4; ++j) lane[j] += h[4 * (size_t)i + j];
+  for (int j = 0; j < 4; ++j) lane[j] *= (uint32_t)passes;
+  *checksum = (int32_t)(lane[0] ^ lane[1] ^ lane[2] ^ lane[3]);
+  *ms = (double)t / passes;
+  return HE_OK;
+}
+
 }  // extern "C"

@@ -151,6 +151,10 @@ bool attention_supported(int32_t hs, int32_t nh, int32_t nkv);
 // of 32 (a block holds a whole group) and whose context fits the decode kernel's LDS
 bool attention_quantizes(const AttnArgs &a);
 
+// a streaming read of bytes (a multiple of 16) at p: block b's sums of its 32-bit words lane by lane (j = word index
+// % 4) into partial[4 b + j], for read_ceiling_blocks(bytes) blocks
+int32_t read_ceiling_blocks(int64_t bytes);
+hipError_t launch_read_ceiling(const void *p, int64_t bytes, uint32_t *partial, hipStream_t s);
 // greedy: the first index of the largest logit into *out (and the value into *value)
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
                          hipStream_t s);

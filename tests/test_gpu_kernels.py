@@ -1,10 +1,13 @@
 """The HIP kernels through the C ABI against the oracle, to the bit: quantize_x, the exact int32 group sums and the
 float32 outputs of the decode GEMV and the prefill GEMM (matmul_q8r / q8 / q6r / q6), at the reference's
 known-answer sizes and at the standalone matmul's full sizes (K=4096, N in {4096, 14336}, M in {1, 4, 16, 512})."""
+import ctypes
+
 import numpy as np
 import pytest
 
 import gpu_lib as gl
+from paths import package
 import oracle_lib as ol
 
 pytestmark = pytest.mark.gpu
@@ -136,3 +139,18 @@ def test_extremes_of_int8_equal_float64(reps):
     got = gl.matmul(xq, xs, w, ws, rows, n, 64, 0)
     want = (w.astype(np.float64)[None] * (xq.astype(np.float64)[:, None] - 64)).sum(-1) * 2.0 ** -7 * xs[:, :1].astype(np.float64)
     assert np.array_equal(got.astype(np.float64), want)
+
+
+@pytest.mark.parametrize("nbytes, passes", [(64, 1), (4096, 3), (1 << 20, 2), ((1 << 20) + 192, 5)])
+def test_read_ceiling_checksum(nbytes, passes):
+    """hk_read_ceiling returns kernels/ceilings.ts:9-25 read()'s checksum: the xor of the four lanes j of passes times
+    the sum (mod 2^32) of the 32-bit words at p + 16k + 4j"""
+    rng = np.random.default_rng(nbytes)
+    words = rng.integers(0, 2**32, size=nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = gl.upload(words)
+    lanes = [int(words[j::4].astype(np.uint64).sum() * passes) & 0xFFFFFFFF for j in range(4)]
+    want = lanes[0] ^ lanes[1] ^ lanes[2] ^ lanes[3]
+    got, ms = ctypes.c_int32(0), ctypes.c_double(0.0)
+    gl.check(package().library().hk_read_ceiling(buf.ptr, nbytes, passes, ctypes.byref(got), ctypes.byref(ms), None))
+    assert (got.value & 0xFFFFFFFF) == want
+    assert ms.value > 0
