@@ -364,6 +364,9 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->sample_best, sizeof(float) * 4);
   ALLOC(e->sink, sizeof(uint32_t) * 64);
   {
+    // the fills pay where a token's weights come from HBM; a checkpoint that the 256 MB MALL holds whole (with room for
+    // the cache and activations) finds them there, and the fill blocks would only add latency
+    if (e->size < (192ull << 20)) e->fetch_xcd_bytes = 0;
     // PYODIDE_LLM_HIP_L2FETCH: KiB an XCD of the L2 fills ahead of the one-token GEMVs (0: none)
     const char *env = std::getenv("PYODIDE_LLM_HIP_L2FETCH");
     if (env && *env) e->fetch_xcd_bytes = std::max(0L, std::atol(env)) << 10;
