@@ -610,7 +610,12 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     }
     const bool fuse_qkv = c.arch == HE_ARCH_LLAMA && !c.qk_norm && m == 1 &&
                           decode_fuses_qkv(dim, c.six != 0, c.relaxed != 0);
-    if (!ln) {
+    // one token of a small model (dim <= 1024): the q/k/v and w1/w3 GEMVs take the float32 token and run rmsnorm and
+    // quantize_x in each block (an ordered sum of 256 steps at most), two launches a layer fewer. (At dim 4096 each
+    // block repeating the 1024-step sum costs more than the launch.)
+    const bool norm_in_gemv = !ln && m == 1 && dim <= 1024 && decode_takes_f32(dim, c.six != 0, c.relaxed != 0);
+    const F32Source att_src{e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim)};
+    if (!ln && !norm_in_gemv) {
       const L2Fetch fq = fetch_for(e, qkv, 3, dim, m, 256, fuse_qkv);
       HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
         return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_ATT, (int64_t)l * dim), m, dim, dim,
@@ -621,9 +626,9 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
       // one token: the q/k/v GEMV adds the biases, rotates q and k and writes k and v into the cache itself
       const QkvFuse fuse{1, qp.bq, qp.bk, qp.bv, e->cos_t, e->sin_t, qp.kcache, qp.vcache, pos0, hs, kvdim, c.half_kv,
                          qp.vstride, dpos};
-      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, nullptr, &fuse));
+      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, norm_in_gemv ? &att_src : nullptr, &fuse));
     } else {
-      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs));
+      HIP_TRY(matmul(e, qkv, 3, dim, m, e->xq, e->xs, norm_in_gemv ? &att_src : nullptr));
       if (c.qk_norm) {
         // Qwen3: the q/k biases, then every head normalized, before RoPE
         HIP_TRY(timed(e, HE_K_NORM, (double)m * (qdim + kvdim) * 8, [&] {
@@ -700,11 +705,14 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     const MatSeg w13[2] = {{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), e->hb, hidden, hidden, 0},
                            {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), e->hb2, hidden, hidden, 0}};
     const L2Fetch f13 = fetch_for(e, w13, 2, dim, m, 256);
-    HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
-      return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim, W,
-                                  W / 32, 0, c.rms_norm_eps, e->bias, s, &f13);
-    }));
-    HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs));
+    if (!norm_in_gemv) {
+      HIP_TRY(timed(e, HE_K_NORM, (double)m * dim * (8 + 1 + 0.125) + dim * 4.0, [&] {
+        return launch_rmsnorm_quant(e->xq, e->xs, nullptr, e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim), m, dim, dim,
+                                    W, W / 32, 0, c.rms_norm_eps, e->bias, s, &f13);
+      }));
+    }
+    const F32Source ffn_src{e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim)};
+    HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs, norm_in_gemv ? &ffn_src : nullptr));
     const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
     HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * hidden * (8 + 1 + 0.125), [&] {
       return launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s);
