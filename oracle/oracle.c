@@ -1,7 +1,7 @@
 /*
  * oracle.c — TEST INFRASTRUCTURE, NOT PART OF THE PRODUCT: the CPU restatement of pyodide-llm's int8/int6 forward
  * path in the reference's float32 order. Loaded only by tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg (as the checker / the timed CPU baseline). Built with -ffp-contract=off: no fused multiply-adds,
+ * cpu_baseline leg (as the parity reference / the timed CPU baseline). Built with -ffp-contract=off: no fused multiply-adds,
  * every float32 operation rounded on its own as WebAssembly's f32 arithmetic is.
  *
  * How each part is pinned (tests/test_oracle_*.py):

@@ -4,7 +4,7 @@
  * A plain-C restatement of the arithmetic of pyodide-llm's CPU path (kernels/kernel.ts, kernels/kernel_relaxed.ts,
  * kernels/six.ts, public/forward.js run(), public/llama2_convert.py quantize(), public/llama2_numpy.py
  * quantize6/pack6/Places), in the reference's exact float32 order. Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load it, as the checker or the CPU baseline, never as the thing measured on the GPU.
+ * cpu_baseline leg may load it, as the parity reference or the CPU baseline, never as the thing measured on the GPU.
  * Every function cites the reference lines it follows; oracle/oracle.c's header lists how each one is pinned.
  */
 #ifndef PYODIDE_LLM_ORACLE_H

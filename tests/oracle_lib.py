@@ -1,4 +1,4 @@
-"""ctypes over oracle/liboracle.so — TEST INFRASTRUCTURE (the checker and the CPU baseline), never the product."""
+"""ctypes over oracle/liboracle.so — TEST INFRASTRUCTURE (the parity reference and the CPU baseline), never the product."""
 import ctypes
 import os
 

@@ -81,7 +81,7 @@ def test_device_checkpoint_equals_host_checkpoint(name):
 
 
 def test_greedy_generation_matches_the_oracle():
-    """configs[0]'s shape: a 32-token prompt through forwardMany, then 128 greedy tokens (stop tokens off)"""
+    """stories15M shape: a 32-token prompt through forwardMany, then 128 greedy tokens (stop tokens off)"""
     cfg, tensors, ck, cos, sin, _ = build("stories15m", half_kv=1)
     rng = np.random.default_rng(2)
     prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=32)]
