@@ -469,6 +469,14 @@ void or_from_f16(float *out, const uint16_t *x, int32_t n) {
   for (int32_t i = 0; i < n; i++) out[i] = half_to_f32(x[i]);
 }
 
+/* public/forward.js:593-597 halfToFloat, what keysAndValues() reads a float16 cache with: exact for every finite half,
+ * and unlike the kernels' half() an infinity stays infinite and a NaN is NaN */
+static float half_to_float(uint16_t h) {
+  const uint32_t exponent = (h >> 10) & 0x1f, fraction = h & 0x3ff;
+  if (exponent == 31) return fraction ? NAN : ((h & 0x8000) ? -INFINITY : INFINITY);
+  return half_to_f32(h);
+}
+
 /* kernels/kernel.ts:654-667 swiglu: v / (1 + vexp(-v)) * h3 (the scalar tail's fexp gives the same bits: where the
  * two differ, 1 + exp(x) is 1 either way) */
 void or_swiglu(float *out, const float *h1, const float *h3, int32_t n) {
@@ -948,11 +956,58 @@ void or_model_close(or_model *m) {
   free(m);
 }
 
+/* kernels/kernel_relaxed.ts:84-183 matmul_q8r_tile (public/jobs.js:96 runs it on prompt blocks): a row's weights
+ * against every token of the block while the row is at hand. Per (row, token) it is the one-token kernel to the bit
+ * (the same exact group sums, relaxed_row / plain_row in the same order), so this only changes how often a row is
+ * read: once a block instead of once a token. xq [count][K] from quantize_x(bias), xs [count][K/32]. */
+static void matmul_tokens(float *out, int64_t out_stride, const int8_t *xq, const float *xs, const void *w,
+                          const float *ws, int32_t rows, int32_t K, int32_t count, int32_t bias, int32_t six) {
+  const int32_t ng = K / GS;
+  int8_t *xc = (int8_t *)malloc((size_t)count * (size_t)K);
+  if (bias) centred(xc, xq, count * K);
+  else memcpy(xc, xq, (size_t)count * (size_t)K);
+#pragma omp parallel
+  {
+    int8_t *wide = (int8_t *)malloc((size_t)K);
+    int32_t *S = (int32_t *)malloc(sizeof(int32_t) * 4 * (size_t)ng);
+#pragma omp for schedule(dynamic, 8)
+    for (int32_t r = 0; r < rows; r++) {
+      const int8_t *row;
+      if (six) {
+        or_unpack6(wide, (const uint8_t *)w + (int64_t)r * ng * 24, ng);
+        row = wide;
+      } else {
+        row = (const int8_t *)w + (int64_t)r * K;
+      }
+      for (int32_t t = 0; t < count; t++) {
+        const int8_t *x = xc + (int64_t)t * K;
+        const float *st = xs + (int64_t)t * ng;
+        if (bias) {
+          for (int32_t g = 0; g < ng; g++) S[g] = dot32(row + g * GS, x + g * GS);
+          out[t * out_stride + r] = relaxed_row(S, ws + (int64_t)r * ng, st, ng);
+        } else {
+          for (int32_t g = 0; g < ng; g++) lanes32(S + 4 * g, row + g * GS, x + g * GS);
+          out[t * out_stride + r] = plain_row(S, ws + (int64_t)r * ng, st, ng);
+        }
+      }
+    }
+    free(S);
+    free(wide);
+  }
+  free(xc);
+}
+
 /* public/forward.js:954-960 matmuls(): every token's input quantized once, then every matrix of the list */
 static void matmuls(or_model *m, const float *input, int64_t in_stride, int32_t count, int32_t K, int32_t id,
                     int32_t l, int32_t rows, float *out, int64_t out_stride) {
   const int8_t *w = mat_values(m, id, l, rows, K);
   const float *ws = mat_scales(m, id, l, rows, K);
+  if (count > 1) {
+    for (int32_t t = 0; t < count; t++)
+      or_quantize_x(m->xq + (int64_t)t * K, m->xs + (int64_t)t * (K / GS), input + t * in_stride, K, m->bias);
+    matmul_tokens(out, out_stride, m->xq, m->xs, w, ws, rows, K, count, m->bias, m->c.six);
+    return;
+  }
   for (int32_t t = 0; t < count; t++) {
     int8_t *xq = m->xq + (int64_t)t * K;
     float *xs = m->xs + (int64_t)t * (K / GS);
@@ -1104,8 +1159,10 @@ void or_model_kv(const or_model *m, int32_t from, int32_t count, float *keys, fl
       const int64_t at = ((int64_t)l * m->c.seq_len + from + t) * m->kvdim;
       float *ko = keys + ((int64_t)l * count + t) * m->kvdim, *vo = values + ((int64_t)l * count + t) * m->kvdim;
       if (m->c.half_kv) {
-        or_from_f16(ko, (const uint16_t *)m->keys + at, m->kvdim);
-        or_from_f16(vo, (const uint16_t *)m->values + at, m->kvdim);
+        for (int32_t i = 0; i < m->kvdim; i++) {
+          ko[i] = half_to_float(((const uint16_t *)m->keys)[at + i]);
+          vo[i] = half_to_float(((const uint16_t *)m->values)[at + i]);
+        }
       } else {
         memcpy(ko, (const float *)m->keys + at, sizeof(float) * (size_t)m->kvdim);
         memcpy(vo, (const float *)m->values + at, sizeof(float) * (size_t)m->kvdim);

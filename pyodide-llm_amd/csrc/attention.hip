@@ -568,6 +568,10 @@ __global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a
 }
 #undef ATT_FETCH
 
+// LDS bytes of softmax_kernel for a (token, head) of count positions: the exponentials as four ordered sums' rows and
+// the tail
+size_t softmax_lds(int count) { return sizeof(float) * (size_t)(4 * chain_rowstride((count & ~3) / 4) + 4); }
+
 // LDS bytes of attend_kernel for the largest count of a launch (ring slots into *nslot), 0 where it does not fit
 template <int HS>
 int attend_lds(const AttnArgs &a, int *nslot) {
@@ -590,7 +594,7 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   }
   int nslot = 0;
-  const int fused = a.m <= DECODE_TOKENS ? attend_lds<HS>(a, &nslot) : 0;
+  const int fused = a.m <= DECODE_TOKENS && !a.split ? attend_lds<HS>(a, &nslot) : 0;
   if (fused) {
     static bool sized = false;  // once a process: let the kernel take LDS past 64 KiB
     if (!sized) {
@@ -604,8 +608,17 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
                        a, nslot);
     return hipGetLastError();
   }
-  const int most4 = (a.pos0 + a.m) & ~3;
-  const size_t lds_b = sizeof(float) * (size_t)(4 * chain_rowstride(most4 / 4) + 4);
+  const size_t lds_b = softmax_lds(a.pos0 + a.m);
+  if (lds_b > (size_t)ALDS) return hipErrorInvalidValue;
+  if (lds_b > 64 * 1024) {
+    static bool sized = false;  // once a process: let the kernel take LDS past 64 KiB
+    if (!sized) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&softmax_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, ALDS);
+      if (e != hipSuccess) return e;
+      sized = true;
+    }
+  }
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
   constexpr int COLS = HS % 32 == 0 ? 32 : 16;
   const int tt = 2 * std::max(1, 256 / COLS / (a.nh / a.nkv));  // tokens a block: two sums a thread
@@ -634,8 +647,14 @@ bool attention_supported(int32_t hs, int32_t nh, int32_t nkv) {
   return sizes && nkv > 0 && nh % nkv == 0 && nh / nkv <= MAXMUL;
 }
 
+int32_t attention_most_positions() {
+  int32_t n = (ALDS / 4) & ~3;
+  while (n > 0 && softmax_lds(n) > (size_t)ALDS) n -= 4;
+  return n;
+}
+
 bool attention_quantizes(const AttnArgs &a) {
-  if (!attention_supported(a.hs, a.nh, a.nkv) || a.m > DECODE_TOKENS || a.hs % 32) return false;
+  if (!attention_supported(a.hs, a.nh, a.nkv) || a.m > DECODE_TOKENS || a.hs % 32 || a.split) return false;
   int nslot = 0;
   switch (a.hs) {
     case 32: return attend_lds<32>(a, &nslot) > 0;

@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <limits>
 #include <string>
 #include <vector>
 
@@ -173,6 +174,9 @@ struct he_engine {
   float *before = nullptr, *columns = nullptr, *picked = nullptr;
   OutlierSet outliers{};
   bool replayable = false;  // run_chunk is building the graph (positions from state, no host copies)
+  // PYODIDE_LLM_HIP_ATTEND=split: decode steps take the separate softmax and weighted-value kernels that contexts
+  // past the fused decode kernel's LDS take (a check of that path at any context)
+  bool attend_split = false;
   // one-token GEMVs whose first rows extra blocks of the launch before them bring into L2 (L2Fetch); sink: their
   // 64 words
   int64_t fetch_xcd_bytes = 3 << 20;
@@ -231,6 +235,9 @@ int32_t check_config(const he_config &c) {
   if (!attention_supported(c.head_size, c.n_heads, c.n_kv_heads))
     return fail(HE_E_ARG, "attention takes head sizes 16, 32, 48, 64, 96, 128, 256 and at most 8 query heads a kv head");
   if (c.seq_len % 4) return fail(HE_E_ARG, "seq_len must be a multiple of 4");
+  if (c.seq_len > attention_most_positions())
+    return fail(HE_E_ARG, "seq_len is longer than the attention kernels take (" +
+                              std::to_string(attention_most_positions()) + " positions)");
   if (c.arch != HE_ARCH_LLAMA && c.arch != HE_ARCH_GPT2 && c.arch != HE_ARCH_NEOX)
     return fail(HE_E_ARG, "arch is not one of llama, gpt2, neox");
   if (layer_norm(c)) {
@@ -370,6 +377,8 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
     // PYODIDE_LLM_HIP_L2FETCH: KiB an XCD of the L2 fills ahead of the one-token GEMVs (0: none)
     const char *env = std::getenv("PYODIDE_LLM_HIP_L2FETCH");
     if (env && *env) e->fetch_xcd_bytes = std::max(0L, std::atol(env)) << 10;
+    const char *attend = std::getenv("PYODIDE_LLM_HIP_ATTEND");
+    e->attend_split = attend && std::strcmp(attend, "split") == 0;
   }
   if (c.parallel_residual) ALLOC(e->before, sizeof(float) * T * c.dim);
   e->outliers.n = c.n_outliers;
@@ -664,6 +673,7 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.xq_stride = W;
     at.xs_stride = W / 32;
     at.bias = e->bias;
+    at.split = e->attend_split;
     const bool quantized = attention_quantizes(at);
     if (!quantized) at.xq = nullptr;
     double kv_rows = 0;
@@ -1116,8 +1126,14 @@ int32_t he_kv_read(he_engine *e, int32_t from, int32_t count, float *keys, float
       std::memcpy(&f, &rows[i * 4], 4);
       return f;
     }
+    // public/forward.js:593-597 halfToFloat: exact for finite halves; an infinity stays infinite, a NaN is NaN (the
+    // kernels' widening, which attention uses, reads an infinity as 65536)
     uint16_t h;
     std::memcpy(&h, &rows[i * 2], 2);
+    if ((h & 0x7c00) == 0x7c00)
+      return (h & 0x3ff) ? std::numeric_limits<float>::quiet_NaN()
+                         : ((h & 0x8000) ? -std::numeric_limits<float>::infinity()
+                                         : std::numeric_limits<float>::infinity());
     int32_t bits = ((int32_t)(int16_t)h << 13) & (int32_t)0x8fffffff;
     float f;
     std::memcpy(&f, &bits, 4);

@@ -143,10 +143,15 @@ struct AttnArgs {
   int8_t *xq;
   float *xs;
   int32_t xq_stride, xs_stride, bias;
+  // decode launches take the prompt's separate softmax and weighted-value kernels, as past the fused kernel's LDS
+  int32_t split;
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the head sizes and grouping the attention kernels take (hs in {16, 32, 48, 64, 96, 128, 256}, nh / nkv <= 8)
 bool attention_supported(int32_t hs, int32_t nh, int32_t nkv);
+// the longest context (a multiple of 4) the attention kernels take: a (token, head)'s exponentials are held in one
+// block's LDS (160 KiB on gfx950) for their ordered sum
+int32_t attention_most_positions();
 // whether launch_attention writes quantize_x of its output too (a.xq): decode launches whose head size is a multiple
 // of 32 (a block holds a whole group) and whose context fits the decode kernel's LDS
 bool attention_quantizes(const AttnArgs &a);

@@ -98,18 +98,32 @@ static int get_u64(napi_env env, napi_value v, uint64_t *out) {
   return 1;
 }
 
-static he_engine *engine_of(napi_env env, napi_value v) {
+/* what a JavaScript engine external points to: the handle (NULL once closed) and the sizes its output arrays are
+ * checked against, so that a short typed array is a TypeError instead of a write past its end */
+typedef struct engine_slot {
+  he_engine *e;
+  int64_t vocab;  /* floats of the logits */
+  int64_t layers; /* keysAndValues: layers * count * kv_dim floats of keys, and of values */
+  int64_t kv_dim;
+} engine_slot;
+
+static engine_slot *slot_of(napi_env env, napi_value v) {
   void *p = NULL;
   if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
     napi_throw_type_error(env, NULL, "hip_engine: not an engine (or one already closed)");
     return NULL;
   }
-  he_engine **slot = (he_engine **)p;
-  if (!*slot) {
+  engine_slot *slot = (engine_slot *)p;
+  if (!slot->e) {
     napi_throw_error(env, NULL, "hip_engine: the engine was released");
     return NULL;
   }
-  return *slot;
+  return slot;
+}
+
+static he_engine *engine_of(napi_env env, napi_value v) {
+  engine_slot *slot = slot_of(env, v);
+  return slot ? slot->e : NULL;
 }
 
 /* the bytes of a TypedArray (of the given type, or any if type < 0) or a DataView-less ArrayBuffer */
@@ -202,19 +216,22 @@ static int tensors_of(napi_env env, napi_value arr, he_tensor *t) {
 static void finalize_engine(napi_env env, void *data, void *hint) {
   (void)env;
   (void)hint;
-  he_engine **slot = (he_engine **)data;
-  if (*slot) he_close(*slot);
+  engine_slot *slot = (engine_slot *)data;
+  if (slot->e) he_close(slot->e);
   free(slot);
 }
 
-static napi_value wrap_engine(napi_env env, he_engine *e) {
-  he_engine **slot = (he_engine **)malloc(sizeof *slot);
+static napi_value wrap_engine(napi_env env, he_engine *e, const he_config *c) {
+  engine_slot *slot = (engine_slot *)malloc(sizeof *slot);
   if (!slot) {
     he_close(e);
     napi_throw_error(env, NULL, "hip_engine: out of host memory");
     return NULL;
   }
-  *slot = e;
+  slot->e = e;
+  slot->vocab = c->vocab_size;
+  slot->layers = c->n_layers;
+  slot->kv_dim = (int64_t)c->n_kv_heads * c->head_size;
   napi_value out;
   if (napi_create_external(env, slot, finalize_engine, NULL, &out) != napi_ok) {
     he_close(e);
@@ -248,7 +265,7 @@ static napi_value js_open(napi_env env, napi_callback_info info) {
   const int32_t rc = he_open(&c, t, (const uint8_t *)data + base, size, (const float *)cos_d, (const float *)sin_d,
                              max_block, &e);
   if (rc) return throw_engine(env, rc);
-  return wrap_engine(env, e);
+  return wrap_engine(env, e, &c);
 }
 
 /* openSynthetic(config, tensors, size, seed, cos, sin, maxBlock) -> engine (he_open_synthetic) */
@@ -271,17 +288,18 @@ static napi_value js_open_synthetic(napi_env env, napi_callback_info info) {
   he_engine *e = NULL;
   const int32_t rc = he_open_synthetic(&c, t, size, seed, (const float *)cos_d, (const float *)sin_d, max_block, &e);
   if (rc) return throw_engine(env, rc);
-  return wrap_engine(env, e);
+  return wrap_engine(env, e, &c);
 }
 
 /* forward(engine, token, pos, needLogits, logits: Float32Array|null) */
 static napi_value js_forward(napi_env env, napi_callback_info info) {
   napi_value argv[5];
   if (!args_of(env, info, 5, argv)) return NULL;
-  he_engine *e = engine_of(env, argv[0]);
+  engine_slot *slot = slot_of(env, argv[0]);
   int32_t token, pos;
   bool need = false;
-  if (!e || !get_i32(env, argv[1], &token) || !get_i32(env, argv[2], &pos)) return NULL;
+  if (!slot || !get_i32(env, argv[1], &token) || !get_i32(env, argv[2], &pos)) return NULL;
+  he_engine *e = slot->e;
   NAPI_TRY(env, napi_get_value_bool(env, argv[3], &need));
   napi_valuetype tt;
   NAPI_TRY(env, napi_typeof(env, argv[4], &tt));
@@ -290,8 +308,8 @@ static napi_value js_forward(napi_env env, napi_callback_info info) {
     void *d;
     size_t n;
     if (!bytes_of(env, argv[4], napi_float32_array, &d, &n)) return NULL;
+    if (n < 4 * (size_t)slot->vocab) return throw_type(env, "hip_engine: logits holds fewer than vocab_size floats");
     logits = (float *)d;
-    (void)n;
   }
   const int32_t rc = he_forward(e, token, pos, need ? 1 : 0, logits);
   if (rc) return throw_engine(env, rc);
@@ -355,11 +373,12 @@ static napi_value js_generate_many(napi_env env, napi_callback_info info) {
 static napi_value js_logits(napi_env env, napi_callback_info info) {
   napi_value argv[2];
   if (!args_of(env, info, 2, argv)) return NULL;
-  he_engine *e = engine_of(env, argv[0]);
+  engine_slot *slot = slot_of(env, argv[0]);
   void *d;
   size_t n;
-  if (!e || !bytes_of(env, argv[1], napi_float32_array, &d, &n)) return NULL;
-  const int32_t rc = he_logits(e, (float *)d);
+  if (!slot || !bytes_of(env, argv[1], napi_float32_array, &d, &n)) return NULL;
+  if (n < 4 * (size_t)slot->vocab) return throw_type(env, "hip_engine: out holds fewer than vocab_size floats");
+  const int32_t rc = he_logits(slot->e, (float *)d);
   if (rc) return throw_engine(env, rc);
   return undefined(env);
 }
@@ -368,14 +387,18 @@ static napi_value js_logits(napi_env env, napi_callback_info info) {
 static napi_value js_kv_read(napi_env env, napi_callback_info info) {
   napi_value argv[5];
   if (!args_of(env, info, 5, argv)) return NULL;
-  he_engine *e = engine_of(env, argv[0]);
+  engine_slot *slot = slot_of(env, argv[0]);
   int32_t from, count;
   void *k, *v;
   size_t nk, nv;
-  if (!e || !get_i32(env, argv[1], &from) || !get_i32(env, argv[2], &count) ||
+  if (!slot || !get_i32(env, argv[1], &from) || !get_i32(env, argv[2], &count) ||
       !bytes_of(env, argv[3], napi_float32_array, &k, &nk) || !bytes_of(env, argv[4], napi_float32_array, &v, &nv))
     return NULL;
-  const int32_t rc = he_kv_read(e, from, count, (float *)k, (float *)v);
+  if (count < 0) return throw_type(env, "hip_engine: count is negative");
+  const uint64_t need = 4 * (uint64_t)slot->layers * (uint64_t)count * (uint64_t)slot->kv_dim;
+  if (nk < need || nv < need)
+    return throw_type(env, "hip_engine: keys or values holds fewer than layers * count * kv_dim floats");
+  const int32_t rc = he_kv_read(slot->e, from, count, (float *)k, (float *)v);
   if (rc) return throw_engine(env, rc);
   return undefined(env);
 }
@@ -421,10 +444,10 @@ static napi_value js_close(napi_env env, napi_callback_info info) {
   if (!args_of(env, info, 1, argv)) return NULL;
   void *p = NULL;
   NAPI_TRY(env, napi_get_value_external(env, argv[0], &p));
-  he_engine **slot = (he_engine **)p;
-  if (slot && *slot) {
-    he_engine *e = *slot;
-    *slot = NULL;
+  engine_slot *slot = (engine_slot *)p;
+  if (slot && slot->e) {
+    he_engine *e = slot->e;
+    slot->e = NULL;
     const int32_t rc = he_close(e);
     if (rc) return throw_engine(env, rc);
   }

@@ -7,7 +7,10 @@
 //     node tests/node/run_engine.mjs job.json
 import fs from "fs";
 import path from "path";
+import { createRequire } from "module";
 import * as F from "../../pyodide-llm_amd/forward_hip.mjs";
+
+const addon = createRequire(import.meta.url)("../../pyodide-llm_amd/hip_engine.node");
 
 const job = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
 const dir = path.dirname(process.argv[2]);
@@ -60,7 +63,30 @@ try {
   threw = e.message;
 }
 
+// the addon itself refuses output arrays shorter than what it would write (a TypeError, nothing written)
+const { config, tensors } = F.planToConfig(plan, { relaxedKernels: job.relaxed });
+const f32 = (bytes) => new Float32Array(Uint8Array.from(bytes).buffer);  // a copy of exactly the file's floats
+const raw = addon.open(config, tensors, memory.buffer, base, job.size, f32(read("cos.bin")), f32(read("sin.bin")), 16);
+const kvDim = config.n_kv_heads * config.head_size;
+const short = [];
+const refuses = (what, call) => {
+  try {
+    call();
+    short.push(`${what}: no error`);
+  } catch (e) {
+    short.push(e instanceof TypeError ? "TypeError" : `${what}: ${e.message}`);
+  }
+};
+refuses("forward", () => addon.forward(raw, 1, 0, true, new Float32Array(plan.vocab_size - 1)));
+refuses("logits", () => addon.logits(raw, new Float32Array(plan.vocab_size - 1)));
+refuses("kvRead keys", () => addon.kvRead(raw, 0, 1, new Float32Array(config.n_layers * kvDim - 1),
+  new Float32Array(config.n_layers * kvDim)));
+refuses("kvRead values", () => addon.kvRead(raw, 0, 2, new Float32Array(2 * config.n_layers * kvDim),
+  new Float32Array(2 * config.n_layers * kvDim - 1)));
+addon.close(raw);
+
 Promise.all([engine.release(), second.release()]).then((released) => {
   console.log(JSON.stringify({ ids, backend: engine.backend, promptBlock: engine.promptBlock, tokenBlock: engine.tokenBlock,
-    memoryBytes, sampled: sampled === undefined ? null : Array.from(sampled), released, threw, header: Array.from(header) }));
+    memoryBytes, sampled: sampled === undefined ? null : Array.from(sampled), released, threw, short,
+    header: Array.from(header) }));
 });

@@ -5,6 +5,7 @@ import glob
 import os
 import re
 
+import numpy as np
 import pytest
 
 from paths import REPO, package
@@ -64,3 +65,18 @@ def test_plan_conversion_takes_the_reference_plan_and_refuses_other_forms():
     assert (c.arch, c.rotary, t[pk.T["positions"]].offset) == (1, 0, 70000)
     c, _ = pk.plan_to_config({**plan, "arch": "neox", "rotary": 8, "parallel_residual": True})
     assert (c.arch, c.rotary, c.parallel_residual) == (2, 8, 1)
+
+
+def test_open_refuses_a_context_past_the_attention_kernels():
+    """a (token, head)'s exponentials are summed in order from one block's LDS (160 KiB): he_open refuses a seq_len
+    past what that holds (40704 positions) before it touches the device"""
+    pk = package()
+    lib = pk.library()
+    cfg = pk.config(dim=64, hidden_dim=128, n_layers=1, n_heads=4, n_kv_heads=4, head_size=16, vocab_size=64,
+                    seq_len=40708, shared_classifier=1)
+    tables = np.zeros(16, dtype=np.float32)
+    p = ctypes.c_void_p(tables.ctypes.data)
+    h = ctypes.c_void_p()
+    rc = lib.he_open(ctypes.byref(cfg), pk.TensorArray(), p, 16, p, p, 1, ctypes.byref(h))
+    assert rc == pk.hip_engine.HE_E_ARG and not h.value
+    assert b"seq_len is longer than the attention kernels take (40704 positions)" in lib.he_last_error()

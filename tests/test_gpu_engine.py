@@ -52,6 +52,25 @@ def test_forward_logits_and_cache_bits(name, relaxed, half_kv):
     eng.release()
 
 
+def test_kv_read_keeps_an_infinite_half_infinite():
+    """keysAndValues() of a float16 cache reads an infinity (a value past 65520) as infinity, as public/forward.js:
+    593-597 halfToFloat does, and the oracle's cache bits; attention reads it as 65536 (kernels/kernel.ts:383-392),
+    and the logits are the oracle's"""
+    cfg, tensors, ck, cos, sin, _ = build("tiny_qwen_int6", half_kv=1)
+    at = tensors[package().T["bv"]].offset
+    ck[at:at + 4] = np.frombuffer(np.float32(1e5).tobytes(), dtype=np.uint8)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=8)
+    eng = package().open_config(cfg, tensors, ck, cos, sin, max_block=8)
+    ref.run([1, 17, 3], 0, True)
+    eng.forwardMany([1, 17], 0)
+    eng.forward(3, 2, True)
+    assert same_bits(eng.logits(), ref.logits())
+    kv, (k, v) = eng.keysAndValues(0, 3), ref.kv(0, 3)
+    assert np.all(np.isposinf(kv["values"].reshape(v.shape)[0, :, 0]))
+    assert same_bits(kv["keys"], k.reshape(-1)) and same_bits(kv["values"], v.reshape(-1))
+    eng.release()
+
+
 @pytest.mark.parametrize("name", ["tiny_gqa", "stories15m"])
 def test_prompt_blocks_equal_one_at_a_time(name):
     cfg, tensors, ck, cos, sin, _ = build(name)
@@ -151,17 +170,20 @@ LONG = {
     # two chunks in registers
     "hs128_mul4": (dict(dim=512, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=1, head_size=128, vocab_size=320,
                         seq_len=3700, shared_classifier=1), 3600),
-    # eight query heads a kv head past 2048 positions: more exponentials than one block's LDS takes, so the decode
-    # steps run the separate softmax and weighted-value kernels
-    "mul8_past_lds": (dict(dim=256, hidden_dim=128, n_layers=1, n_heads=16, n_kv_heads=2, head_size=16,
-                           vocab_size=320, seq_len=2200, shared_classifier=1), 2100),
+    # eight query heads a kv head past 2048 positions, heads of 16 (a block takes 16 columns)
+    "mul8_hs16": (dict(dim=256, hidden_dim=128, n_layers=1, n_heads=16, n_kv_heads=2, head_size=16,
+                       vocab_size=320, seq_len=2200, shared_classifier=1), 2100),
 }
 
 
 @pytest.mark.parametrize("name", sorted(LONG))
 @pytest.mark.parametrize("half_kv", [0, 1])
-def test_long_decode_attention(name, half_kv):
-    """decode steps after a long prompt, every count % 4, against the oracle to the bit"""
+@pytest.mark.parametrize("attend", ["fused", "split"])
+def test_long_decode_attention(name, half_kv, attend, monkeypatch):
+    """decode steps after a long prompt, every count % 4, against the oracle to the bit: through the fused decode
+    kernel, and through the separate softmax and weighted-value kernels that contexts past its LDS take
+    (PYODIDE_LLM_HIP_ATTEND=split sends every decode step there)"""
+    monkeypatch.setenv("PYODIDE_LLM_HIP_ATTEND", attend)
     fields, prompt = LONG[name]
     cfg = ol.config(**{**fields, "half_kv": half_kv})
     tensors, size = ol.places(cfg)

@@ -93,5 +93,6 @@ def test_node_host_matches_the_oracle(name, tmp_path):
     assert out["sampled"] == expect
     assert out["released"] == [True, True]
     assert "context" in out["threw"]  # a position past seq_len throws, as forward.js does
+    assert out["short"] == ["TypeError"] * 4  # the addon refuses output arrays shorter than it writes
     assert out["header"] == list(ck[:28])
     assert out["memoryBytes"] > size

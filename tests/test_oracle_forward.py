@@ -85,3 +85,25 @@ def test_generate_is_greedy_over_forward():
         token = int(np.argmax(step.logits()))
         assert token == out[pos - len(prompt)]
     assert np.array_equal(step.logits(), last)
+
+
+def overflowing_value_bias(name="tiny_qwen_int6"):
+    """a float16-cache model whose layer-0 value bias of channel 0 is 1e5: that value rounds to infinity in the cache
+    (kernels/kernel.ts:570-599 to_f16 gives infinity from 65520 on)"""
+    from paths import package
+    cfg, tensors, ck, cos, sin = build(name, half_kv=1)
+    at = tensors[package().T["bv"]].offset
+    ck[at:at + 4] = np.frombuffer(np.float32(1e5).tobytes(), dtype=np.uint8)
+    return cfg, tensors, ck, cos, sin
+
+
+def test_keys_and_values_keep_an_infinite_half_infinite():
+    """public/forward.js:593-597 halfToFloat, which keysAndValues() reads a float16 cache with: a cached infinity
+    stays infinite (the kernels' half() reads it as 65536 inside attention; the logits stay finite)"""
+    cfg, tensors, ck, cos, sin = overflowing_value_bias()
+    model = ol.Model(cfg, tensors, ck, cos, sin, max_block=8)
+    model.run([1, 17, 3], 0, True)
+    keys, values = model.kv(0, 3)
+    assert np.all(np.isposinf(values[0, :, 0]))
+    assert np.all(np.isfinite(values[0, :, 1:])) and np.all(np.isfinite(values[1:])) and np.all(np.isfinite(keys))
+    assert np.all(np.isfinite(model.logits()))
