@@ -225,6 +225,16 @@ int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t coun
 int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
                   void *stream);
 
+/* No counterpart in the reference: hk_sample for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc). The same draw as hk_sample, token for token, with the
+ * sampler's scratch (n probabilities and n token indices, the token and the largest logit) in a static device array of
+ * the library, which every GPU it runs on holds until the process ends; n <= HK_SAMPLE_STATIC_MOST, else HE_E_ARG.
+ * It allocates nothing. Every call on one GPU uses that GPU's one array: calls that overlap on one GPU (two streams,
+ * two threads) race, and the caller must order them. Blocks until done. */
+#define HK_SAMPLE_STATIC_MOST 262144
+int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
+                         void *stream);
+
 /* The memory's read ceiling, kernels/ceilings.ts:9-25 read(p, bytes, passes) on the device: bytes (a multiple of 64)
  * at the device pointer p read passes times by a streaming kernel (one launch a pass). *checksum is read()'s: the
  * xor of the four lanes j of passes times the sum (mod 2^32) of the 32-bit words at p + 16k + 4j. *ms is the mean

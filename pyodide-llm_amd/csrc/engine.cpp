@@ -15,6 +15,7 @@
 #include <cstring>
 #include <functional>
 #include <limits>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1307,6 +1308,60 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
     if (p) (void)hipFree(p);
   if (rc) return rc;
   if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_sample: ") + hipGetErrorString(err));
+  return HE_OK;
+}
+
+}  // extern "C"
+
+// hk_sample_static's scratch: probabilities [HK_SAMPLE_STATIC_MOST] float32, token indices [HK_SAMPLE_STATIC_MOST]
+// int32, then the drawn token and the largest logit, 256 bytes apart (2 MiB and 512 bytes). Every GPU holds its own
+// copy at its own address, found once a device with hipGetSymbolAddress: in host code the array's name is a stand-in,
+// not a device address, and is never passed to a kernel or a copy.
+namespace ple {
+constexpr size_t SAMPLE_INDEX_AT = 4 * (size_t)HK_SAMPLE_STATIC_MOST, SAMPLE_TOKEN_AT = 8 * (size_t)HK_SAMPLE_STATIC_MOST;
+constexpr size_t SAMPLE_BEST_AT = SAMPLE_TOKEN_AT + 256, SAMPLE_SCRATCH_BYTES = SAMPLE_BEST_AT + 256;
+__device__ __align__(256) uint8_t scratch[SAMPLE_SCRATCH_BYTES];
+}  // namespace ple
+
+namespace {
+constexpr int MOST_DEVICES = 64;
+std::mutex g_scratch_lock;
+uint8_t *g_scratch[MOST_DEVICES] = {};
+
+// the current device's copy of `scratch`
+int32_t sample_scratch(uint8_t **out) {
+  int device = -1;
+  HIP_TRY(hipGetDevice(&device));
+  if (device < 0 || device >= MOST_DEVICES) return fail(HE_E_HIP, "hk_sample_static: a device index past 63");
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch[device]) {
+    void *p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(HE_E_HIP, "hk_sample_static: no address for the scratch array");
+    g_scratch[device] = reinterpret_cast<uint8_t *>(p);
+  }
+  *out = g_scratch[device];
+  return HE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
+                         void *stream) {
+  if (!logits || !token || n < 1 || !(temperature > 0.0f)) return fail(HE_E_ARG, "hk_sample_static: bad arguments");
+  if (n > HK_SAMPLE_STATIC_MOST)
+    return fail(HE_E_ARG, "hk_sample_static takes at most HK_SAMPLE_STATIC_MOST (262144) logits");
+  uint8_t *base = nullptr;
+  const int32_t rc = sample_scratch(&base);
+  if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int32_t *out = reinterpret_cast<int32_t *>(base + SAMPLE_TOKEN_AT);
+  HIP_TRY(launch_sample(reinterpret_cast<const float *>(logits), n, temperature, topp, random,
+                        reinterpret_cast<float *>(base), reinterpret_cast<int32_t *>(base + SAMPLE_INDEX_AT), out,
+                        reinterpret_cast<float *>(base + SAMPLE_BEST_AT), s));
+  HIP_TRY(hipMemcpyAsync(token, out, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
   return HE_OK;
 }
 
