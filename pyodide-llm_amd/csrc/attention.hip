@@ -568,6 +568,121 @@ __global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a
 }
 #undef ATT_FETCH
 
+// (B + C) for a few tokens (decode) whose output the caller quantizes itself: one block of 1024 threads a (token,
+// query head, 16 columns), thread b owning the four-position block b (positions 4b .. 4b+3) of the weighted values.
+// The head's tile maxima and scores are requested at once, the exponentials go into LDS by lane (four rows: positions
+// t % 4 == k), four lanes of wave 0 run the ordered sums; then every thread requests its block's 16 columns x 4
+// values, turns them into the columns' four-position products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), p = e * f32(1 /
+// sum), into LDS rows (one a column), and 16 lanes of wave 0 add their column's products in order, then the tail.
+// (The values are requested after the sums: requested at the start, their arrival slowed the scores' loads and
+// the exponential sum.) Blocks of the query heads that share a kv head's columns go to one XCD, as in attend_kernel.
+constexpr int A2_NT = 1024;  // threads a block
+constexpr int A2_AC = 16;    // columns a block
+constexpr int A2_SV = 4;     // scores a thread a pass (4096 positions)
+constexpr int A2_MOST = 2 * 4 * A2_NT;  // positions: two four-position blocks a thread at most
+
+// LDS bytes of attend2_kernel for the largest count of a launch: the exponentials' four rows, the tail, the columns'
+// rows of products
+size_t attend2_lds(int count) {
+  const int rs = chain_rowstride((count & ~3) >> 2);
+  return sizeof(float) * (size_t)((4 + A2_AC) * rs + 4);
+}
+
+template <int HS, bool HALF>
+__global__ __launch_bounds__(A2_NT) void attend2_kernel(const AttnArgs a) {
+  constexpr int NT = A2_NT, AC = A2_AC, S = HS / AC;
+  extern __shared__ float4 lds4[];
+  float *const lds = reinterpret_cast<float *>(lds4);
+  __shared__ float shared_mx, shared_inv;
+  const int mul = a.nh / a.nkv, groups = a.nkv * S;
+  const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3, hl = idx % mul, g = (idx / mul) * 8 + xcd;
+  if (g >= groups) return;  // the grid's rounding up: whole blocks leave
+  const int kh = g / S, j0 = (g % S) * AC, h = kh * mul + hl;
+  const int t = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int count = first_position(a) + t + 1, count4 = count & ~3, q4 = count4 >> 2, rs = chain_rowstride(q4);
+  float *const e4 = lds;             // [4][rs]
+  float *const tail = lds + 4 * rs;  // [4]
+  float *const blk = tail + 4;       // [AC][rs] (16-byte aligned: rs is a multiple of 16)
+  const float *sc = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
+  const int64_t vcol = (int64_t)(kh * HS + j0) * a.vstride;  // the block's first value column
+  const int tiles = (count + TILE - 1) / TILE;
+  const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
+  float tmr[2];
+  if (wave == 0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) tmr[u] = tm[min(lane + 64 * u, tiles - 1)];  // clamped: a repeat changes no max
+  }
+  float sv[A2_SV];
+#pragma unroll
+  for (int u = 0; u < A2_SV; ++u) sv[u] = sc[min(tid + NT * u, count - 1)];  // clamped, unconditional
+  float tv[3];  // wave 0, lane j < AC: column j's values past the fours (at most 3)
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+      tv[r] = cache1<HALF>(a.vcache, vcol + (int64_t)(lane % AC) * a.vstride + min(count4 + r, count - 1));
+  }
+  if (wave == 0) {
+    float mx = wmax(tmr[0], tmr[1]);
+    for (int i = lane + 128; i < tiles; i += 64) mx = wmax(mx, tm[i]);  // past 8192 positions
+    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) shared_mx = mx;
+  }
+  __syncthreads();
+  const float mx = shared_mx;
+  for (int base = 0; base < count; base += NT * A2_SV) {
+    if (base > 0) {
+#pragma unroll
+      for (int u = 0; u < A2_SV; ++u) sv[u] = sc[min(base + tid + NT * u, count - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < A2_SV; ++u) {
+      if (base + NT * u < count) {  // the block's test first (a scalar branch): no exponentials past the count
+        const int i = base + tid + NT * u;
+        if (i < count) {
+          const float d = sv[u] - mx;
+          if (i < count4) e4[(i & 3) * rs + (i >> 2)] = vexp(d);
+          else tail[i - count4] = fexp(d);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // lanes 0-3: lane k's sum; ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
+    const float part = lane < 4 ? lds_chain(e4 + lane * rs, q4, 0.0f) : 0.0f;
+    const float c1 = __shfl(part, 1, 64), c2 = __shfl(part, 2, 64), c3 = __shfl(part, 3, 64);
+    if (lane == 0) {
+      float sum = ((part + c1) + c2) + c3;
+      for (int r = 0; r < count - count4; ++r) sum = sum + tail[r];
+      shared_inv = 1.0f / sum;
+    }
+  }
+  __syncthreads();
+  const float inv = shared_inv;
+  for (int b0 = 0; b0 < q4; b0 += NT) {  // (a scalar loop: every thread takes the same passes)
+    const int b = b0 + tid, bc = min(b, q4 - 1);  // clamped: never stored past q4
+    float4 v[AC];
+#pragma unroll
+    for (int j = 0; j < AC; ++j) v[j] = cache4<HALF>(a.vcache, vcol + (int64_t)j * a.vstride + 4 * bc);
+    if (b < q4) {
+      const float p0 = e4[b] * inv, p1 = e4[rs + b] * inv, p2 = e4[2 * rs + b] * inv, p3 = e4[3 * rs + b] * inv;
+#pragma unroll
+      for (int j = 0; j < AC; ++j) {
+        const float4 x = v[j];
+        blk[j * rs + b] = (p0 * x.x + p1 * x.y) + (p2 * x.z + p3 * x.w);
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && lane < AC) {
+    float acc = lds_chain(blk + lane * rs, q4, 0.0f);
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+      if (r < count - count4) acc = acc + (tail[r] * inv) * tv[r];
+    a.out[(int64_t)t * a.out_stride + h * HS + j0 + lane] = acc;
+  }
+}
+
 // LDS bytes of softmax_kernel for a (token, head) of count positions: the exponentials as four ordered sums' rows and
 // the tail
 size_t softmax_lds(int count) { return sizeof(float) * (size_t)(4 * chain_rowstride((count & ~3) / 4) + 4); }
@@ -584,6 +699,13 @@ int attend_lds(const AttnArgs &a, int *nslot) {
   return head + n * slot;
 }
 
+// whether attend2_kernel takes a decode launch: head sizes of whole 16-column slices, a context that fits its LDS
+// and its two four-position blocks a thread
+bool attend2_takes(const AttnArgs &a) {
+  const int count = a.pos0 + a.m;
+  return a.hs % A2_AC == 0 && count <= A2_MOST && attend2_lds(count) <= (size_t)ALDS;
+}
+
 template <int HS, bool HALF>
 hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
@@ -592,6 +714,22 @@ hipError_t launch_hs(const AttnArgs &a, hipStream_t s) {
   } else {
     const int tt = std::max(1, scores_rows<HS>() / (a.nh / a.nkv));
     hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
+  }
+  if (a.m <= DECODE_TOKENS && !a.split && !a.xq && attend2_takes(a)) {
+    // the caller quantizes the output itself: blocks of 16 columns
+    const size_t lds = attend2_lds(a.pos0 + a.m);
+    if (lds > 64 * 1024) {
+      static bool sized = false;  // once a process: let the kernel take LDS past 64 KiB
+      if (!sized) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&attend2_kernel<HS, HALF>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, ALDS);
+        if (e != hipSuccess) return e;
+        sized = true;
+      }
+    }
+    const int groups = a.nkv * (HS / A2_AC), g8 = (groups + 7) & ~7;
+    hipLaunchKernelGGL((attend2_kernel<HS, HALF>), dim3(g8 * (a.nh / a.nkv), 1, a.m), dim3(A2_NT), lds, s, a);
+    return hipGetLastError();
   }
   int nslot = 0;
   const int fused = a.m <= DECODE_TOKENS && !a.split ? attend_lds<HS>(a, &nslot) : 0;

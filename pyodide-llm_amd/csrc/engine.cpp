@@ -464,7 +464,8 @@ struct F32Source {
 };
 
 hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq,
-                         const float *xs, const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr) {
+                         const float *xs, const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr,
+                         bool persistent = false) {
   const int32_t xq_stride = e->widest, xs_stride = e->widest / 32;
   const int32_t step = gemv_tokens(k, e->c.relaxed);
   if (step < 1) return hipErrorInvalidValue;
@@ -490,6 +491,7 @@ hipError_t matmul_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, 
       a.eps = e->c.rms_norm_eps;
     }
     if (qkv) a.qkv = *qkv;
+    a.persistent = persistent && a.m == 1 && decode_persistent(k, e->c.six != 0, e->c.relaxed != 0);
     hipError_t err = launch_gemv(a, e->c.six, e->c.relaxed, e->stream);
     if (err != hipSuccess) return err;
   }
@@ -519,12 +521,12 @@ hipError_t gemm_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, in
 }
 
 hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs,
-                  const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr) {
+                  const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr, bool persistent = false) {
   if (use_gemm(e, k, m))
     return timed(e, HE_K_GEMM, matmul_bytes(e, segs, nseg, k, m),
                  [&] { return gemm_launch(e, segs, nseg, k, m, xq, xs); });
   return timed(e, HE_K_GEMV, matmul_bytes(e, segs, nseg, k, m),
-               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, f32, qkv); });
+               [&] { return matmul_launch(e, segs, nseg, k, m, xq, xs, f32, qkv, persistent); });
 }
 
 // one token whose rows of k the decode GEMV quantizes itself: it saves a launch where the GEMV is about one block a
@@ -675,7 +677,11 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
     at.xs_stride = W / 32;
     at.bias = e->bias;
     at.split = e->attend_split;
-    const bool quantized = attention_quantizes(at);
+    // wo quantizes the attention's float32 output itself where its decode GEMV takes a float32 token (then the
+    // attention runs blocks of 16 columns); else the attention writes quantize_x of its output too where it can
+    const bool wo_quantizes = quantizes_itself(e, qdim, m, dim);
+    if (wo_quantizes) at.xq = nullptr;
+    const bool quantized = at.xq && attention_quantizes(at);
     if (!quantized) at.xq = nullptr;
     double kv_rows = 0;
     for (int32_t t = 0; t < m; ++t) kv_rows += pos0 + t + 1;
@@ -684,9 +690,10 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
                   [&] { return launch_attention(at, s); }));
     if (quantized) {
       HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs));
-    } else if (quantizes_itself(e, qdim, m, dim)) {
+    } else if (wo_quantizes) {
+      // the wide models' output projection on the persistent GEMV (each block quantizes the token once)
       const F32Source src{e->xb, nullptr};
-      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs, &src));
+      HIP_TRY(matmul(e, wo, 1, qdim, m, e->xq, e->xs, &src, nullptr, true));
     } else {
       HIP_TRY(timed(e, HE_K_NORM, (double)m * qdim * (4 + 1 + 0.125),
                     [&] { return launch_quantize(e->xq, e->xs, e->xb, m, qdim, e->xw, W, W / 32, e->bias, s); }));

@@ -243,28 +243,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 // launch of their own): with a.xnorm, rmsnorm first (kernels/kernel.ts:330-342: the squares in four lanes j % 4 added
 // in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
 // out = w * (s * x)), then quantize_x with bias 64 (kernels/kernel.ts:129-156) a half-wave a group, stored centred
-// (q - 64) into xl with the group scales into xsl. Every block computes the same bits. Thread tid takes positions
-// tid + 256 u (group tid / 32 + 8 u), requested by load_f32 before the rows. MAXU * 256 >= K; sq: 4 *
-// chain_rowstride(K / 4) floats of LDS.
-template <int MAXU>
+// (q - 64) into xl with the group scales into xsl. Every block computes the same bits. Thread tid of the block's NT
+// takes positions tid + NT u (group tid / 32 + NT / 32 u), requested by load_f32 before the rows. MAXU * NT >= K;
+// sq: 4 * chain_rowstride(K / 4) floats of LDS.
+// NORM (rmsnorm with a.xnorm) is a template argument: a load under a run-time test of the pointer is waited for
+// before the next is requested, which made the token's loads one round trip each.
+template <int MAXU, bool NORM, int NT = 256>
 __device__ __forceinline__ void load_f32(const MatArgs &a, float (&xv)[MAXU], float (&wv)[MAXU]) {
 #pragma unroll
   for (int u = 0; u < MAXU; ++u) {
-    const int j = min((int)threadIdx.x + 256 * u, a.k - 1);  // clamped: every load unconditional
+    const int j = min((int)threadIdx.x + NT * u, a.k - 1);  // clamped: every load unconditional
     xv[u] = a.xf[j];
-    wv[u] = a.xnorm ? a.xnorm[j] : 1.0f;
+    if constexpr (NORM) wv[u] = a.xnorm[j];
+    else wv[u] = 1.0f;
   }
 }
-template <int MAXU>
+template <int MAXU, bool NORM, int NT = 256>
 __device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&xv)[MAXU], const float (&wv)[MAXU],
                                                uint8_t *xl, float *xsl, float *sq) {
   __shared__ float part[4], sval;
   const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = chain_rowstride(q4);
   float sc = 1.0f;
-  if (a.xnorm) {
+  if constexpr (NORM) {
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
-      const int j = tid + 256 * u;
+      const int j = tid + NT * u;
       if (j < K) sq[(j & 3) * qs + (j >> 2)] = xv[u] * xv[u];
     }
     __syncthreads();
@@ -276,15 +279,14 @@ __device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&x
   }
   // every group's maximum, scale and values computed unconditionally (positions past K repeat the last one and are
   // not stored), so that the MAXU half-wave reductions overlap instead of running one after another
-  const bool norm = a.xnorm != nullptr;
   float o[MAXU], amax[MAXU];
 #pragma unroll
-  for (int u = 0; u < MAXU; ++u) o[u] = norm ? wv[u] * (sc * xv[u]) : xv[u];
+  for (int u = 0; u < MAXU; ++u) o[u] = NORM ? wv[u] * (sc * xv[u]) : xv[u];
 #pragma unroll
   for (int u = 0; u < MAXU; ++u) amax[u] = wave_max32(__builtin_fabsf(o[u]));
 #pragma unroll
   for (int u = 0; u < MAXU; ++u) {
-    const int j = tid + 256 * u;
+    const int j = tid + NT * u;
     const float scale = amax[u] / 63.0f;
     const float inv = scale > 0 ? 1.0f / scale : 0.0f;
     const uint8_t q = (uint8_t)(quant_value(o[u], inv, 64) - 64);
@@ -300,8 +302,10 @@ __device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&x
 // the loads next to their uses); meanwhile the block stages the token's activations, centred, and their scales in
 // LDS once. The R rows' products go to LDS and 4R lanes add them in the reference's order at once.
 // NS: wave steps (1 KiB of a row), NS * 1024 >= K.
-template <int R, int NS, bool F32>
+// SRC: 0 the activations from xq / xs; 1 the float32 token (a.xf); 2 a.xf after rmsnorm with a.xnorm
+template <int R, int NS, int SRC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv1_kernel(const MatArgs a) {
+  constexpr bool F32 = SRC != 0;
   constexpr int SV = (NS * 32 + 255) / 256;  // float4 of a row's scales a lane
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -326,7 +330,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   float fx[FU], fw[FU];
   if constexpr (F32) {
     static_assert(NS <= 4, "the float32 token is held a thread at a time");
-    load_f32<FU>(a, fx, fw);
+    load_f32<FU, SRC == 2>(a, fx, fw);
   } else {
 #pragma unroll
     for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
@@ -365,7 +369,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   __builtin_amdgcn_sched_barrier(0);
   // the block's activations into LDS: K / 16 uint4, centred (or made here from the float32 token)
   if constexpr (F32) {
-    stage_from_f32<FU>(a, fx, fw, reinterpret_cast<uint8_t *>(xl), xsl, P - wave * R * lay.stride);
+    stage_from_f32<FU, SRC == 2>(a, fx, fw, reinterpret_cast<uint8_t *>(xl), xsl, P - wave * R * lay.stride);
   } else {
 #pragma unroll
     for (int u = 0; u < XL; ++u) {
@@ -425,6 +429,205 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
   }
   store_row(a, row0 + lane, sum, lane < R && row0 + lane < a.total_rows);
+}
+
+// The persistent decode path (one token, int8, bias 64; a launch that asks for it: MatArgs.persistent): one block of
+// PW waves a CU, and wave w
+// of block b takes the row groups gw, gw + NWV, gw + 2 NWV, ... (gw = b PW + w, NWV = every wave of the grid) of R
+// consecutive rows, requesting a group's rows and scales, then adding them up, then the next group. The CU hides each
+// wave's load latency behind its other waves' groups. The block stages the token's activations in LDS once, while
+// every wave's first group is in flight: from xq / xs (centred), or (F32) from the float32 token, after rmsnorm where
+// a.xnorm is given, in the block itself (stage_from_f32), so that the norm's ordered sum runs once a CU while HBM
+// delivers the first rows, instead of in a launch of its own. Per row the arithmetic is gemv1_kernel's: exact group
+// sums by v_dot4, their float32 products into LDS, 4R lanes adding the reference's four chains in order, and
+// store_row (the residual add, or the q / k / v epilogue).
+template <int R, int NS>
+struct RowSet {
+  uint32_t w[R][NS][4];
+  float s[R][(NS * 32 + 255) / 256][4];
+};
+
+// the launch's segments as named scalars, read once: a segment picked among them by a wave-uniform row is a scalar
+// select (picked among the argument struct's array members, the compiler can turn it into an indexed copy in scratch)
+struct SegPick {
+  const uint8_t *w0, *w1, *w2;
+  const float *s0, *s1, *s2;
+  int32_t n0, n1, nseg;
+};
+__device__ __forceinline__ SegPick seg_pick(const MatArgs &a) {
+  return {a.seg[0].w, a.seg[1].w, a.seg[2].w, a.seg[0].ws, a.seg[1].ws, a.seg[2].ws, a.seg[0].rows, a.seg[1].rows,
+          a.nseg};
+}
+// the values and scales of row `row` (wave-uniform)
+__device__ __forceinline__ void pick_row(const SegPick &p, int row, int k, int g, const uint8_t **w, const float **ws) {
+  if (p.nseg > 2 && row >= p.n0 + p.n1) {
+    *w = p.w2 + (int64_t)(row - p.n0 - p.n1) * k;
+    *ws = p.s2 + (int64_t)(row - p.n0 - p.n1) * g;
+  } else if (p.nseg > 1 && row >= p.n0) {
+    *w = p.w1 + (int64_t)(row - p.n0) * k;
+    *ws = p.s1 + (int64_t)(row - p.n0) * g;
+  } else {
+    *w = p.w0 + (int64_t)row * k;
+    *ws = p.s0 + (int64_t)row * g;
+  }
+}
+
+// a group's rows and scales (every load unconditional, from clamped addresses); ALIGNED: every row's scales start on
+// 16 bytes, read as float4
+template <int R, int NS, bool ALIGNED>
+__device__ __forceinline__ void request_rows(RowSet<R, NS> &b, const SegPick &sp, int K, int total_rows, int group,
+                                             int ngroups, int lane) {
+  constexpr int SV = (NS * 32 + 255) / 256;
+  const int G = K / GS, G16 = (G + 3) & ~3, half = (lane & 1) * 16;
+  const int row0 = __builtin_amdgcn_readfirstlane(min(group, ngroups - 1) * R);
+  const uint8_t *wrows[R];
+  const float *srows[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) pick_row(sp, min(row0 + i, total_rows - 1), K, G, &wrows[i], &srows[i]);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const float *ws = srows[i];
+#pragma unroll
+    for (int u = 0; u < SV; ++u) {
+      const int f = min(4 * (lane + 64 * u), G16 - 4);
+      if constexpr (ALIGNED) {
+        const float4 v = *reinterpret_cast<const float4 *>(ws + f);
+        b.s[i][u][0] = v.x; b.s[i][u][1] = v.y; b.s[i][u][2] = v.z; b.s[i][u][3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b.s[i][u][e] = ws[min(f + e, G - 1)];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint8_t *wrow = wrows[i];
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const int g = min(u * 32 + (lane >> 1), G - 1);
+      const uint4 v = *reinterpret_cast<const uint4 *>(wrow + (int64_t)g * 32 + half);
+      b.w[i][u][0] = v.x; b.w[i][u][1] = v.y; b.w[i][u][2] = v.z; b.w[i][u][3] = v.w;
+    }
+  }
+}
+
+// one group's rows against the staged activations: the products into P, the four chains of each row, the store
+template <int R, int NS>
+__device__ __forceinline__ void finish_rows(const RowSet<R, NS> &b, const MatArgs &a, int group, const uint32_t *xl,
+                                            const float *xsl, float *wsl, float *P, int lane) {
+  constexpr int SV = (NS * 32 + 255) / 256;
+  const int K = a.k, G = K / GS, G4 = G & ~3, G16 = (G + 3) & ~3;
+  const int steps = (G + 31) / 32, half = (lane & 1) * 16;
+  const bool holder = (lane & 1) == 0;
+  const RowLayout lay = row_layout(K, true);
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int u = 0; u < SV; ++u) {
+      const int f = 4 * (lane + 64 * u);
+      if (f < G16)
+        *reinterpret_cast<float4 *>(wsl + i * G16 + f) = make_float4(b.s[i][u][0], b.s[i][u][1], b.s[i][u][2], b.s[i][u][3]);
+    }
+  wave_sync_lds();
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    if (u < steps) {
+      const int g = u * 32 + (lane >> 1);
+      const int gc = min(g, G - 1);
+      const uint4 x4 = reinterpret_cast<const uint4 *>(xl)[(gc * 32 + half) / 16];
+      const uint32_t xc[4] = {x4.x, x4.y, x4.z, x4.w};
+      const float xs_g = xsl[gc];
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        int32_t S = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) S = dot4(b.w[i][u][j], xc[j], S);
+        S += dpp_xor1(S);
+        if (holder && g < G) {
+          const float p = (float)S * (wsl[i * G16 + g] * xs_g);
+          float *pi = P + i * lay.stride;
+          if (g < G4) pi[(g & 3) * lay.q + (g >> 2)] = p;
+          else pi[4 * lay.q + (g - G4)] = p;
+        }
+      }
+    }
+  }
+  wave_sync_lds();
+  float chain = 0.0f;  // lane 4i + k: accumulator k of row row0 + i
+  if (lane < 4 * R) chain = lds_chain(P + (lane >> 2) * lay.stride + (lane & 3) * lay.q, G4 / 4, 0.0f);
+  const int src = (lane < R ? lane : 0) * 4;
+  const float c0 = __shfl(chain, src, 64), c1 = __shfl(chain, src + 1, 64);
+  const float c2 = __shfl(chain, src + 2, 64), c3 = __shfl(chain, src + 3, 64);
+  float sum = ((c0 + c1) + c2) + c3;
+  if (lane < R) {
+    const float *tl = P + lane * lay.stride + 4 * lay.q;
+    for (int g = G4; g < G; ++g) sum = sum + tl[g - G4];
+  }
+  const int row0 = __builtin_amdgcn_readfirstlane(group * R);
+  store_row(a, row0 + lane, sum, lane < R && row0 + lane < a.total_rows);
+  wave_sync_lds();  // the next group writes wsl and P again
+}
+
+// SRC: 0 the activations from xq / xs; 1 the float32 token (a.xf); 2 a.xf after rmsnorm with a.xnorm
+template <int PW, int R, int NS, int SRC, bool ALIGNED>
+__global__ __launch_bounds__(64 * PW) void gemvp_kernel(const MatArgs a) {
+  constexpr int PNT = 64 * PW;
+  constexpr bool F32 = SRC != 0;
+  extern __shared__ float smem[];
+  // the wave's index in a scalar register: every row index below is the wave's own, so segment picks stay scalar
+  // (an index the compiler takes for a lane's makes it copy the argument struct to scratch and index it there)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = a.k, G = K / GS, G16 = (G + 3) & ~3;
+  const RowLayout lay = row_layout(K, true);
+  uint32_t *xl = reinterpret_cast<uint32_t *>(smem);               // K bytes of centred activations
+  float *xsl = smem + K / 4;                                       // G scales of the activations
+  float *wsl = xsl + G16 + wave * R * G16;                         // this wave's rows' weight scales
+  float *P = xsl + G16 + PW * R * G16 + wave * R * lay.stride;     // this wave's products
+  float *sq = xsl + G16 + PW * R * G16 + PW * R * lay.stride;      // F32 with a norm: the squares' four rows
+  const int ngroups = (a.total_rows + R - 1) / R, nwv = gridDim.x * PW;
+  int group = blockIdx.x * PW + wave;
+  const SegPick sp = seg_pick(a);
+  RowSet<R, NS> rows;
+  // the token first (small; staged while the rows fly), then the first group's rows
+  constexpr int XL = (NS * 1024 / 16 + PNT - 1) / PNT;
+  constexpr int XSV = (NS * 32 + PNT - 1) / PNT;
+  constexpr int FU = F32 ? (NS * 1024 + PNT - 1) / PNT : 1;
+  uint4 xv[XL];
+  float sv[XSV];
+  float fx[FU], fw[FU];
+  if constexpr (F32) {
+    load_f32<FU, SRC == 2, PNT>(a, fx, fw);
+  } else {
+#pragma unroll
+    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + PNT * u, K / 16 - 1)];
+#pragma unroll
+    for (int u = 0; u < XSV; ++u) sv[u] = a.xs[min((int)threadIdx.x + PNT * u, G - 1)];
+  }
+  request_rows<R, NS, ALIGNED>(rows, sp, K, a.total_rows, group, ngroups, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (F32) {
+    stage_from_f32<FU, SRC == 2, PNT>(a, fx, fw, reinterpret_cast<uint8_t *>(xl), xsl, sq);
+  } else {
+#pragma unroll
+    for (int u = 0; u < XL; ++u) {
+      const int i = threadIdx.x + PNT * u;
+      if (i < K / 16)
+        reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
+                                                      centre4(xv[u].w));
+    }
+#pragma unroll
+    for (int u = 0; u < XSV; ++u) {
+      const int i = threadIdx.x + PNT * u;
+      if (i < G) xsl[i] = sv[u];
+    }
+  }
+  __syncthreads();
+  if (group >= ngroups) return;  // (after the block's barrier; no barrier follows)
+  finish_rows<R, NS>(rows, a, group, xl, xsl, wsl, P, lane);
+  for (group += nwv; group < ngroups; group += nwv) {
+    request_rows<R, NS, ALIGNED>(rows, sp, K, a.total_rows, group, ngroups, lane);
+    finish_rows<R, NS>(rows, a, group, xl, xsl, wsl, P, lane);
+  }
 }
 
 // The int6 decode path (one token, six.ts groups, bias 64: kernels/kernel_relaxed.ts:189-218 matmul_q6r): as
@@ -582,12 +785,86 @@ hipError_t launch_gemv1(const MatArgs &a, hipStream_t s) {
   const size_t lds = head + products;
   if constexpr (NS <= 4) {
     if (a.xf) {
-      hipLaunchKernelGGL((gemv1_kernel<R, NS, true>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+      if (a.xnorm) hipLaunchKernelGGL((gemv1_kernel<R, NS, 2>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+      else hipLaunchKernelGGL((gemv1_kernel<R, NS, 1>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((gemv1_kernel<R, NS, false>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+  hipLaunchKernelGGL((gemv1_kernel<R, NS, 0>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
   return hipGetLastError();
+}
+
+// the persistent grid: one block a CU (the device's count, asked once)
+int persistent_blocks() {
+  static int cus = 0;
+  if (!cus) {
+    int device = 0, n = 0;
+    if (hipGetDevice(&device) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+constexpr size_t PLDS = 160 * 1024 - 1024;  // LDS a persistent block may take (gfx950: 160 KiB a workgroup)
+
+// the LDS of a persistent block: the activations and their scales, every wave's rows' scales and products, the squares
+size_t gemvp_lds(int pw, int r, int k, bool norm) {
+  const size_t g16 = ((k / GS) + 3) & ~3;
+  size_t lds = (size_t)k + sizeof(float) * g16 * (1 + (size_t)pw * r) +
+               sizeof(float) * (size_t)pw * r * (size_t)row_layout(k, true).stride;
+  if (norm) lds += sizeof(float) * 4 * (size_t)chain_rowstride(k / 4);
+  return lds;
+}
+
+template <int PW, int R, int NS, int SRC, bool ALIGNED>
+hipError_t launch_gemvp_one(const MatArgs &a, int blocks, size_t lds, hipStream_t s) {
+  if (lds > 64 * 1024) {
+    static bool sized = false;  // once a process: let the kernel take LDS past 64 KiB
+    if (!sized) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemvp_kernel<PW, R, NS, SRC, ALIGNED>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)PLDS);
+      if (e != hipSuccess) return e;
+      sized = true;
+    }
+  }
+  hipLaunchKernelGGL((gemvp_kernel<PW, R, NS, SRC, ALIGNED>), dim3(blocks), dim3(64 * PW), lds, s, a);
+  return hipGetLastError();
+}
+
+// a persistent launch of PW waves a block and R rows a group over the device's CUs (one block a CU)
+template <int PW, int R, int NS>
+hipError_t launch_gemvp(const MatArgs &a, hipStream_t s, int blocks_a_cu = 1) {
+  const bool f32 = a.xf != nullptr;
+  if (f32 && (NS > 4 || a.k % 32)) return hipErrorInvalidValue;
+  const int G = a.k / GS, ngroups = (a.total_rows + R - 1) / R;
+  const int blocks = std::min((ngroups + PW - 1) / PW, blocks_a_cu * persistent_blocks());
+  const size_t lds = gemvp_lds(PW, R, a.k, f32 && a.xnorm);
+  if (lds > PLDS) return hipErrorInvalidValue;
+  // the rows' scales as float4 where every segment's start and row length keep them on 16 bytes
+  bool aligned = G % 4 == 0;
+  for (int i = 0; i < a.nseg; ++i) aligned = aligned && reinterpret_cast<uintptr_t>(a.seg[i].ws) % 16 == 0;
+  if constexpr (NS <= 4) {
+    if (f32 && a.xnorm)
+      return aligned ? launch_gemvp_one<PW, R, NS, 2, true>(a, blocks, lds, s)
+                     : launch_gemvp_one<PW, R, NS, 2, false>(a, blocks, lds, s);
+    if (f32)
+      return aligned ? launch_gemvp_one<PW, R, NS, 1, true>(a, blocks, lds, s)
+                     : launch_gemvp_one<PW, R, NS, 1, false>(a, blocks, lds, s);
+  }
+  return aligned ? launch_gemvp_one<PW, R, NS, 0, true>(a, blocks, lds, s)
+                 : launch_gemvp_one<PW, R, NS, 0, false>(a, blocks, lds, s);
+}
+
+// the persistent path (measured on the 8B shapes: 8 waves a block and 2 rows a group for rows of 2-4 KiB, the output
+// projection from the attention's float32 output 7.35 against 9.44 us for gemv1_kernel<4, 4>)
+hipError_t launch_persistent(const MatArgs &a, hipStream_t s) {
+  const int steps = (a.k / GS + 31) / 32;  // 1 KiB steps of a row
+  if (steps <= 2) return launch_gemvp<8, 2, 2>(a, s);
+  if (steps <= 4) return launch_gemvp<8, 2, 4>(a, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_decode(const MatArgs &a, hipStream_t s) {
@@ -642,6 +919,8 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
 
 bool decode_takes_f32(int32_t k, bool six, bool relaxed) { return !six && relaxed && k <= 4 * 1024 && k % 32 == 0; }
 
+bool decode_persistent(int32_t k, bool six, bool relaxed) { return !six && relaxed && k > 1024 && k <= 4 * 1024; }
+
 // the decode paths whose waves take rows in pairs: int8 rows up to 8 KiB, int6 rows up to 256 groups (even)
 bool decode_fuses_qkv(int32_t k, bool six, bool relaxed) {
   if (!relaxed) return false;
@@ -671,6 +950,8 @@ hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s) 
   const bool sums = a.sums != nullptr;
   if (a.xf && (sums || a.m != 1 || !decode_takes_f32(a.k, six, relaxed))) return hipErrorInvalidValue;
   if (a.qkv.on && (sums || a.m != 1 || !decode_fuses_qkv(a.k, six, relaxed))) return hipErrorInvalidValue;
+  if (a.persistent && (sums || a.m != 1 || !decode_persistent(a.k, six, relaxed))) return hipErrorInvalidValue;
+  if (a.persistent) return launch_persistent(a, s);
   if (!sums && !six && relaxed && a.m == 1 && a.k <= 20 * 1024) return launch_decode(a, s);
   if (!sums && six && relaxed && a.m == 1 && a.k <= 24 * 1024 && (a.k / GS) % 2 == 0) return launch_decode6(a, s);
   if (!sums && a.m > gemv_tokens(a.k, relaxed)) return hipErrorInvalidValue;

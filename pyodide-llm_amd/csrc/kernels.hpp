@@ -67,6 +67,9 @@ struct MatArgs {
   const float *xnorm;
   float eps;
   QkvFuse qkv;  // decode_fuses_qkv()
+  // one token, rows of 1-4 KiB (decode_persistent): the persistent GEMV, about one block a CU that loops over its
+  // rows (no L2Fetch fits it: its blocks take rows in another order)
+  int32_t persistent;
 };
 
 // rows a block of the one-token decode GEMV takes (launch_gemv with m = 1, bias 64, no sums) for rows of k, 0 where
@@ -80,6 +83,8 @@ constexpr int32_t GEMV_MOST = 8;
 hipError_t launch_gemv(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
 // whether a one-token launch_gemv of rows of k takes its activations as float32 (MatArgs.xf)
 bool decode_takes_f32(int32_t k, bool six, bool relaxed);
+// whether a one-token launch_gemv of rows of k may ask for the persistent path (MatArgs.persistent)
+bool decode_persistent(int32_t k, bool six, bool relaxed);
 // whether a one-token launch_gemv of rows of k finishes q / k / v itself (MatArgs.qkv)
 bool decode_fuses_qkv(int32_t k, bool six, bool relaxed);
 // the most tokens one launch_gemv takes for rows of k (its products of a row fit the block's LDS)
