@@ -2,20 +2,25 @@
 """The headline measurement: greedy decode of a Llama-3-8B-shaped int8 model at batch 1 on one MI355X, after a
 2048-token prompt prefill, through the engine's C ABI (include/pyodide_llm_hip.h).
 
-    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--model llama3-8b] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--model llama3-8b] [--only] [--no-cpu] [--no-node]
 
 A step is one decode token: the forward pass of the token fed at its position over the growing KV cache, the
 classifier, and the greedy choice on the device. Weights are synthetic (N(0, 0.02) by a counter-based generator made
 on the device, quantized by the reference's quantize() rules into the quantize.py layout); the prompt is random ids.
-Printed: one JSON line with decode tok/s as `value`, prefill tok/s, the decode GEMV's HBM GB/s against the 8 TB/s
-roofline (the algorithmic bytes of every matmul launch of one profiled decode step over their HIP-event-timed
-duration), and the oracle's decode rate on the host's cores as the CPU baseline.
+Printed: one JSON line with decode tok/s as `value`, the decode GEMV's HBM GB/s against the 8 TB/s roofline (the
+algorithmic bytes of every matmul launch of a decode step over their HIP-event-timed duration), the prompt's GEMM
+against the int8 MFMA peak and the ceilings measured in the same run (kernels/ceilings.ts on the device), the same
+decode timed through the JavaScript host (Node over forward_hip.mjs), the oracle's decode rate on the host's cores as
+the CPU baseline, and a record of each other model shape (150M, stories15M, Qwen2.5-7B int6) unless --only.
 """
 import argparse
 import ctypes
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -27,6 +32,7 @@ from paths import package  # noqa: E402
 
 METRIC = "decode tok/s + GEMV HBM GB/s (8B-shape int8, batch 1); prefill tok/s"
 HBM_PEAK_GBS = 8000.0
+I8_MFMA_PEAK_TOPS = 5000.0  # MI355X dense int8
 PROFILED_STEPS = 8
 # HBM bytes of one pass of the decode matmuls (every layer's, and the classifier's), from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE runs of this script, each counter scaled by what it reads on HIP's device-to-device copy of 1 GiB
@@ -54,6 +60,7 @@ MODELS = {
                                     half_kv=0, rms_norm_eps=1e-6),
                            theta=1000000.0, prompt=1024, decode=256),
 }
+OTHERS = ("llm150m", "stories15m", "qwen25-7b-int6")
 
 
 def hip_sync():
@@ -84,9 +91,8 @@ def copy_calibration(nbytes=1 << 30, reps=4):
 
 def read_ceiling(pk, nbytes=4 << 30, passes=4):
     """the HBM read bandwidth a plain streaming kernel reaches on this GPU (hk_read_ceiling, the device form of the
-    reference's kernels/ceilings.ts read()): 4 GiB (more than the 256 MB MALL holds) read 4 times after a memset,
-    GB/s of one pass. A practical figure, not a bound: the decode GEMV's access pattern reads its largest matrices a
-    little faster."""
+    reference's kernels/ceilings.ts read()): 4 GiB (more than the 256 MB MALL holds), the fastest of its launch shapes,
+    GB/s of one pass"""
     lib = ctypes.CDLL("libamdhip64.so")
     buf = ctypes.c_void_p()
     if lib.hipMalloc(ctypes.byref(buf), ctypes.c_size_t(nbytes)) != 0:
@@ -103,6 +109,23 @@ def read_ceiling(pk, nbytes=4 << 30, passes=4):
     return nbytes / (ms.value * 1e-3) / 1e9
 
 
+def valu_ceiling(pk, passes=65536):
+    """ceilings.ts fma(passes, 1, 0.9999, 1e-7) in every lane of a launch that fills the device: float32 multiply +
+    add pairs a second, each rounded (no FMA, no packed FP32)"""
+    result, ms, pairs = ctypes.c_float(0), ctypes.c_double(0), ctypes.c_double(0)
+    pk.hip_engine.check(pk.library().hk_valu_ceiling(passes, 1.0, 0.9999, 1e-7, ctypes.byref(result), ctypes.byref(ms),
+                                                     ctypes.byref(pairs), None))
+    return pairs.value / (ms.value * 1e-3), result.value
+
+
+def mfma_ceiling(pk, passes=16384):
+    """v_mfma_i32_32x32x32_i8 from registers in a launch that fills the device: int operations a second"""
+    checksum, ms, ops = ctypes.c_int32(0), ctypes.c_double(0), ctypes.c_double(0)
+    pk.hip_engine.check(pk.library().hk_mfma_ceiling(passes, 3, 5, 0x81, ctypes.byref(checksum), ctypes.byref(ms),
+                                                     ctypes.byref(ops), None))
+    return ops.value / (ms.value * 1e-3)
+
+
 def host_cpu():
     """the host's CPU model and the logical CPUs this process may run on"""
     model = "unknown"
@@ -117,15 +140,14 @@ def host_cpu():
     return {"model": model, "logical_cpus_available": len(os.sched_getaffinity(0))}
 
 
-def cpu_baseline(pk, spec, seconds=20.0):
+def cpu_baseline(pk, spec, prompt_len, tokens, seconds=15.0):
     """the oracle (oracle/liboracle.so, the reference's arithmetic restated in C) on the host's cores, on a bounded
-    sample of the same workload: the model's widths with 2 of its layers and its classifier, a few decode tokens,
-    scaled to all layers"""
+    sample of the same workload: the whole model (every layer, the classifier, the greedy choice) decoding the
+    measured run's tokens at its positions, from the prompt's end (the cache before it left at zero: attention reads
+    that many positions, the same arithmetic), until `tokens` steps or `seconds` have passed"""
     import oracle_lib as ol
     fields = dict(spec["cfg"])
-    layers = fields["n_layers"]
-    sample_layers = min(2, layers)
-    fields.update(n_layers=sample_layers, seq_len=64)
+    fields.update(seq_len=prompt_len + tokens + 1)
     cfg = pk.config(**fields)
     tensors, size = ol.places(cfg)
     made = time.perf_counter()
@@ -133,56 +155,68 @@ def cpu_baseline(pk, spec, seconds=20.0):
     cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, spec["theta"])
     model = ol.Model(cfg, tensors, ck, cos, sin, max_block=1)
     made = time.perf_counter() - made
-    t_layers, t_full, pos, token = [], [], 0, 1
+    pos, token, done = prompt_len, 1, 0
+    model.run([token], pos, True)  # the first step (page-ins) untimed
+    token, pos = int(np.argmax(model.logits())), pos + 1
     begin = time.perf_counter()
-    while pos < 48 and (time.perf_counter() - begin < seconds or pos < 4):
-        t0 = time.perf_counter()
-        model.run([token], pos, False)
-        t1 = time.perf_counter()
-        model.run([token], pos + 1, True)
-        t2 = time.perf_counter()
-        t_layers.append(t1 - t0)
-        t_full.append(t2 - t1)
+    while done < tokens and (time.perf_counter() - begin < seconds or done < 2):
+        model.run([token], pos, True)
         token = int(np.argmax(model.logits()))
-        pos += 2
-    tl, tf = float(np.median(t_layers)), float(np.median(t_full))
-    per_token = tl * layers / sample_layers + (tf - tl)
+        pos, done = pos + 1, done + 1
+    spent = time.perf_counter() - begin
     model.close()
-    return {"value": 1.0 / per_token, "unit": "tok/s", "cores": int(ol.load().or_get_threads()), "kind": "port",
-            "host": host_cpu(),
-            "sample": (f"oracle decode (C restatement of the reference's WASM path, OpenMP) at the model's widths with "
-                       f"{sample_layers} of {layers} layers and the classifier, {len(t_layers) * 2} tokens at positions "
-                       f"0-{pos - 1}; per-layer time scaled to {layers} layers; short context (the measured 8B run is "
-                       f"at positions past the prompt); checkpoint made in {made:.1f} s")}
+    del ck
+    return {"value": round(done / spent, 4), "unit": "tok/s", "cores": int(ol.load().or_get_threads()),
+            "kind": "port", "host": host_cpu(),
+            "sample": (f"oracle greedy decode (C restatement of the reference's WASM path, OpenMP) of the whole model "
+                       f"({cfg.n_layers} layers and the classifier), {done} tokens at positions {prompt_len + 1}-"
+                       f"{pos - 1} (a cache of zeros before them) in {spent:.1f} s; checkpoint made on the host in "
+                       f"{made:.1f} s")}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="decode steps timed (default: the model's 256/128)")
-    ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--model", default="llama3-8b", choices=sorted(MODELS))
-    ap.add_argument("--prompt", type=int, default=None)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the oracle's CPU baseline")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run 4 device copies of 1 GiB (the reference kernel for scaling HBM counters)")
-    args = ap.parse_args()
-    if args.copy_calibration:
-        copy_calibration()
-        return
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU: every box here has one, and this engine has no multi-GPU path "
-              f"(asked for --gpus {args.gpus})", file=sys.stderr)
-        sys.exit(2)
-    spec = MODELS[args.model]
-    steps = args.steps if args.steps is not None else spec["decode"]
-    prompt_len = args.prompt if args.prompt is not None else spec["prompt"]
-    pk = package()
+def layer_weights(cfg):
+    """the weights of one layer's matrices"""
+    q, kv = cfg.n_heads * cfg.head_size, cfg.n_kv_heads * cfg.head_size
+    return cfg.dim * (q + 2 * kv) + q * cfg.dim + 3 * cfg.dim * cfg.hidden_dim
+
+
+def node_decode(pk, name, spec, cfg, tensors, size, prompt, warmup, steps):
+    """the same decode through the JavaScript host: Node runs pyodide-llm_amd/decode_bench.mjs on an engine made from
+    the same seed, and its ids must equal this process's"""
+    from plans import plan_of
+    node = shutil.which("node")
+    addon = os.path.join(HERE, "pyodide-llm_amd", "hip_engine.node")
+    if node is None or not os.path.exists(addon):
+        return None
+    cos, sin = pk.rope_tables(cfg.seq_len, cfg.head_size, spec["theta"])
+    with tempfile.TemporaryDirectory() as tmp:
+        np.asarray(cos, np.float32).tofile(os.path.join(tmp, "cos.bin"))
+        np.asarray(sin, np.float32).tofile(os.path.join(tmp, "sin.bin"))
+        job = {"plan": plan_of(cfg, tensors), "size": int(size), "seed": 0, "prompt": prompt, "warmup": warmup,
+               "steps": steps, "promptBlock": len(prompt)}
+        with open(os.path.join(tmp, "job.json"), "w") as f:
+            json.dump(job, f)
+        print(f"node host: {name}", file=sys.stderr, flush=True)
+        proc = subprocess.run([node, os.path.join(HERE, "pyodide-llm_amd", "decode_bench.mjs"),
+                               os.path.join(tmp, "job.json")], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                              text=True, timeout=300)
+    if proc.returncode != 0:
+        raise RuntimeError("node decode failed:\n" + proc.stderr[-3000:])
+    return json.loads(proc.stdout.strip().splitlines()[-1])
+
+
+def measure(pk, name, steps=None, warmup=8, prompt_len=None, detail=False, cpu=True, node=False):
+    """one model shape: open (synthetic), prompt, timed greedy decode; the decode matmuls' GB/s; with detail the
+    per-kind profile of decode steps and of the prompt, each kind of matrix on its own, the Node host's run"""
+    spec = MODELS[name]
+    steps = steps if steps is not None else spec["decode"]
+    prompt_len = prompt_len if prompt_len is not None else spec["prompt"]
     cfg = pk.config(**spec["cfg"])
-    if prompt_len + args.warmup + steps + PROFILED_STEPS > cfg.seq_len:
+    if prompt_len + warmup + steps + PROFILED_STEPS > cfg.seq_len:
         raise SystemExit("the prompt and the steps do not fit the context")
     tensors, size = pk.places(cfg)
     cos, sin = pk.rope_tables(cfg.seq_len, cfg.head_size, spec["theta"])
+    print(f"model: {name}", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     eng = pk.open_synthetic(cfg, tensors, size, 0, cos, sin, max_block=prompt_len)
     setup_s = time.perf_counter() - t0
@@ -199,80 +233,189 @@ def main():
 
     token, pos = prompt[-1], prompt_len
     block = eng.tokenBlock
+    ids = []
 
     def decode(n):
         nonlocal token, pos
         done = 0
         while done < n:
-            ids = eng.generateMany(token, pos, [], 0, min(block, n - done), 0.0, 0.9, 1.0, [], [])
-            token, pos, done = ids[-1], pos + len(ids), done + len(ids)
+            got = eng.generateMany(token, pos, [], 0, min(block, n - done), 0.0, 0.9, 1.0, [], [])
+            ids.extend(got)
+            token, pos, done = got[-1], pos + len(got), done + len(got)
 
-    decode(args.warmup)
+    decode(warmup)
     hip_sync()
     t0 = time.perf_counter()
     decode(steps)
     hip_sync()
     decode_s = time.perf_counter() - t0
-    tok_s = steps / decode_s
+    rec = {"model": name, "dtype": "int6" if cfg.six else "int8", "kv_cache": "f16" if cfg.half_kv else "f32",
+           "prompt_tokens": prompt_len, "decode_tokens": steps, "warmup": warmup,
+           "tok_s": steps / decode_s, "ms_per_step": 1e3 * decode_s / steps, "prefill_tok_s": prompt_len / prefill_s,
+           "setup_s": setup_s}
 
-    # decode steps timed kernel by kind (a HIP event pair around every launch on the engine's stream), at the
-    # positions the run reached: the GEMV's achieved GB/s is the algorithmic bytes of its launches over their time
-    prof = {}
-    for i in range(PROFILED_STEPS):
-        for kind, (ms, nbytes, launches) in eng.profile(token, pos + i, True).items():
-            acc = prof.setdefault(kind, [0.0, 0.0, 0])
-            acc[0] += ms / PROFILED_STEPS
-            acc[1] += nbytes / PROFILED_STEPS
-            acc[2] += launches / PROFILED_STEPS
-    step_ms = sum(v[0] for v in prof.values())
     # the roofline's kernel: every decode matmul of a step (m = 1, the engine's weights, every layer, the classifier)
-    # back to back between one HIP event pair on the engine's stream, 4 passes; then each kind of matrix alone
+    # back to back between one HIP event pair on the engine's stream, 4 passes
     gemv_ms, gemv_bytes, gemv_launches = eng.profile_matmul("all", rounds=4)
-    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
-    by_matrix = {}
-    for which in ("qkv", "wo", "w13", "w2", "classifier"):
-        ms, nbytes, launches = eng.profile_matmul(which, rounds=2)
-        by_matrix[which] = {"us_per_launch": round(1e3 * ms / launches, 2), "bytes_per_launch": round(nbytes / launches),
-                            "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-    traffic = TRAFFIC.get(args.model)
+    rec["gemv"] = {"ms_per_pass": gemv_ms, "bytes_per_pass": gemv_bytes, "launches_per_pass": gemv_launches,
+                   "gb_s": gemv_bytes / (gemv_ms * 1e-3) / 1e9}
+    # the weights a decode step streams at the measured step rate
+    rec["effective_gb_s"] = gemv_bytes * rec["tok_s"] / 1e9
+    if detail:
+        # decode steps timed kernel by kind (a HIP event pair around every launch on the engine's stream), at the
+        # positions the run reached
+        prof = {}
+        for i in range(PROFILED_STEPS):
+            for kind, (ms, nbytes, launches) in eng.profile(token, pos + i, True).items():
+                acc = prof.setdefault(kind, [0.0, 0.0, 0])
+                acc[0] += ms / PROFILED_STEPS
+                acc[1] += nbytes / PROFILED_STEPS
+                acc[2] += launches / PROFILED_STEPS
+        rec["profile_ms"] = {k: round(v[0], 4) for k, v in prof.items()}
+        rec["profiled_step_ms"] = round(sum(v[0] for v in prof.values()), 4)
+        by_matrix = {}
+        for which in ("qkv", "wo", "w13", "w2", "classifier"):
+            ms, nbytes, launches = eng.profile_matmul(which, rounds=2)
+            by_matrix[which] = {"us_per_launch": round(1e3 * ms / launches, 2),
+                                "bytes_per_launch": round(nbytes / launches),
+                                "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        rec["gemv_by_matrix"] = by_matrix
+        # the prompt again (the same tokens at the same positions: the cache gets the same bits), every launch timed
+        pprof = eng.profileMany(fed, 0)
+        rec["prefill_profile_ms"] = {k: round(v[0], 3) for k, v in pprof.items()}
+        rec["prefill_gemm"] = {"ms": pprof["gemm"][0], "launches": pprof["gemm"][2],
+                               "int_ops": 2.0 * prompt_len * cfg.n_layers * layer_weights(cfg)}
     eng.release()
-    ceiling_gbs = read_ceiling(pk)
+    if node:
+        got = node_decode(pk, name, spec, cfg, tensors, size, prompt, warmup, steps)
+        if got is not None:
+            rec["node_host"] = {"tok_s": round(got["decode_tok_s"], 3), "ms_per_step": round(got["ms_per_step"], 4),
+                                "prefill_tok_s": round(got["prefill_tok_s"], 2),
+                                "ids_equal": got["ids"] == [int(t) for t in ids]}
+    if cpu:
+        rec["cpu_baseline"] = cpu_baseline(pk, spec, prompt_len, steps, seconds=15.0 if detail else 10.0)
+    return rec
 
-    cpu = None if args.no_cpu else cpu_baseline(pk, spec)
+
+def brief(rec):
+    """the record of another model shape in the JSON line"""
+    out = {"value": round(rec["tok_s"], 3), "unit": "tok/s", "dtype": rec["dtype"], "kv_cache": rec["kv_cache"],
+           "workload": f"{rec['model']}-shape {rec['dtype']} greedy decode at batch 1 after a "
+                       f"{rec['prompt_tokens']}-token prefill",
+           "decode_tokens": rec["decode_tokens"], "ms_per_step": round(rec["ms_per_step"], 4),
+           "prefill_tok_s": round(rec["prefill_tok_s"], 2),
+           "gemv_gb_s": round(rec["gemv"]["gb_s"], 1),
+           "effective_gb_s": round(rec["effective_gb_s"], 1),
+           "weights_bytes_per_step": round(rec["gemv"]["bytes_per_pass"])}
+    if rec["dtype"] == "int6":
+        # the fused 6-bit loader: 0.75 B a weight and 4 B of scale a group of 32, 0.875 B a weight
+        out["roofline"] = {"bound": "hbm", "achieved": round(rec["gemv"]["gb_s"], 1), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(rec["gemv"]["gb_s"] / HBM_PEAK_GBS, 4),
+                           "kernel": "decode GEMV on int6 rows (every matmul of a decode step, m = 1, back to back)",
+                           "bytes_per_weight": 0.875}
+    else:
+        out["note"] = ("the weights fit the 256 MB MALL: effective_gb_s is the step's matmul bytes at the decode rate "
+                       "(cache-resident, not an HBM figure)")
+    if "cpu_baseline" in rec:
+        out["cpu_baseline"] = rec["cpu_baseline"]
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="decode steps timed (default: the model's 256/128)")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--model", default="llama3-8b", choices=sorted(MODELS))
+    ap.add_argument("--prompt", type=int, default=None)
+    ap.add_argument("--only", action="store_true", help="only the named model (no records of the other shapes)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the oracle's CPU baselines")
+    ap.add_argument("--no-node", action="store_true", help="skip the decode through the JavaScript host")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 4 device copies of 1 GiB (the reference kernel for scaling HBM counters)")
+    args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: every box here has one, and this engine has no multi-GPU path "
+              f"(asked for --gpus {args.gpus})", file=sys.stderr)
+        sys.exit(2)
+    pk = package()
+    rec = measure(pk, args.model, args.steps, args.warmup, args.prompt, detail=True, cpu=not args.no_cpu,
+                  node=not args.no_node)
+    print("ceilings", file=sys.stderr, flush=True)
+    ceiling_gbs = read_ceiling(pk)
+    pairs_s, _ = valu_ceiling(pk)
+    mfma_ops_s = mfma_ceiling(pk)
+    others = {}
+    if not args.only:
+        for name in OTHERS:
+            if name != args.model:
+                others[name] = brief(measure(pk, name, warmup=args.warmup, cpu=not args.no_cpu))
+
+    gemv = rec["gemv"]
+    gemv_gbs = gemv["gb_s"]
+    traffic = TRAFFIC.get(args.model)
+    gemm = rec["prefill_gemm"]
+    gemm_tops = gemm["int_ops"] / (gemm["ms"] * 1e-3) / 1e12
+    # the exact order's float32 work after each int32 group sum: 4 VALU operations (the scale product, the
+    # conversion, the multiply, the add to the chain) for the group's 32 multiply-adds (64 int operations) of a
+    # (row, token): at the measured multiply + add rate (2 operations a pair), 16 int operations an operation
+    valu_ops_s = 2.0 * pairs_s
+    exact_cap_tops = valu_ops_s * 16 / 1e12
+    cfg_name = args.model
     out = {
         "metric": METRIC,
-        "value": round(tok_s, 3),
+        "value": round(rec["tok_s"], 3),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": rec["decode_tokens"],
         "warmup": args.warmup,
-        "ms_per_step": round(1e3 * decode_s / steps, 4),
+        "ms_per_step": round(rec["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int6" if cfg.six else "int8",
+        "dtype": rec["dtype"],
         "data": "synthetic (random-init weights N(0,0.02) quantized by the reference's rules; random prompt ids)",
-        "config": {"workload": f"{args.model}-shape {'int6' if cfg.six else 'int8'} greedy decode at batch 1 after a "
-                               f"{prompt_len}-token prefill",
-                   "model": args.model, "prompt_tokens": prompt_len, "decode_tokens": steps,
-                   "kv_cache": "f16" if cfg.half_kv else "f32", "order": "exact (the reference's float32 order)"},
-        "prefill_tok_s": round(prompt_len / prefill_s, 2),
+        "config": {"workload": f"{cfg_name}-shape {rec['dtype']} greedy decode at batch 1 after a "
+                               f"{rec['prompt_tokens']}-token prefill",
+                   "model": cfg_name, "prompt_tokens": rec["prompt_tokens"], "decode_tokens": rec["decode_tokens"],
+                   "kv_cache": rec["kv_cache"], "order": "exact (the reference's float32 order)"},
+        "prefill_tok_s": round(rec["prefill_tok_s"], 2),
         "gemv_hbm_gb_s": round(gemv_gbs, 1),
+        "effective_gb_s": round(rec["effective_gb_s"], 1),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": round(traffic["bytes_per_pass"] / gemv_launches) if traffic else None,
-                     "kernel": "decode GEMV (gemv1_kernel: every matmul of a decode step, m = 1, back to back)",
-                     "launches_per_pass": int(gemv_launches),
-                     "algorithmic_bytes_per_launch": round(gemv_bytes / gemv_launches),
-                     "us_per_launch": round(1e3 * gemv_ms / gemv_launches, 3),
+                     "traffic": round(traffic["bytes_per_pass"] / gemv["launches_per_pass"]) if traffic else None,
+                     "kernel": "decode GEMV (every matmul of a decode step, m = 1, back to back)",
+                     "launches_per_pass": int(gemv["launches_per_pass"]),
+                     "algorithmic_bytes_per_launch": round(gemv["bytes_per_pass"] / gemv["launches_per_pass"]),
+                     "us_per_launch": round(1e3 * gemv["ms_per_pass"] / gemv["launches_per_pass"], 3),
                      "traffic_source": traffic["source"] if traffic else None,
                      "read_ceiling_gb_s": round(ceiling_gbs, 1),
                      "frac_of_read_ceiling": round(gemv_gbs / ceiling_gbs, 4)},
-        "gemv_by_matrix": by_matrix,
-        "profile_ms": {k: round(v[0], 4) for k, v in prof.items()},
-        "profiled_step_ms": round(step_ms, 4),
-        "setup_s": round(setup_s, 2),
-        "cpu_baseline": cpu,
+        "prefill_roofline": {"bound": "mfma", "kernel": "prompt GEMM (gemm_kernel, every matmul of the prompt)",
+                             "achieved": round(gemm_tops, 1), "peak": I8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                             "frac": round(gemm_tops / I8_MFMA_PEAK_TOPS, 4),
+                             "gemm_ms": round(gemm["ms"], 3), "int_ops": gemm["int_ops"],
+                             "mfma_ceiling_top_s": round(mfma_ops_s / 1e12, 1),
+                             "frac_of_mfma_ceiling": round(gemm_tops * 1e12 / mfma_ops_s, 4),
+                             "exact_order_cap_top_s": round(exact_cap_tops, 1),
+                             "frac_of_exact_order_cap": round(gemm_tops / exact_cap_tops, 4)},
+        "ceilings": {"read_gb_s": round(ceiling_gbs, 1),
+                     "valu_mul_add_pairs_t_s": round(pairs_s / 1e12, 3),
+                     "valu_f32_ops_t_s": round(valu_ops_s / 1e12, 2),
+                     "mfma_i8_top_s": round(mfma_ops_s / 1e12, 1),
+                     "source": "hk_read_ceiling, hk_valu_ceiling, hk_mfma_ceiling (kernels/ceilings.ts on the device)"},
+        "gemv_by_matrix": rec["gemv_by_matrix"],
+        "profile_ms": rec["profile_ms"],
+        "profiled_step_ms": rec["profiled_step_ms"],
+        "prefill_profile_ms": rec["prefill_profile_ms"],
+        "setup_s": round(rec["setup_s"], 2),
+        "node_host": rec.get("node_host"),
+        "cpu_baseline": rec.get("cpu_baseline"),
+        "other_shapes": others,
     }
     print(json.dumps(out))
 

@@ -185,6 +185,11 @@ enum {
 int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, double *ms, double *bytes,
                            int32_t *launches);
 
+/* he_profile_forward for a prompt chunk: he_forward_many(tokens, count, pos) (count <= the engine's promptBlock)
+ * with every launch timed and summed by kind the same way. */
+int32_t he_profile_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos, double *ms,
+                                double *bytes, int32_t *launches);
+
 /* The decode matmuls (one token, m = 1) of the engine's own weights timed on their own, the counterpart of the
  * reference's matmul timing over its weights (tests/q8r-bench.mjs:115-135): `which` -1 runs every matmul of a decode
  * step in the step's order (q/k/v, wo, w1/w3, w2 of each layer, then the classifier), 0..4 only q/k/v, wo, w1/w3, w2
@@ -236,10 +241,32 @@ int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float
                          void *stream);
 
 /* The memory's read ceiling, kernels/ceilings.ts:9-25 read(p, bytes, passes) on the device: bytes (a multiple of 64)
- * at the device pointer p read passes times by a streaming kernel (one launch a pass). *checksum is read()'s: the
- * xor of the four lanes j of passes times the sum (mod 2^32) of the 32-bit words at p + 16k + 4j. *ms is the mean
- * time of a pass (HIP events on the stream). Blocks until done. */
+ * at the device pointer p read by a streaming kernel in each of a few launch shapes (8 to 16 loads of 16 bytes a lane
+ * in flight, 256 to 2048 blocks), one untimed pass then passes timed ones a shape. *checksum is read()'s: the xor of
+ * the four lanes j of passes times the sum (mod 2^32) of the 32-bit words at p + 16k + 4j (every shape's must agree,
+ * else HE_E_HIP). *ms is the fastest shape's mean time of a pass (HIP events on the stream). Blocks until done. */
 int32_t hk_read_ceiling(const void *p, int64_t bytes, int32_t passes, int32_t *checksum, double *ms, void *stream);
+
+/* The float32 multiply-add ceiling, kernels/ceilings.ts:27-50 fma(passes, w, x0, step) in every lane of a launch
+ * that fills the device (8192 waves of 64): eight accumulators (starting at 0..7), a pass adds w_j * x and w_j * y
+ * (w_j = w + {0, 2^-10, 2^-9, 3 * 2^-10}; x from x0, y from x0 + 0.25, both moving by -step a pass) to them, each
+ * product and sum rounded on its own (no FMA, no packed FP32: the form of every step of the exact order). *result is
+ * one lane's ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)), which every wave must agree on (else HE_E_HIP); fma()
+ * returns the sum of its four equal lanes of it. *ms is the mean time of a launch (three after one untimed), *pairs
+ * the multiply + add pairs a launch makes (8 a pass a lane). Blocks until done. */
+int32_t hk_valu_ceiling(int32_t passes, float w, float x0, float step, float *result, double *ms, double *pairs,
+                        void *stream);
+
+/* The int8 matrix-core ceiling, kernels/ceilings_relaxed.ts:33-50 dotRegisters(passes, first, times, step) on the
+ * instruction the prompt GEMM takes (v_mfma_i32_32x32x32_i8), from registers only, in 4096 waves: four 32 x 32 int32
+ * accumulators a wave, accumulator n starting at 1000 n + e in element e of every lane; a pass one product into each
+ * with every byte of A = first (xor flip after every pass, in place of dotRegisters' moving step) and every byte of
+ * B = times. *checksum is a wave's sum (mod 2^32) of the elements of its four accumulators in its 64 lanes, which every
+ * wave must agree on (else HE_E_HIP): 4 * 64 * 16 * (mean start) + 4 * 1024 * 32 * times * (the sum of A's byte over
+ * the passes) as int8 arithmetic mod 2^32. *ms is the mean time of a launch (three after one untimed), *ops its
+ * integer operations (a multiply and an add for each of the 32768 products of every MFMA). Blocks until done. */
+int32_t hk_mfma_ceiling(int32_t passes, int32_t first, int32_t times, int32_t flip, int32_t *checksum, double *ms,
+                        double *ops, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1021,9 +1021,11 @@ int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, const int32_t
   return HE_OK;
 }
 
-int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, double *ms, double *bytes,
-                           int32_t *launches) {
-  if (!e || !ms || !bytes || !launches) return fail(HE_E_ARG, "a required pointer is null");
+namespace {
+// run_tokens with a HIP event pair around every launch, summed by kind; the greedy choice timed too where logits are
+int32_t profile_tokens(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos, bool need_logits, double *ms,
+                       double *bytes, int32_t *launches) {
+  if (!e || !tokens || !ms || !bytes || !launches) return fail(HE_E_ARG, "a required pointer is null");
   for (int k = 0; k < HE_K_COUNT; ++k) {
     ms[k] = 0;
     bytes[k] = 0;
@@ -1032,7 +1034,7 @@ int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t nee
   HIP_TRY(hipStreamSynchronize(e->stream));
   e->profiling = true;
   e->marks.clear();
-  int32_t rc = run_tokens(e, &token, 1, pos, need_logits != 0);
+  int32_t rc = run_tokens(e, tokens, count, pos, need_logits);
   if (rc == HE_OK && need_logits)
     rc = timed(e, HE_K_ARGMAX, (double)e->c.vocab_size * 4, [&] {
            return launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream);
@@ -1053,6 +1055,18 @@ int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t nee
   if (err != hipSuccess) return fail(HE_E_HIP, std::string("profile: ") + hipGetErrorString(err));
   return HE_OK;
 }
+}  // namespace
+
+int32_t he_profile_forward(he_engine *e, int32_t token, int32_t pos, int32_t need_logits, double *ms, double *bytes,
+                           int32_t *launches) {
+  return profile_tokens(e, &token, 1, pos, need_logits != 0, ms, bytes, launches);
+}
+
+int32_t he_profile_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int32_t pos, double *ms,
+                                double *bytes, int32_t *launches) {
+  if (e && count > e->max_block) return fail(HE_E_ARG, "more tokens than the prompt block");
+  return profile_tokens(e, tokens, count, pos, false, ms, bytes, launches);
+}
 
 int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *ms, double *bytes, int32_t *launches) {
   if (!e || !ms || !bytes || !launches) return fail(HE_E_ARG, "a required pointer is null");
@@ -1068,6 +1082,7 @@ int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *m
     MatSeg seg[3];
     int nseg;
     int32_t k;
+    bool persistent;  // the output projection: as the step launches it
   };
   std::vector<Launch> seq;
   for (int32_t l = 0; l < c.n_layers; ++l) {
@@ -1075,20 +1090,20 @@ int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *m
       seq.push_back({{{e->mat(HE_T_WQ, l), e->mat_scales(HE_T_WQ, l), out, qdim, qdim, 0},
                       {e->mat(HE_T_WK, l), e->mat_scales(HE_T_WK, l), out + qdim, kvdim, kvdim, 0},
                       {e->mat(HE_T_WV, l), e->mat_scales(HE_T_WV, l), out + qdim + kvdim, kvdim, kvdim, 0}},
-                     3, dim});
+                     3, dim, false});
     if (which == -1 || which == 1)
-      seq.push_back({{{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), out, dim, dim, 1}}, 1, qdim});
+      seq.push_back({{{e->mat(HE_T_WO, l), e->mat_scales(HE_T_WO, l), out, dim, dim, 1}}, 1, qdim, true});
     if ((which == -1 || which == 2) && present(c, HE_T_W3))
       seq.push_back({{{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), out, hidden, hidden, 0},
                       {e->mat(HE_T_W3, l), e->mat_scales(HE_T_W3, l), out + hidden, hidden, hidden, 0}},
-                     2, dim});
+                     2, dim, false});
     else if (which == -1 || which == 2)
-      seq.push_back({{{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), out, hidden, hidden, 0}}, 1, dim});
+      seq.push_back({{{e->mat(HE_T_W1, l), e->mat_scales(HE_T_W1, l), out, hidden, hidden, 0}}, 1, dim, false});
     if (which == -1 || which == 3)
-      seq.push_back({{{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), out, dim, dim, 1}}, 1, hidden});
+      seq.push_back({{{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), out, dim, dim, 1}}, 1, hidden, false});
   }
   if (which == -1 || which == 4)
-    seq.push_back({{{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), out, c.vocab_size, 0, 0}}, 1, dim});
+    seq.push_back({{{e->mat(HE_T_WCLS, 0), e->mat_scales(HE_T_WCLS, 0), out, c.vocab_size, 0, 0}}, 1, dim, false});
   double pass_bytes = 0;
   for (const Launch &l : seq) pass_bytes += matmul_bytes(e, l.seg, l.nseg, l.k, 1);
   hipEvent_t a = nullptr, b = nullptr;
@@ -1098,7 +1113,7 @@ int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *m
   if (err == hipSuccess) err = hipEventRecord(a, e->stream);
   for (int32_t r = 0; r < rounds && err == hipSuccess; ++r)
     for (const Launch &l : seq) {
-      err = matmul_launch(e, l.seg, l.nseg, l.k, 1, e->xq, e->xs);
+      err = matmul_launch(e, l.seg, l.nseg, l.k, 1, e->xq, e->xs, nullptr, nullptr, l.persistent);
       if (err != hipSuccess) break;
     }
   if (err == hipSuccess) err = hipEventRecord(b, e->stream);
@@ -1350,6 +1365,35 @@ int32_t sample_scratch(uint8_t **out) {
   *out = g_scratch[device];
   return HE_OK;
 }
+
+// the mean time of three launches of one ceiling loop between an event pair (after one untimed launch), and the
+// output words (one a wave) of the last
+template <class T, class F>
+int32_t time_ceiling(const char *what, int32_t waves, hipStream_t s, std::vector<T> &host, double *ms, F &&launch) {
+  T *out = nullptr;
+  int32_t rc = dev_alloc(&out, sizeof(T) * waves);
+  if (rc) return rc;
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t err = hipEventCreate(&a);
+  if (err == hipSuccess) err = hipEventCreate(&b);
+  if (err == hipSuccess) err = launch(out);
+  if (err == hipSuccess) err = hipEventRecord(a, s);
+  const int reps = 3;
+  for (int r = 0; r < reps && err == hipSuccess; ++r) err = launch(out);
+  if (err == hipSuccess) err = hipEventRecord(b, s);
+  if (err == hipSuccess) err = hipEventSynchronize(b);
+  float t = 0;
+  if (err == hipSuccess) err = hipEventElapsedTime(&t, a, b);
+  host.assign(waves, T{});
+  if (err == hipSuccess) err = hipMemcpy(host.data(), out, sizeof(T) * waves, hipMemcpyDeviceToHost);
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  (void)hipFree(out);
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string(what) + ": " + hipGetErrorString(err));
+  *ms = (double)t / reps;
+  return HE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1376,32 +1420,85 @@ int32_t hk_read_ceiling(const void *p, int64_t bytes, int32_t passes, int32_t *c
   if (!p || !checksum || !ms || bytes < 64 || bytes % 64 || passes < 1)
     return fail(HE_E_ARG, "hk_read_ceiling: bad arguments");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int32_t blocks = read_ceiling_blocks(bytes);
+  int32_t most = 1;
+  for (int32_t i = 0; i < read_ceiling_shapes(); ++i) most = std::max(most, read_ceiling_blocks(bytes, i));
   uint32_t *partial = nullptr;
-  int32_t rc = dev_alloc(&partial, sizeof(uint32_t) * 4 * blocks);
+  int32_t rc = dev_alloc(&partial, sizeof(uint32_t) * 4 * most);
   if (rc) return rc;
   hipEvent_t a = nullptr, b = nullptr;
   hipError_t err = hipEventCreate(&a);
   if (err == hipSuccess) err = hipEventCreate(&b);
-  if (err == hipSuccess) err = hipEventRecord(a, s);
-  for (int32_t r = 0; r < passes && err == hipSuccess; ++r) err = launch_read_ceiling(p, bytes, partial, s);
-  if (err == hipSuccess) err = hipEventRecord(b, s);
-  if (err == hipSuccess) err = hipEventSynchronize(b);
-  float t = 0;
-  if (err == hipSuccess) err = hipEventElapsedTime(&t, a, b);
-  std::vector<uint32_t> h(4 * (size_t)blocks);
-  if (err == hipSuccess) err = hipMemcpy(h.data(), partial, sizeof(uint32_t) * h.size(), hipMemcpyDeviceToHost);
+  std::vector<uint32_t> h(4 * (size_t)most);
+  double best = 0;
+  int64_t sum = -1;
+  bool agree = true;
+  // each launch shape: one untimed pass, then `passes` between an event pair; the fastest shape's mean pass
+  for (int32_t shape = 0; shape < read_ceiling_shapes() && err == hipSuccess; ++shape) {
+    err = launch_read_ceiling(p, bytes, shape, partial, s);
+    if (err == hipSuccess) err = hipEventRecord(a, s);
+    for (int32_t r = 0; r < passes && err == hipSuccess; ++r) err = launch_read_ceiling(p, bytes, shape, partial, s);
+    if (err == hipSuccess) err = hipEventRecord(b, s);
+    if (err == hipSuccess) err = hipEventSynchronize(b);
+    float t = 0;
+    if (err == hipSuccess) err = hipEventElapsedTime(&t, a, b);
+    const int32_t blocks = read_ceiling_blocks(bytes, shape);
+    if (err == hipSuccess)
+      err = hipMemcpy(h.data(), partial, sizeof(uint32_t) * 4 * blocks, hipMemcpyDeviceToHost);
+    if (err != hipSuccess) break;
+    // every pass reads the same words: passes times one pass's lane sums (mod 2^32)
+    uint32_t lane[4] = {0, 0, 0, 0};
+    for (int32_t i = 0; i < blocks; ++i)
+      for (int j = 0; j < 4; ++j) lane[j] += h[4 * (size_t)i + j];
+    for (int j = 0; j < 4; ++j) lane[j] *= (uint32_t)passes;
+    const int64_t x = (int64_t)(lane[0] ^ lane[1] ^ lane[2] ^ lane[3]);
+    if (sum >= 0 && x != sum) agree = false;
+    sum = x;
+    const double pass_ms = (double)t / passes;
+    if (best == 0 || pass_ms < best) best = pass_ms;
+  }
   if (a) (void)hipEventDestroy(a);
   if (b) (void)hipEventDestroy(b);
   (void)hipFree(partial);
   if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_read_ceiling: ") + hipGetErrorString(err));
-  // every pass reads the same words: passes times one pass's lane sums (mod 2^32)
-  uint32_t lane[4] = {0, 0, 0, 0};
-  for (int32_t i = 0; i < blocks; ++i)
-    for (int j = 0; j < 4; ++j) lane[j] += h[4 * (size_t)i + j];
-  for (int j = 0; j < 4; ++j) lane[j] *= (uint32_t)passes;
-  *checksum = (int32_t)(lane[0] ^ lane[1] ^ lane[2] ^ lane[3]);
-  *ms = (double)t / passes;
+  if (!agree) return fail(HE_E_HIP, "hk_read_ceiling: the launch shapes' checksums differ");
+  *checksum = (int32_t)(uint32_t)sum;
+  *ms = best;
+  return HE_OK;
+}
+
+int32_t hk_valu_ceiling(int32_t passes, float w, float x0, float step, float *result, double *ms, double *pairs,
+                        void *stream) {
+  if (!result || !ms || !pairs || passes < 1) return fail(HE_E_ARG, "hk_valu_ceiling: bad arguments");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int32_t waves = valu_ceiling_waves();
+  std::vector<float> h;
+  const int32_t rc = time_ceiling("hk_valu_ceiling", waves, s, h, ms, [&](float *out) {
+    return launch_valu_ceiling(passes, w, x0, step, 0.0f, out, s);
+  });
+  if (rc) return rc;
+  for (int32_t i = 1; i < waves; ++i)
+    if (std::memcmp(&h[i], &h[0], sizeof(float)))
+      return fail(HE_E_HIP, "hk_valu_ceiling: the waves' sums differ");
+  *result = h[0];
+  *pairs = (double)waves * 64 * passes * 8;
+  return HE_OK;
+}
+
+int32_t hk_mfma_ceiling(int32_t passes, int32_t first, int32_t times, int32_t flip, int32_t *checksum, double *ms,
+                        double *ops, void *stream) {
+  if (!checksum || !ms || !ops || passes < 1) return fail(HE_E_ARG, "hk_mfma_ceiling: bad arguments");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int32_t waves = mfma_ceiling_waves();
+  std::vector<uint32_t> h;
+  const int32_t rc = time_ceiling("hk_mfma_ceiling", waves, s, h, ms, [&](uint32_t *out) {
+    return launch_mfma_ceiling(passes, first, times, flip, out, s);
+  });
+  if (rc) return rc;
+  for (int32_t i = 1; i < waves; ++i)
+    if (h[i] != h[0]) return fail(HE_E_HIP, "hk_mfma_ceiling: the waves' sums differ");
+  *checksum = (int32_t)h[0];
+  // 4 products of 32 x 32 x 32 a pass, a multiply and an add each
+  *ops = (double)waves * passes * 4 * 32768.0 * 2;
   return HE_OK;
 }
 

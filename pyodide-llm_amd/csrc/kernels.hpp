@@ -161,10 +161,22 @@ int32_t attention_most_positions();
 // of 32 (a block holds a whole group) and whose context fits the decode kernel's LDS
 bool attention_quantizes(const AttnArgs &a);
 
-// a streaming read of bytes (a multiple of 16) at p: block b's sums of its 32-bit words lane by lane (j = word index
-// % 4) into partial[4 b + j], for read_ceiling_blocks(bytes) blocks
-int32_t read_ceiling_blocks(int64_t bytes);
-hipError_t launch_read_ceiling(const void *p, int64_t bytes, uint32_t *partial, hipStream_t s);
+// a streaming read of bytes (a multiple of 16) at p in launch shape `shape` (0 .. read_ceiling_shapes() - 1: loads a
+// lane per tile, blocks): block b's sums of its 32-bit words lane by lane (j = word index % 4) into partial[4 b + j],
+// for read_ceiling_blocks(bytes, shape) blocks
+int32_t read_ceiling_shapes();
+int32_t read_ceiling_blocks(int64_t bytes, int32_t shape);
+int32_t read_ceiling_loads(int32_t shape);
+hipError_t launch_read_ceiling(const void *p, int64_t bytes, int32_t shape, uint32_t *partial, hipStream_t s);
+// ceilings.ts fma() in every lane of valu_ceiling_waves() waves, passes times (8 multiplies and 8 adds a pass, each
+// rounded): lane 0 of wave i writes its sum of the eight accumulators to out[i]
+int32_t valu_ceiling_waves();
+hipError_t launch_valu_ceiling(int32_t passes, float w, float x0, float step, float spread, float *out, hipStream_t s);
+// four v_mfma_i32_32x32x32_i8 a pass in each of mfma_ceiling_waves() waves: out[i] is wave i's sum (mod 2^32) of its
+// accumulators' elements
+int32_t mfma_ceiling_waves();
+hipError_t launch_mfma_ceiling(int32_t passes, int32_t first, int32_t times, int32_t flip, uint32_t *out,
+                               hipStream_t s);
 // greedy: the first index of the largest logit into *out (and the value into *value)
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
                          hipStream_t s);

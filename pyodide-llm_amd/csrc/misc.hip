@@ -307,56 +307,7 @@ int blocks_for(int64_t items, int64_t per_block, int64_t cap = 1 << 20) {
   return (int)(b > cap ? cap : b);
 }
 
-// the memory's read ceiling (kernels/ceilings.ts:9-25 read()): a wave reads 16 KiB tiles of the buffer (a lane 16
-// loads of 16 bytes, all requested together: the decode GEMV's pattern), tile w + waves * k for wave w of the launch;
-// the words added lane by lane (uint32, wrapping, order-free) into the block's four partial sums, partial[4 * block +
-// j] (no atomics: a few addresses taken by every block would serialize the launch). A tile past the end is clamped to
-// the buffer's last 16 bytes and adds nothing.
-__global__ __launch_bounds__(256) void read_ceiling_kernel(const uint4 *p, int64_t n16, uint32_t *partial) {
-  __shared__ uint4 waves[4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t nw = (int64_t)gridDim.x * 4, tiles = (n16 + 1023) / 1024;
-  uint4 acc = {0u, 0u, 0u, 0u};
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < tiles; t += nw) {
-    uint4 v[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) v[u] = p[min(t * 1024 + u * 64 + lane, n16 - 1)];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      if (t * 1024 + u * 64 + lane < n16) {
-        acc.x += v[u].x;
-        acc.y += v[u].y;
-        acc.z += v[u].z;
-        acc.w += v[u].w;
-      }
-    }
-  }
-  for (int o = 32; o >= 1; o >>= 1) {
-    acc.x += __shfl_xor(acc.x, o, 64);
-    acc.y += __shfl_xor(acc.y, o, 64);
-    acc.z += __shfl_xor(acc.z, o, 64);
-    acc.w += __shfl_xor(acc.w, o, 64);
-  }
-  if (lane == 0) waves[wave] = acc;
-  __syncthreads();
-  if (threadIdx.x < 4) {
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(waves);
-    partial[4 * blockIdx.x + threadIdx.x] = w[threadIdx.x] + w[4 + threadIdx.x] + w[8 + threadIdx.x] + w[12 + threadIdx.x];
-  }
-}
-
 }  // namespace
-
-int32_t read_ceiling_blocks(int64_t bytes) {
-  // 16 KiB tiles, four waves a block: at most 2048 blocks (8 a CU), fewer for a small buffer
-  return (int32_t)std::min<int64_t>(2048, std::max<int64_t>(1, (bytes / 16384 + 3) / 4));
-}
-
-hipError_t launch_read_ceiling(const void *p, int64_t bytes, uint32_t *partial, hipStream_t s) {
-  hipLaunchKernelGGL(read_ceiling_kernel, dim3(read_ceiling_blocks(bytes)), dim3(256), 0, s,
-                     reinterpret_cast<const uint4 *>(p), bytes / 16, partial);
-  return hipGetLastError();
-}
 
 hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n, int32_t x_stride,
                            int32_t xq_stride, int32_t xs_stride, int32_t bias, hipStream_t s) {

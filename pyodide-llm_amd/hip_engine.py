@@ -95,6 +95,7 @@ def library():
             "he_device_bytes": (U64, [P]),
             "he_close": (I32, [P]),
             "he_profile_forward": (I32, [P, I32, I32, I32, P, P, P]),
+            "he_profile_forward_many": (I32, [P, P, I32, I32, P, P, P]),
             "he_profile_matmul": (I32, [P, I32, I32, P, P, P]),
             "hk_quantize_x": (I32, [P, P, P, I32, I32, I32, P]),
             "hk_matmul": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, P]),
@@ -103,6 +104,8 @@ def library():
             "hk_sample": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
             "hk_sample_static": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
             "hk_read_ceiling": (I32, [P, ctypes.c_int64, I32, P, P, P]),
+            "hk_valu_ceiling": (I32, [I32, F, F, F, P, P, P, P]),
+            "hk_mfma_ceiling": (I32, [I32, I32, I32, I32, P, P, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -261,7 +264,18 @@ class Engine:
                                            _ptr(nbytes), _ptr(launches)))
         return {k: (float(ms[i]), float(nbytes[i]), int(launches[i])) for i, k in enumerate(KINDS)}
 
-    MATMULS = {"all": -1, "qkv": 0, "wo": 1, "w13": 2, "w2": 3, "classifier": 4}
+    def profileMany(self, tokens, pos):
+        """one prompt chunk (forwardMany of at most promptBlock tokens) timed by kind of kernel: {kind: (ms,
+        algorithmic bytes, launches)}"""
+        ms = np.zeros(len(KINDS), dtype=np.float64)
+        nbytes = np.zeros(len(KINDS), dtype=np.float64)
+        launches = np.zeros(len(KINDS), dtype=np.int32)
+        ids = np.ascontiguousarray(tokens, dtype=np.int32)
+        check(library().he_profile_forward_many(self._h, _ptr(ids), len(ids), int(pos), _ptr(ms), _ptr(nbytes),
+                                                _ptr(launches)))
+        return {k: (float(ms[i]), float(nbytes[i]), int(launches[i])) for i, k in enumerate(KINDS)}
+
+    MATMULS ={"all": -1, "qkv": 0, "wo": 1, "w13": 2, "w2": 3, "classifier": 4}
 
     def profile_matmul(self, which="all", rounds=4):
         """the decode matmuls of `which` (every layer) timed back to back: (ms a pass, algorithmic bytes a pass,

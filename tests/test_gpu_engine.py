@@ -88,6 +88,26 @@ def test_prompt_blocks_equal_one_at_a_time(name):
     assert same_bits(a["keys"], b["keys"]) and same_bits(a["values"], b["values"])
 
 
+def test_profiled_prompt_times_every_kind_and_keeps_the_bits():
+    """he_profile_forward_many runs the prompt chunk as forwardMany does (the cache gets the oracle's bits) and reports
+    the prompt's matmuls as GEMM launches"""
+    cfg, tensors, ck, cos, sin, _ = build("stories15m")
+    pk = package()
+    tokens = [int(t) for t in np.random.default_rng(8).integers(0, cfg.vocab_size, size=40)]
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    prof = eng.profileMany(tokens, 0)
+    assert prof["gemm"][2] == cfg.n_layers * 4 and prof["gemm"][0] > 0  # q/k/v, wo, w1/w3, w2 a layer
+    assert prof["gemv"][2] == 0 and prof["attention"][2] >= cfg.n_layers and prof["argmax"][2] == 0
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    ref.run(tokens, 0, False)
+    k, v = ref.kv(0, len(tokens))
+    kv = eng.keysAndValues(0, len(tokens))
+    assert same_bits(kv["keys"], k.reshape(-1)) and same_bits(kv["values"], v.reshape(-1))
+    with pytest.raises(pk.HipError):
+        eng.profileMany(tokens * 2, 0)  # more than the prompt block
+    eng.release()
+
+
 @pytest.mark.parametrize("name", sorted(MODELS))
 def test_device_checkpoint_equals_host_checkpoint(name):
     cfg, tensors, ck, cos, sin, size = build(name)

@@ -154,3 +154,51 @@ def test_read_ceiling_checksum(nbytes, passes):
     gl.check(package().library().hk_read_ceiling(buf.ptr, nbytes, passes, ctypes.byref(got), ctypes.byref(ms), None))
     assert (got.value & 0xFFFFFFFF) == want
     assert ms.value > 0
+
+
+def fma_lane(passes, w, x0, step):
+    """kernels/ceilings.ts fma() for one lane in float32, each step rounded (the benchmark page's fmaSum before its
+    four-lane sum)"""
+    f = np.float32
+    ws = [f(w), f(w) + f(0.0009765625), f(w) + f(0.001953125), f(w) + f(0.0029296875)]
+    x, d = f(x0), f(step)
+    y = x + f(0.25)
+    a = [f(i) for i in range(8)]
+    for _ in range(passes):
+        for k in range(4):
+            a[k] = a[k] + ws[k] * x
+            a[4 + k] = a[4 + k] + ws[k] * y
+        x, y = x - d, y - d
+    return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]))
+
+
+@pytest.mark.parametrize("passes, w, x0, step", [(1, 1.0, 0.9999, 1e-7), (1000, 1.0, 0.9999, 1e-7),
+                                                 (333, 0.37, -1.5, 0.003)])
+def test_valu_ceiling_sum(passes, w, x0, step):
+    """hk_valu_ceiling computes ceilings.ts fma()'s float32 sums (no FMA, no reordering) in every lane"""
+    result, ms, pairs = ctypes.c_float(0), ctypes.c_double(0), ctypes.c_double(0)
+    gl.check(package().library().hk_valu_ceiling(passes, w, x0, step, ctypes.byref(result), ctypes.byref(ms),
+                                                 ctypes.byref(pairs), None))
+    want = fma_lane(passes, w, x0, step)
+    assert np.float32(result.value).view(np.uint32) == want.view(np.uint32)
+    assert ms.value > 0 and pairs.value == 8192 * 64 * passes * 8
+
+
+def int8(v):
+    return ((v + 128) % 256) - 128
+
+
+@pytest.mark.parametrize("passes, first, times, flip", [(1, 3, 5, 0x81), (2, 3, 5, 0x81), (255, -128, 127, 0xFF),
+                                                        (1000, 3, 5, 0x81)])
+def test_mfma_ceiling_checksum(passes, first, times, flip):
+    """hk_mfma_ceiling's v_mfma_i32_32x32x32_i8 sums: every element of a 32 x 32 product gains 32 * a * b a pass (A's
+    bytes first, then first ^ flip, alternately; B's times), on accumulators that start at 1000 n + e"""
+    checksum, ms, ops = ctypes.c_int32(0), ctypes.c_double(0), ctypes.c_double(0)
+    gl.check(package().library().hk_mfma_ceiling(passes, first, times, flip, ctypes.byref(checksum), ctypes.byref(ms),
+                                                 ctypes.byref(ops), None))
+    a0, a1 = int8(first & 255), int8((first ^ flip) & 255)
+    sum_a = ((passes + 1) // 2) * a0 + (passes // 2) * a1
+    start = 64 * (16 * (0 + 1000 + 2000 + 3000) + 4 * sum(range(16)))
+    want = (start + 4 * 1024 * 32 * int8(times & 255) * sum_a) & 0xFFFFFFFF
+    assert (checksum.value & 0xFFFFFFFF) == want
+    assert ms.value > 0 and ops.value == 4096 * passes * 4 * 32768 * 2
