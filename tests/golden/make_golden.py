@@ -9,7 +9,7 @@ forward's logits on tiny int8/int6 models of every form (public/llama2_numpy.py:
 int8 path is held to within a line, tests/test_quantize.py:81-90). Inputs are seeded; outputs are stored as NumPy arrays (no pickles)
 and JSON. The reference is read from /root/reference/public; it does not travel with the fixtures.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [group ...]   (default: every group of GROUPS)
 """
 import ctypes
 import hashlib
@@ -30,6 +30,7 @@ import llama2_numpy  # noqa: E402
 sys.path.insert(0, os.path.join(REPO, "tests"))
 import oracle_lib  # noqa: E402
 from forms import FORM_TINY, form_checkpoint  # noqa: E402
+from tiny import TINY, sharp_checkpoint  # noqa: E402
 
 
 def save(name, **arrays):
@@ -118,15 +119,6 @@ def tokenizer_bytes(vocab):
     return b"".join(out)
 
 
-TINY = {
-    # name: (he_config fields, rope theta, dtype)
-    "tiny_gqa_int8": (dict(dim=64, hidden_dim=128, n_layers=2, n_heads=4, n_kv_heads=2, head_size=16, vocab_size=320,
-                           seq_len=32, shared_classifier=1, six=0, qkv_bias=0), 10000.0),
-    "tiny_mha_own_cls_int8": (dict(dim=96, hidden_dim=160, n_layers=2, n_heads=3, n_kv_heads=3, head_size=32,
-                                   vocab_size=256, seq_len=32, shared_classifier=0, six=0, qkv_bias=0), 10000.0),
-    "tiny_qwen_int6": (dict(dim=64, hidden_dim=96, n_layers=2, n_heads=4, n_kv_heads=1, head_size=16, vocab_size=288,
-                            seq_len=32, shared_classifier=0, six=1, qkv_bias=1), 1000000.0),
-}
 TOKENS = [1, 5, 9, 3, 7, 200, 11, 4]
 
 
@@ -146,6 +138,20 @@ def forwards():
     save("numpy_forward.npz", **out)
 
 
+def sharp_forwards():
+    """the NumPy forward's logits on the TINY models with attention that leans on a few keys (sharp_checkpoint)"""
+    out = {}
+    for name, (fields, theta) in TINY.items():
+        _, _, ck, _, _, tokens = sharp_checkpoint(name)
+        dtype = "int6" if fields["six"] else "int8"
+        model = llama2_numpy.Llama(bytes(ck), tokenizer_bytes(fields["vocab_size"]), dtype=dtype, rope_theta=theta,
+                                   bias=bool(fields["qkv_bias"]))
+        out[f"logits_{name}"] = np.stack([model.forward(tok, pos).astype(np.float32) for pos, tok in enumerate(tokens)])
+        out[f"tokens_{name}"] = np.array(tokens, dtype=np.int32)
+        out[f"sha256_{name}"] = np.frombuffer(hashlib.sha256(bytes(ck)).digest(), dtype=np.uint8)
+    save("numpy_forward_sharp.npz", **out)
+
+
 def form_forwards():
     out = {}
     for name, (fields, theta, keywords) in FORM_TINY.items():
@@ -160,12 +166,11 @@ def form_forwards():
     save("numpy_forms.npz", **out)
 
 
+GROUPS = {"quantizers": quantizers, "ropes": ropes, "plans": plans, "forwards": forwards, "layouts": layouts,
+          "form_forwards": form_forwards, "sharp_forwards": sharp_forwards}
+
 if __name__ == "__main__":
     oracle_lib.load()
-    quantizers()
-    ropes()
-    plans()
-    forwards()
-    layouts()
-    form_forwards()
+    for group in sys.argv[1:] or list(GROUPS):
+        GROUPS[group]()
     print("golden fixtures written to", HERE)

@@ -307,6 +307,19 @@ def vary_vectors(cfg, tensors, ck, seed):
     return ck
 
 
+def sharpen(cfg, tensors, ck, factor):
+    """in place: the scales of every layer's wq and wk times factor (their int8 / int6 values kept), so that q . k /
+    sqrt(head_size) spans a few units and each position's attention leans on a few keys: where attention is near
+    uniform (N(0, 0.02) weights), a rotation turned the wrong way or a misplaced pair hardly moves the logits"""
+    T = package().T
+    for name, rows in (("wq", cfg.n_heads * cfg.head_size), ("wk", cfg.n_kv_heads * cfg.head_size)):
+        t = tensors[T[name]]
+        n = cfg.n_layers * rows * (cfg.dim // 32)
+        scales = np.frombuffer(ck[t.scales:t.scales + 4 * n].tobytes(), dtype=np.float32) * np.float32(factor)
+        ck[t.scales:t.scales + 4 * n] = np.frombuffer(scales.astype(np.float32).tobytes(), dtype=np.uint8)
+    return ck
+
+
 def outlier_channels(weight, count=8, ratio=4.0):
     """public/llama2_numpy.py:807-813: the count channels with the largest |final-norm weight|, in order, or none where
     the largest is below ratio times the median"""

@@ -236,6 +236,52 @@ def test_rmsnorm_against_float64():
         assert np.allclose(got, want, rtol=2e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("nh, hs, rot", [(4, 16, 0), (3, 32, 32), (2, 32, 12), (5, 64, 16)])
+def test_rope_is_the_float64_rotation_of_interleaved_pairs(nh, hs, rot):
+    """kernels/kernel.ts:344-357: each head's pairs (v[2i], v[2i+1]), i < rot / 2 (rot 0 or hs: all of them), turned by
+    the angle whose cosine and sine the tables give at i; the values past rot untouched. Against the float64 rotation
+    of the same float32 inputs: a rotation the other way, swapped pair members, a table read at i instead of i / 2 or
+    a head offset by a pair all miss it by far more than float32's rounding"""
+    rng = np.random.default_rng(hs + rot)
+    v = (rng.standard_normal(nh * hs) * 2).astype(np.float32)
+    angles = rng.uniform(-math.pi, math.pi, hs // 2)
+    fcr, fci = np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
+    out = v.copy()
+    ol.load().or_rope(ol.ptr(out), ol.ptr(fcr), ol.ptr(fci), nh, hs, rot)
+    turned = rot if 0 < rot < hs else hs
+    heads, got = v.reshape(nh, hs).astype(np.float64), out.reshape(nh, hs)
+    v0, v1 = heads[:, 0:turned:2], heads[:, 1:turned:2]
+    c, s_ = fcr[:turned // 2].astype(np.float64), fci[:turned // 2].astype(np.float64)
+    want0, want1 = v0 * c - v1 * s_, v0 * s_ + v1 * c
+    # each output is a difference or sum of two rounded products: within 2 ulps of the larger product, at most
+    bound = 2.0 ** -22 * (np.abs(v0 * c) + np.abs(v1 * s_)) + 1e-30
+    assert (np.abs(got[:, 0:turned:2] - want0) <= bound).all()
+    assert (np.abs(got[:, 1:turned:2] - want1) <= bound).all()
+    assert np.array_equal(got[:, turned:], v.reshape(nh, hs)[:, turned:])
+    # a rotation keeps each pair's length
+    assert np.allclose(np.hypot(got[:, 0:turned:2], got[:, 1:turned:2]), np.hypot(v0, v1), rtol=1e-6)
+
+
+def test_rope_by_the_tables_turns_position_p_by_p_times_the_pair_frequency():
+    """or_rope_tables (public/llama2_numpy.py:484-542 for theta, no scaling): turning a pair by position a's angle then
+    by position b's is turning it by position a + b's (float64, to float32's rounding), and position 0 is the
+    identity"""
+    hs, theta, seq = 64, 10000.0, 64
+    cos, sin = ol.rope_tables(seq, hs, theta)
+    assert np.array_equal(cos[0], np.ones(hs // 2, np.float32)) and np.array_equal(sin[0], np.zeros(hs // 2, np.float32))
+    rng = np.random.default_rng(9)
+    v = rng.standard_normal(hs).astype(np.float32)
+    for a, b in ((3, 5), (10, 31), (1, 1)):
+        once = v.copy()
+        ol.load().or_rope(ol.ptr(once), ol.ptr(cos[a]), ol.ptr(sin[a]), 1, hs, 0)
+        ol.load().or_rope(ol.ptr(once), ol.ptr(cos[b]), ol.ptr(sin[b]), 1, hs, 0)
+        both = v.copy()
+        ol.load().or_rope(ol.ptr(both), ol.ptr(cos[a + b]), ol.ptr(sin[a + b]), 1, hs, 0)
+        assert np.allclose(once, both, rtol=0, atol=2e-6 * np.abs(v).max())
+        freq = 1.0 / theta ** (np.arange(0, hs, 2) / hs)
+        assert np.allclose(cos[a], np.cos(a * freq), atol=1e-7) and np.allclose(sin[a], np.sin(a * freq), atol=1e-7)
+
+
 def attention64(q, kc, vc, pos, nh, nkv, hs):
     out = np.zeros(nh * hs)
     for h in range(nh):
