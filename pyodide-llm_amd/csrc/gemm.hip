@@ -7,13 +7,16 @@
 // one group sum, never a sum across groups. The float32 part is the reference's: p_g = f32(S_g) * f32(ws_g * xs_g)
 // added to lane chain g mod 4 for the groups below 4*floor(G/4), the chains combined ((l0 + l1) + l2) + l3, then the
 // tail groups added in order; y = result (or y + result, the fused residual add). Those four float32 steps a group
-// (product of scales, convert, multiply, add) run on the VALU for every (row, token, group), so the kernel is bound by
-// the VALU, not by the MFMA pipe: one MFMA a group a tile against 64 VALU instructions.
+// (product of scales, conversion, multiply, add; the conversion done as a subtraction, see MAGIC) run on the VALU for
+// every (row, token, group), so the kernel is bound by the VALU, not by the MFMA pipe: one MFMA a group a tile against
+// 64 VALU instructions.
 //
-// Tiling: a block of 512 threads (8 waves) makes 64 rows x 128 tokens. Each K step stages 4 groups (128 bytes of K:
-// one group for each lane chain) of the block's weights, activations (centred: q - 64) and scales in LDS, double
-// buffered: the next step's global loads are in flight while the current one is computed. A wave makes one 32 x 32
-// MFMA tile: 4 chains x 16 accumulators a lane, few enough registers for two waves a SIMD and no AGPR traffic.
+// Tiling: a block of 256 threads (4 waves, one a SIMD) makes 64 rows x 64 tokens; each K step stages 4 groups (128
+// bytes of K: one group for each lane chain) of the block's weights, activations (centred: q - 64) and scales in LDS,
+// double buffered: the next step's global loads are in flight while the current one is computed. A wave makes one
+// 32 x 32 MFMA tile: 4 chains x 16 accumulators a lane. The register and LDS footprint lets three blocks share a CU,
+// so that while one block waits at its barrier or for its MFMA results the others' float32 work fills the VALU (with
+// one block of 8 waves a CU, every barrier and every MFMA latency left the VALU idle).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -21,7 +24,9 @@ namespace ple {
 namespace {
 
 constexpr int BR = 64;             // weight rows a block
-constexpr int BT = 128;            // tokens a block
+constexpr int BT = 64;             // tokens a block
+constexpr int NT = 256;            // threads a block: 2 x 2 waves of 32 x 32 tiles
+constexpr int NB = 2;              // MFMAs issued together before their float32 work
 constexpr int KS = 4;              // groups a K step: one for each lane chain
 constexpr int ROWB = KS * 32 + 16; // LDS bytes of one row of a stage (128 and 16 of padding against bank conflicts)
 
@@ -47,12 +52,11 @@ __device__ __forceinline__ SegRow seg_row(const MatArgs &a, int row) {
   return {a.seg[0].w, a.seg[0].ws, row};
 }
 
-// what one thread loads of a K step: half of one (row, group) of the weights (int8; int6: a whole group by the first
-// 256 threads) with its scale, one (token, group) of the activations with its scale. Registers between the global
-// load and the LDS store.
+// what one thread loads of a K step: one (row, group) of the weights (int8: 32 bytes; int6: the 24-byte group) with its
+// scale, one (token, group) of the activations with its scale. Registers between the global load and the LDS store.
 template <bool SIX>
 struct Fetch {
-  uint32_t w[SIX ? 6 : 4];
+  uint32_t w[SIX ? 6 : 8];
   float wsv;
   uint4 x[2];
   float xsv;
@@ -62,22 +66,21 @@ template <bool SIX, bool SUMS>
 __device__ __forceinline__ void fetch(Fetch<SIX> &f, const MatArgs &a, int r0, int t0, int g0, int G, int tid) {
   // rows, groups and tokens past the end clamped: the loads stay unconditional and valid; what they bring is never
   // added
+  const int row = min(r0 + (tid >> 2), a.total_rows - 1), g = min(g0 + (tid & 3), G - 1);
+  const SegRow s = seg_row(a, row);
   if constexpr (SIX) {
-    const int q = tid & 255, row = min(r0 + (q >> 2), a.total_rows - 1), g = min(g0 + (q & 3), G - 1);
-    const SegRow s = seg_row(a, row);
     const uint2 *p = reinterpret_cast<const uint2 *>(s.w + ((int64_t)s.r * G + g) * 24);
     const uint2 l0 = p[0], l1 = p[1], tops = p[2];
     f.w[0] = l0.x; f.w[1] = l0.y; f.w[2] = l1.x; f.w[3] = l1.y; f.w[4] = tops.x; f.w[5] = tops.y;
-    f.wsv = SUMS ? 0.0f : s.ws[(int64_t)s.r * G + g];
   } else {
-    const int row = min(r0 + (tid >> 3), a.total_rows - 1), g = min(g0 + ((tid >> 1) & 3), G - 1);
-    const SegRow s = seg_row(a, row);
-    const uint4 v = *reinterpret_cast<const uint4 *>(s.w + ((int64_t)s.r * G + g) * 32 + (tid & 1) * 16);
-    f.w[0] = v.x; f.w[1] = v.y; f.w[2] = v.z; f.w[3] = v.w;
-    f.wsv = SUMS ? 0.0f : s.ws[(int64_t)s.r * G + g];
+    const uint4 *p = reinterpret_cast<const uint4 *>(s.w + ((int64_t)s.r * G + g) * 32);
+    const uint4 v0 = p[0], v1 = p[1];
+    f.w[0] = v0.x; f.w[1] = v0.y; f.w[2] = v0.z; f.w[3] = v0.w;
+    f.w[4] = v1.x; f.w[5] = v1.y; f.w[6] = v1.z; f.w[7] = v1.w;
   }
+  f.wsv = SUMS ? 0.0f : s.ws[(int64_t)s.r * G + g];
   {
-    const int t = min(t0 + (tid >> 2), a.m - 1), g = min(g0 + (tid & 3), G - 1);
+    const int t = min(t0 + (tid >> 2), a.m - 1);
     const uint4 *p = reinterpret_cast<const uint4 *>(a.xq + (int64_t)t * a.xq_stride + (int64_t)g * 32);
     f.x[0] = p[0];
     f.x[1] = p[1];
@@ -89,41 +92,42 @@ __device__ __forceinline__ uint4 centre16(uint4 v) { return {centre4(v.x), centr
 
 template <bool SIX>
 __device__ __forceinline__ void store(Stage &st, const Fetch<SIX> &f, int tid) {
+  const int rt = tid >> 2, gi = tid & 3;  // the row (and the token) and the group of this thread
+  uint4 *d = reinterpret_cast<uint4 *>(st.a + rt * ROWB + gi * 32);
   if constexpr (SIX) {
-    if (tid < 256) {
-      const int row = tid >> 2, gi = tid & 3;
-      uint32_t w[8];
-      const uint32_t L[4] = {f.w[0], f.w[1], f.w[2], f.w[3]};
-      six_widen(L, f.w[4], f.w[5], w);
-      uint4 *d = reinterpret_cast<uint4 *>(st.a + row * ROWB + gi * 32);
-      d[0] = {w[0], w[1], w[2], w[3]};
-      d[1] = {w[4], w[5], w[6], w[7]};
-      st.ws[gi * BR + row] = f.wsv;
-    }
+    uint32_t w[8];
+    const uint32_t L[4] = {f.w[0], f.w[1], f.w[2], f.w[3]};
+    six_widen(L, f.w[4], f.w[5], w);
+    d[0] = {w[0], w[1], w[2], w[3]};
+    d[1] = {w[4], w[5], w[6], w[7]};
   } else {
-    const int row = tid >> 3, gi = (tid >> 1) & 3;
-    *reinterpret_cast<uint4 *>(st.a + row * ROWB + gi * 32 + (tid & 1) * 16) = {f.w[0], f.w[1], f.w[2], f.w[3]};
-    if ((tid & 1) == 0) st.ws[gi * BR + row] = f.wsv;
+    d[0] = {f.w[0], f.w[1], f.w[2], f.w[3]};
+    d[1] = {f.w[4], f.w[5], f.w[6], f.w[7]};
   }
-  {
-    const int tok = tid >> 2, gi = tid & 3;
-    uint4 *d = reinterpret_cast<uint4 *>(st.b + tok * ROWB + gi * 32);
-    d[0] = centre16(f.x[0]);
-    d[1] = centre16(f.x[1]);
-    st.xs[gi * BT + tok] = f.xsv;
-  }
+  st.ws[gi * BR + rt] = f.wsv;
+  uint4 *e = reinterpret_cast<uint4 *>(st.b + rt * ROWB + gi * 32);
+  e[0] = centre16(f.x[0]);
+  e[1] = centre16(f.x[1]);
+  st.xs[gi * BT + rt] = f.xsv;
 }
 
-// p = f32(S) * f32(ws * xs) for the 16 outputs of a lane in one MFMA tile: rows (v / 4) * 8 + (lane / 32) * 4 + v % 4
-// of the tile, the token lane % 32
-__device__ __forceinline__ void products(const v16i &S, const float *ws_rows, float xsv, float p[16]) {
+// The MFMA's accumulator starts at MAGIC (the bits of 1.5 * 2^23), so that it ends at MAGIC + S_g: for |S_g| < 2^22
+// (here |S_g| <= 32 * 128 * 64 = 2^18) those are the bits of the float32 1.5 * 2^23 + S_g, and subtracting
+// 1.5 * 2^23 gives f32(S_g) exactly (both terms and the difference are integers float32 holds). One float32
+// subtraction in place of the int-to-float conversion, which issues at half the rate of a multiply or an add.
+constexpr int MAGIC = 0x4B400000;
+constexpr float MAGIC_F = 12582912.0f;
+
+// p = f32(S) * f32(ws * xs) for the 16 outputs of a lane in one MFMA tile (R = MAGIC + S): rows (v / 4) * 8 +
+// (lane / 32) * 4 + v % 4 of the tile, the token lane % 32
+__device__ __forceinline__ void products(const v16i &R, const float *ws_rows, float xsv, float p[16]) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const float4 w4 = *reinterpret_cast<const float4 *>(ws_rows + q * 8);
-    p[q * 4 + 0] = (float)S[q * 4 + 0] * (w4.x * xsv);
-    p[q * 4 + 1] = (float)S[q * 4 + 1] * (w4.y * xsv);
-    p[q * 4 + 2] = (float)S[q * 4 + 2] * (w4.z * xsv);
-    p[q * 4 + 3] = (float)S[q * 4 + 3] * (w4.w * xsv);
+    p[q * 4 + 0] = (__int_as_float(R[q * 4 + 0]) - MAGIC_F) * (w4.x * xsv);
+    p[q * 4 + 1] = (__int_as_float(R[q * 4 + 1]) - MAGIC_F) * (w4.y * xsv);
+    p[q * 4 + 2] = (__int_as_float(R[q * 4 + 2]) - MAGIC_F) * (w4.z * xsv);
+    p[q * 4 + 3] = (__int_as_float(R[q * 4 + 3]) - MAGIC_F) * (w4.w * xsv);
   }
 }
 
@@ -147,12 +151,19 @@ __device__ __forceinline__ void write_sums(const MatArgs &a, const v16i &S, int 
 }
 
 // with SUMS the kernel writes the exact int32 group sums S_g to a.sums [m][rows][G] instead (one segment)
+// (three waves a SIMD: the register budget that keeps the MFMA results in VGPRs, no AGPR copies)
 template <bool SIX, bool SUMS>
-__global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void gemm_kernel(const MatArgs a) {
   __shared__ Stage stage[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave & 1, wt = wave >> 1;  // the wave's 32 rows and 32 tokens of the block
-  const int r0 = blockIdx.x * BR, t0 = blockIdx.y * BT;
+  // block b runs on XCD b % 8; the (row block, token block) pairs, row-block major, are dealt to the XCDs in 8
+  // contiguous ranges, so that the token blocks of one row block run one after another on one XCD and its weights
+  // come from that XCD's L2 after the first (dealt round-robin, every XCD would read every row block's weights)
+  const int tbn = (a.m + BT - 1) / BT, nblk = gridDim.x;
+  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int idx = xcd * (nblk / 8) + min(xcd, nblk % 8) + j;
+  const int r0 = (idx / tbn) * BR, t0 = (idx % tbn) * BT;
   const int G = a.k / 32, G4 = G & ~3, steps = G4 / KS, tail = G - G4;
 
   float acc[KS][16];
@@ -160,7 +171,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
   for (int c = 0; c < KS; ++c)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
-  const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  // the accumulators' start: 0 for the group sums themselves, MAGIC for the float32 path (products)
+  const int c0 = SUMS ? 0 : MAGIC;
+  const v16i start = {c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0};
 
   // the operands of this lane in a stage: weights row wr*32 + lane%32, activations token wt*32 + lane%32, 16 bytes
   // of each group at (lane / 32) * 16 (A and B take the same k bytes, so the sum is the group's)
@@ -182,25 +195,29 @@ __global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
     // below the stores): its groups are clamped into the row, and past the last stage what it stores goes to the
     // buffer no later read takes (the tail's stage is a real one: total > steps)
     fetch<SIX, SUMS>(f, a, r0, t0, (s + 1) * KS, G, tid);
-    // the step's four MFMAs issued together, then the float32 work: each group's products start as its MFMA ends
-    // while the later ones still run
-    v16i S[KS];
+    // NB MFMAs issued together, then their float32 work: each group's products start as its MFMA ends while the
+    // later ones still run (and the other blocks of the CU use the VALU meanwhile)
 #pragma unroll
-    for (int gi = 0; gi < KS; ++gi) {
-      const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
-      const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
-      S[gi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
+    for (int g0 = 0; g0 < KS; g0 += NB) {
+      v16i S[NB];
 #pragma unroll
-    for (int gi = 0; gi < KS; ++gi) {
-      if constexpr (SUMS) {
-        write_sums(a, S[gi], r0 + wr * 32, t0 + wt * 32, s * KS + gi, G, lane);
-      } else {
-        float p[16];
-        products(S[gi], st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
+      for (int u = 0; u < NB; ++u) {
+        const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + (g0 + u) * 32);
+        const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + (g0 + u) * 32);
+        S[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, start, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[gi][v] = acc[gi][v] + p[v];
+      for (int u = 0; u < NB; ++u) {
+        const int gi = g0 + u;
+        if constexpr (SUMS) {
+          write_sums(a, S[u], r0 + wr * 32, t0 + wt * 32, s * KS + gi, G, lane);
+        } else {
+          float p[16];
+          products(S[u], st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[gi][v] = acc[gi][v] + p[v];
+        }
       }
     }
     // the next stage's stores wait for its global loads: kept after the products (the compiler would move them,
@@ -226,7 +243,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(const MatArgs a) {
       if (gi < tail) {
         const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
         const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
-        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
+        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, start, 0, 0, 0);
         if constexpr (SUMS) {
           write_sums(a, S, r0 + wr * 32, t0 + wt * 32, G4 + gi, G, lane);
         } else {
@@ -271,18 +288,19 @@ bool gemm_supported(int32_t k, bool relaxed) { return relaxed && k >= 32 && k % 
 hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s) {
   if (a.m < 1 || a.total_rows < 1 || !gemm_supported(a.k, relaxed)) return hipErrorInvalidValue;
   if (a.sums && a.nseg != 1) return hipErrorInvalidValue;
-  const dim3 grid((a.total_rows + BR - 1) / BR, (a.m + BT - 1) / BT);
-  if (grid.y > 65535) return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)((a.total_rows + BR - 1) / BR) * ((a.m + BT - 1) / BT);
+  if (blocks > (1ll << 30)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks);
   if (a.sums) {
     if (six)
-      gemm_kernel<true, true><<<grid, 512, 0, s>>>(a);
+      gemm_kernel<true, true><<<grid, NT, 0, s>>>(a);
     else
-      gemm_kernel<false, true><<<grid, 512, 0, s>>>(a);
+      gemm_kernel<false, true><<<grid, NT, 0, s>>>(a);
   } else {
     if (six)
-      gemm_kernel<true, false><<<grid, 512, 0, s>>>(a);
+      gemm_kernel<true, false><<<grid, NT, 0, s>>>(a);
     else
-      gemm_kernel<false, false><<<grid, 512, 0, s>>>(a);
+      gemm_kernel<false, false><<<grid, NT, 0, s>>>(a);
   }
   return hipGetLastError();
 }
