@@ -15,6 +15,12 @@ namespace ple {
 
 namespace {
 
+// the row stride of rmsnorm's four sums of squares in LDS: room for WAVE_CHAIN_MOST values where the wave's register
+// chain takes them
+__host__ __device__ constexpr int norm_rowstride(int q4) {
+  return chain_rowstride(q4 <= WAVE_CHAIN_MOST ? WAVE_CHAIN_MOST : q4);
+}
+
 __global__ __launch_bounds__(256) void quantize_kernel(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n,
                                                        int32_t x_stride, int32_t xq_stride, int32_t xs_stride,
                                                        int32_t bias) {
@@ -39,7 +45,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *
     return;
   }
   extern __shared__ float sm[];
-  const int n4 = n & ~3, q4 = n4 >> 2, qs = chain_rowstride(q4);
+  const int n4 = n & ~3, q4 = n4 >> 2, qs = norm_rowstride(q4);
   float *xv = sm;            // n
   float *wv = sm + n;        // n
   float *sq = sm + 2 * n;    // 4 * qs, transposed: lane k's squares side by side
@@ -77,8 +83,21 @@ __global__ __launch_bounds__(1024) void rmsnorm_quant_kernel(int8_t *xq, float *
       if (j < n4) sq[(j & 3) * qs + (j >> 2)] = v * v;
     }
   }
-  __syncthreads();
-  if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
+  if (q4 <= WAVE_CHAIN_MOST) {
+    // the four sums from registers (waves 0 and 1): their rows padded with +0.0 to WAVE_CHAIN_MOST
+    for (int j = q4 + tid; j < WAVE_CHAIN_MOST; j += 1024) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sq[k * qs + j] = 0.0f;
+    }
+    __syncthreads();
+    if (tid < 128) {
+      const float sum = chain4_registers(sq, qs, tid);
+      if ((tid & 31) == 31) part[tid >> 5] = sum;
+    }
+  } else {
+    __syncthreads();
+    if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
+  }
   __syncthreads();
   if (tid == 0) {
     float ss = ((part[0] + part[1]) + part[2]) + part[3];
@@ -320,7 +339,7 @@ hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int
 hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s, const L2Fetch *fetch) {
-  const size_t lds = sizeof(float) * (size_t)(2 * n + 4 * chain_rowstride((n & ~3) >> 2) + 16);
+  const size_t lds = sizeof(float) * (size_t)(2 * n + 4 * norm_rowstride((n & ~3) >> 2) + 16);
   // one token: 4 blocks share its groups (more tokens fill the chip by themselves)
   const int split = m < 64 ? 4 : 1;
   const L2Fetch f = fetch && m == 1 ? *fetch : L2Fetch{};
