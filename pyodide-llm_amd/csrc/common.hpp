@@ -196,24 +196,23 @@ __device__ __forceinline__ float lds_chain(const float *c, int n, float acc) {
   return acc;
 }
 
-// Four ordered sums of up to WAVE_CHAIN_MOST values each, run from registers by two waves: 0 + c_k[0] + c_k[1] + ...
-// in order, every add rounded, where c_k = base + k * stride (k = 0..3) holds the values, +0.0 past the sum's own
-// count up to WAVE_CHAIN_MOST (x + 0 is x for sums whose running values are never -0). Thread t < 128 (wave t / 64)
-// runs sum k = t / 32 as segment s = t % 32: it adds values 32 s .. 32 s + 31 and hands its running sum to segment
-// s + 1 (a DPP row shift inside a 16-lane row, a row broadcast across rows), so the chain's adds come from registers
-// (about 4.3 cycles an add against 8.5 from LDS) and 32 values a lane keep the register count low enough for two
-// 1024-thread blocks a CU. Every lane executes every add; segment s's sum is the true running sum from then on.
-// Returns, in thread 32 k + 31, sum k. base 16-byte aligned, stride a multiple of 4.
-constexpr int WAVE_CHAIN_MOST = 1024;
-__device__ __forceinline__ float chain4_registers(const float *base, int stride, int tid) {
-  const int seg = tid & 31;
-  const float4 *c4 = reinterpret_cast<const float4 *>(base + (tid >> 5) * stride + seg * 32);
+// An ordered sum run from registers by the 32 lanes of a half-wave: 0 + c[0] + c[1] + ... in order, every add
+// rounded, over c = the sum's row of values (16-byte aligned), +0.0 from its count up to 32 * nseg (x + 0 is x for sums
+// whose running values are never -0: they start at +0). Lane seg (0..31) of the half-wave is segment seg: in round
+// s < nseg (nseg <= 32, the same in the whole wave) every lane adds its 32 values c[32 seg ..] to its running sum, and
+// segment s's sum then goes to segment s + 1 (a DPP row shift inside a 16-lane row, a row broadcast from a row's last
+// lane to the next row), so that lane s starts round s from the true running sum: the chain's adds come from registers
+// (about 4.3 cycles an add against 8.5 for LDS reads in the chain). Returns the sum in the lane with seg == nseg - 1.
+// Both half-waves of a wave run it together (each its own sum); the row broadcast writes only rows 1 and 3.
+// nseg >= 1.
+__device__ __forceinline__ float chain32_registers(const float *c, int nseg, int seg) {
+  // lanes past the last segment read the first one (in the row; what they add is never used)
+  const float4 *c4 = reinterpret_cast<const float4 *>(c + (seg < nseg ? seg : 0) * 32);
   float4 v[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) v[u] = c4[u];
   float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < 32; ++s) {
+  for (int s = 0; s < nseg; ++s) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       acc = acc + v[u].x;
@@ -221,16 +220,20 @@ __device__ __forceinline__ float chain4_registers(const float *base, int stride,
       acc = acc + v[u].z;
       acc = acc + v[u].w;
     }
-    if (s < 31) {
-      // segment s + 1 takes segment s's sum: row_shr:1 inside a row; from a row's lane 15 to the next row's lanes,
-      // row_bcast:15 with only rows 1 and 3 written (each 32-lane sum's second row)
-      const int src = __float_as_int(acc);
-      const float moved = __int_as_float(s % 16 == 15 ? __builtin_amdgcn_update_dpp(src, src, 0x142, 0xA, 0xF, false)
-                                                      : __builtin_amdgcn_update_dpp(src, src, 0x111, 0xF, 0xF, false));
-      acc = seg == s + 1 ? moved : acc;
-    }
+    const int src = __float_as_int(acc);
+    const float moved = __int_as_float(s % 16 == 15 ? __builtin_amdgcn_update_dpp(src, src, 0x142, 0xA, 0xF, false)
+                                                    : __builtin_amdgcn_update_dpp(src, src, 0x111, 0xF, 0xF, false));
+    acc = seg == s + 1 ? moved : acc;
   }
   return acc;
+}
+
+// Four ordered sums of up to WAVE_CHAIN_MOST values each by two waves (chain32_registers with 32 rounds): thread
+// t < 128 runs sum k = t / 32 over c_k = base + k * stride (+0.0 past its count up to WAVE_CHAIN_MOST), and thread
+// 32 k + 31 returns it. 32 values a lane keep the register count low enough for two 1024-thread blocks a CU.
+constexpr int WAVE_CHAIN_MOST = 1024;
+__device__ __forceinline__ float chain4_registers(const float *base, int stride, int tid) {
+  return chain32_registers(base + (tid >> 5) * stride, 32, tid & 31);
 }
 
 __device__ __forceinline__ void wave_sync_lds() {

@@ -190,6 +190,10 @@ LONG = {
     # two chunks in registers
     "hs128_mul4": (dict(dim=512, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=1, head_size=128, vocab_size=320,
                         seq_len=3700, shared_classifier=1), 3600),
+    # past 4096 positions: more than 1024 four-position blocks a sum, where the decode kernel's ordered sums run
+    # from LDS instead of registers
+    "hs128_mul4_4600": (dict(dim=512, hidden_dim=256, n_layers=1, n_heads=4, n_kv_heads=1, head_size=128,
+                             vocab_size=320, seq_len=4700, shared_classifier=1), 4600),
     # eight query heads a kv head past 2048 positions, heads of 16 (a block takes 16 columns)
     "mul8_hs16": (dict(dim=256, hidden_dim=128, n_layers=1, n_heads=16, n_kv_heads=2, head_size=16,
                        vocab_size=320, seq_len=2200, shared_classifier=1), 2100),
