@@ -38,8 +38,8 @@ PROFILED_STEPS = 8
 # WRITE_SIZE runs of this script, each counter scaled by what it reads on HIP's device-to-device copy of 1 GiB
 # (FETCH_SIZE read half the bytes copied: x2; WRITE_SIZE all of them: x1). The profile summary names the commands.
 TRAFFIC = {
-    "llama3-8b": {"bytes_per_pass": round((2 * (32 * (13893.9 + 9339.0 + 64598.4 + 32465.7) + 288662.5)
-                                           + (32 * (48.6 + 32 + 112 + 32) + 502.3)) * 1024),
+    "llama3-8b": {"bytes_per_pass": round((2 * (32 * (13900 + 9304 + 64600 + 32500) + 288700)
+                                           + (32 * (48.63 + 16 + 112 + 32) + 502.3)) * 1024),
                   "source": "profiles/decode_gemv_llama3-8b.md"},
 }
 
