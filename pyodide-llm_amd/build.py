@@ -23,8 +23,8 @@ NODE_INCLUDE = "/usr/include/node"
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function"]
-SOURCES = ["gemv.hip", "gemm.hip", "misc.hip", "forms.hip", "attention.hip", "sampling.hip", "ceilings.hip",
-           "engine.cpp"]
+SOURCES = ["gemv.hip", "gemm.hip", "misc.hip", "forms.hip", "attention.hip", "attention_tokens.hip", "sampling.hip",
+           "ceilings.hip", "engine.cpp"]
 
 
 def run(cmd):
