@@ -1,9 +1,9 @@
 // attention_tokens.hip — the attention of a prompt block (many tokens a launch), to the bit of kernels/kernel.ts:448-566
-// attentionOf in the order attention.hip states: (A) the scores of 64-position tiles for blocks of (token, head) rows
-// that share each staged key tile, with each tile's maxima; (B) one block a (token, head) writing the weights p over
-// the scores; (C) blocks of tokens that share the values they stage, a thread two (token, head, column) sums. (B) and
-// (C) also take the decode launches whose context is past the decode kernels' LDS. In a file of their own, so that
-// the decode kernels' code object does not change with them.
+// attentionOf in the order attention.hip states: (A) the scores of 64-position tiles for blocks of 64 (token, head)
+// rows that share each staged key tile, their products on the matrix core; (B) one block a (token, head) taking the
+// row's largest score and writing the weights p over the scores; (C) blocks of tokens that share the values they
+// stage, a thread two (token, head, column) sums. (B) and (C) also take the decode launches whose context is past the
+// decode kernels' LDS. In a file of their own, so that the decode kernels' code object does not change with them.
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -14,118 +14,156 @@ namespace ple {
 
 namespace {
 
-// (A) for many tokens (a prompt block): one block a (64-position tile, kv head, SR / mul tokens): the tile's keys
-// staged once in LDS for every (token, head) row of the block, SR rows (64; 32 for head size 256). A lane takes two
-// positions (2 pl, 2 pl + 1 of the tile) and the rows of its half-wave: wave w's half h takes rows
-// w + 4 (u + RW h), u < RW = SR / 8, and runs their four lane sums for both positions side by side over the head
-// (a query read serves two positions, a key read RW rows). The rows' tile maxima by half-wave reductions.
-template <int HS> constexpr int scores_rows() { return HS <= 128 ? 32 : 16; }
+// (A) for many tokens (a prompt block), products on the matrix core: one block a (64-position tile, kv head,
+// 64 / mul tokens): 64 (token, head) rows x 64 positions, a wave 32 rows x 32 positions. v_mfma_f32_32x32x1_2b_f32
+// with a zero accumulator makes 2 x 32 x 32 single products q[row][d] * k[pos][d], each the correctly rounded float32
+// product (as the VALU's multiply, subnormals kept: a zero accumulator adds nothing), two dims at once (block 0 from
+// lanes 0-31, block 1 from lanes 32-63): dims 4j and 4j + 2 in one, 4j + 1 and 4j + 3 in the next. The VALU then adds
+// each product to its (row, position)'s lane chain d % 4 in order of d, the sums kernels/kernel.ts:448-566 fixes: one
+// add a product instead of a multiply and an add. The head is staged in chunks of DC dims (the rows' queries and the
+// tile's keys, double buffered in LDS: the next chunk's loads in flight while this one is summed). No tile maxima:
+// the softmax takes each row's largest score from the scores themselves.
+template <int HS> constexpr int score_chunk() { return HS % 32 == 0 ? 32 : 16; }
+constexpr int SCORE_ROWS = 64;  // (token, head) rows a block
+
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+// the 16 values live in registers here: an empty asm that takes and gives them keeps the compiler from moving the
+// adds that make them below this point
+__device__ __forceinline__ void pin16(float (&x)[16]) {
+  asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]),
+               "+v"(x[8]), "+v"(x[9]), "+v"(x[10]), "+v"(x[11]), "+v"(x[12]), "+v"(x[13]), "+v"(x[14]), "+v"(x[15]));
+}
 
 template <int HS, bool HALF>
-__global__ __launch_bounds__(256) void scores_tokens_kernel(const AttnArgs a) {
-  constexpr int LD = HS + 4, C4 = HS / 4, SR = scores_rows<HS>(), RW = SR / 8;
-  __shared__ float ks[TILE * LD];
-  __shared__ float qs[SR * HS];
-  const int tile = blockIdx.x, kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = lane >> 5, pl = lane & 31;
-  const int mul = a.nh / a.nkv, tt_n = max(1, SR / mul);
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void scores_tokens_kernel(const AttnArgs a) {
+  constexpr int DC = score_chunk<HS>(), NC = HS / DC;
+  constexpr int LDC = DC + 2;  // floats a staged row: the b64 reads of 32 rows fall on distinct banks
+  constexpr int NF = TILE * DC / 4 / 256;  // float4 of keys (and of queries) a thread stages a chunk
+  __shared__ float ks[2][TILE * LDC];
+  __shared__ float qs[2][SCORE_ROWS * LDC];
+  const int kh = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave & 1, wp = wave >> 1;  // the wave's 32 rows and 32 positions
+  const int h = lane >> 5, l32 = lane & 31;
+  const int mul = a.nh / a.nkv, tt_n = max(1, SCORE_ROWS / mul);
   const int t0 = blockIdx.z * tt_n, last = min(t0 + tt_n, a.m) - 1;
-  const int p0 = tile * TILE, pos0 = first_position(a);
-  if (p0 >= pos0 + last + 1) return;  // past every token of the block (uniform: before any barrier)
+  const int tile = blockIdx.x, p0 = tile * TILE, pos0 = first_position(a), reach = pos0 + last + 1;
+  if (p0 >= reach) return;  // past every token of the block (uniform: before any barrier)
   const int kvdim = a.nkv * HS;
-  const int np = min(TILE, pos0 + last + 1 - p0);  // positions any token of the block reaches
-  // keys: TILE * C4 float4, and the rows' queries: SR * C4 float4, requested together (clamped, unconditional)
-  constexpr int NK = TILE * C4 / 256, NQ = (SR * C4 + 255) / 256;
-  float4 kr[NK], qr[NQ];
+  // a chunk's loads: keys of positions (clamped to the reach: loaded, never used) and queries of rows (token
+  // t0 + r / mul, clamped to the block's last, head kh * mul + r % mul), row/position i / (DC / 4), float4
+  // i % (DC / 4); as 32-bit element offsets from the two bases (the launch checks that the cache and the queries fit)
+  uint32_t ko[NF], qo[NF];
 #pragma unroll
-  for (int u = 0; u < NK; ++u) {
-    const int i = tid + u * 256, p = min(i / C4, np - 1), c = i % C4;
-    kr[u] = cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
+  for (int u = 0; u < NF; ++u) {
+    const int i = tid + 256 * u, r = i / (DC / 4), c4 = i % (DC / 4);
+    ko[u] = (uint32_t)min(p0 + r, reach - 1) * (uint32_t)kvdim + (uint32_t)(kh * HS + 4 * c4);
+    const int t = min(t0 + r / mul, last), hh = kh * mul + r % mul;
+    qo[u] = (uint32_t)t * (uint32_t)a.q_stride + (uint32_t)(hh * HS + 4 * c4);
   }
+  float4 kf[NF], qf[NF];
+  auto fetch = [&](int c) {
 #pragma unroll
-  for (int u = 0; u < NQ; ++u) {
-    const int i = min(tid + u * 256, SR * C4 - 1), r = i / C4, c = i % C4;
-    const int t = min(t0 + r / mul, last), h = kh * mul + r % mul;
-    qr[u] = *reinterpret_cast<const float4 *>(a.q + (int64_t)t * a.q_stride + (int64_t)h * HS + 4 * c);
-  }
+    for (int u = 0; u < NF; ++u) {
+      kf[u] = cache4<HALF>(a.kcache, ko[u] + (uint32_t)(c * DC));
+      qf[u] = *reinterpret_cast<const float4 *>(a.q + (qo[u] + (uint32_t)(c * DC)));
+    }
+  };
+  auto stage = [&](int buf) {
 #pragma unroll
-  for (int u = 0; u < NK; ++u) {
-    const int i = tid + u * 256, p = i / C4, c = i % C4;
-    *reinterpret_cast<float4 *>(ks + p * LD + 4 * c) = kr[u];
-  }
-#pragma unroll
-  for (int u = 0; u < NQ; ++u) {
-    const int i = tid + u * 256;
-    if (i < SR * C4) *reinterpret_cast<float4 *>(qs + 4 * i) = qr[u];
-  }
+    for (int u = 0; u < NF; ++u) {
+      const int i = tid + 256 * u, r = i / (DC / 4), c4 = i % (DC / 4);
+      float2 *kd = reinterpret_cast<float2 *>(ks[buf] + r * LDC + 4 * c4);
+      float2 *qd = reinterpret_cast<float2 *>(qs[buf] + r * LDC + 4 * c4);
+      kd[0] = make_float2(kf[u].x, kf[u].y);
+      kd[1] = make_float2(kf[u].z, kf[u].w);
+      qd[0] = make_float2(qf[u].x, qf[u].y);
+      qd[1] = make_float2(qf[u].z, qf[u].w);
+    }
+  };
+  fetch(0);
+  stage(0);
   __syncthreads();
-  const float isq = 1.0f / __builtin_sqrtf((float)HS);
-  float l[2][RW][4];
+  float acc[4][16];
 #pragma unroll
-  for (int e = 0; e < 2; ++e)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int u = 0; u < RW; ++u) l[e][u][0] = l[e][u][1] = l[e][u][2] = l[e][u][3] = 0.0f;
-  const float *kp0 = ks + (2 * pl) * LD, *kp1 = kp0 + LD;
-  const float *qb = qs + (wave + 4 * RW * half) * HS;  // row u of the half-wave at qb + 4 u HS
-#pragma unroll 4
-  for (int j = 0; j < HS; j += 4) {
-    const float4 k0 = *reinterpret_cast<const float4 *>(kp0 + j);
-    const float4 k1 = *reinterpret_cast<const float4 *>(kp1 + j);
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
+  const v32f zero = {};
+  for (int c = 0; c < NC; ++c) {
+    const bool more = c + 1 < NC;  // uniform
+    if (more) fetch(c + 1);
+    // this lane's operands: row wr * 32 + lane % 32 of the queries and position wp * 32 + lane % 32 of the keys, the
+    // dims 4j + 2 h and 4j + 2 h + 1 of the chunk
+    const float *qb = qs[c & 1] + (wr * 32 + l32) * LDC + 2 * h;
+    const float *kb = ks[c & 1] + (wp * 32 + l32) * LDC + 2 * h;
 #pragma unroll
-    for (int u = 0; u < RW; ++u) {
-      const float4 qv = *reinterpret_cast<const float4 *>(qb + 4 * u * HS + j);
-      l[0][u][0] = l[0][u][0] + qv.x * k0.x;
-      l[0][u][1] = l[0][u][1] + qv.y * k0.y;
-      l[0][u][2] = l[0][u][2] + qv.z * k0.z;
-      l[0][u][3] = l[0][u][3] + qv.w * k0.w;
-      l[1][u][0] = l[1][u][0] + qv.x * k1.x;
-      l[1][u][1] = l[1][u][1] + qv.y * k1.y;
-      l[1][u][2] = l[1][u][2] + qv.z * k1.z;
-      l[1][u][3] = l[1][u][3] + qv.w * k1.w;
+    for (int j = 0; j < DC / 4; ++j) {
+      const float2 qv = *reinterpret_cast<const float2 *>(qb + 4 * j);
+      const float2 kv = *reinterpret_cast<const float2 *>(kb + 4 * j);
+      // one product block in registers at a time: the sums are pinned where they are made (the compiler would
+      // otherwise sink the adds below later MFMAs and keep every product block); the other waves of the SIMD hide
+      // each MFMA's latency
+      v32f d = __builtin_amdgcn_mfma_f32_32x32x1f32(qv.x, kv.x, zero, 0, 0, 0);  // dims 4j, 4j + 2
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc[0][v] = acc[0][v] + d[v];
+        acc[2][v] = acc[2][v] + d[16 + v];
+      }
+      pin16(acc[0]);
+      pin16(acc[2]);
+      d = __builtin_amdgcn_mfma_f32_32x32x1f32(qv.y, kv.y, zero, 0, 0, 0);  // dims 4j + 1, 4j + 3
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc[1][v] = acc[1][v] + d[v];
+        acc[3][v] = acc[3][v] + d[16 + v];
+      }
+      pin16(acc[1]);
+      pin16(acc[3]);
+    }
+    if (more) {
+      stage((c + 1) & 1);  // the other buffer: its last readers passed the previous barrier
+      __syncthreads();
     }
   }
+  // the lane's 16 outputs: rows wr * 32 + (v / 4) * 8 + h * 4 + v % 4 (uniform over the half-wave), position
+  // p0 + wp * 32 + lane % 32
+  const float isq = 1.0f / __builtin_sqrtf((float)HS);
+  const int p = p0 + wp * 32 + l32;
 #pragma unroll
-  for (int u = 0; u < RW; ++u) {
-    const int r = wave + 4 * (u + RW * half), tt = r / mul, hl = r % mul, t = t0 + tt;
-    const bool row = tt < tt_n && t < a.m;  // uniform over the half-wave
-    const int count = first_position(a) + min(t, a.m - 1) + 1;
-    float *srow = a.scores + ((int64_t)t * a.nh + kh * mul + hl) * a.seq_len;
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int p = p0 + 2 * pl + e;
-      if (row && p < count) {
-        const float sc = ((l[e][u][0] + l[e][u][2]) + (l[e][u][1] + l[e][u][3])) * isq;
-        srow[p] = sc;
-        mx = wmax(mx, sc);
-      }
-    }
-    // the tile's largest of this (token, head): the 32 lanes of the half-wave (xor offsets below 32 stay in it)
-    for (int o = 16; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-    if (row && pl == 0 && p0 < count) a.tilemax[((int64_t)t * a.nh + kh * mul + hl) * (a.seq_len / TILE + 1) + tile] = mx;
+  for (int v = 0; v < 16; ++v) {
+    const int r = wr * 32 + (v >> 2) * 8 + h * 4 + (v & 3), tt = r / mul, t = t0 + tt;
+    const int count = pos0 + min(t, a.m - 1) + 1;
+    if (tt < tt_n && t < a.m && p < count)
+      a.scores[((int64_t)t * a.nh + kh * mul + r % mul) * a.seq_len + p] =
+          ((acc[0][v] + acc[2][v]) + (acc[1][v] + acc[3][v])) * isq;
   }
 }
 
-// (B) one block a (head, token): grid (nh, m), block 256. The scores requested at once, the exponentials by every
-// thread into LDS (lane k's positions t % 4 == k side by side), the four ordered sums by four threads, the weights.
+// (B) one block a (head, token): grid (nh, m), block 256. The scores requested at once, their largest by a block
+// reduction, the exponentials by every thread into LDS (lane k's positions t % 4 == k side by side), the four ordered
+// sums by four threads, the weights.
 __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   extern __shared__ float e4[];  // 4 rows of q4s exponentials, then the tail
   __shared__ float part[4];
-  __shared__ float shared_mx, shared_inv;
+  __shared__ float shared_mx, shared_inv, wave_mx[4];
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const int count = first_position(a) + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = chain_rowstride(q4);
-  const int tiles = (count + TILE - 1) / TILE;
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
-  const float *tm = a.tilemax + ((int64_t)t * a.nh + h) * (a.seq_len / TILE + 1);
-  float sv[16];  // up to 16 scores a thread, requested with the tile maxima
+  float sv[16];  // up to 16 scores a thread
 #pragma unroll
   for (int u = 0; u < 16; ++u) sv[u] = scores[min(tid + 256 * u, count - 1)];  // clamped, unconditional
-  if (tid < 64) {
-    float mx = -3.4028234663852886e38f;
-    for (int i = tid; i < tiles; i += 64) mx = wmax(mx, tm[i]);
-    for (int o = 32; o >= 1; o >>= 1) mx = wmax(mx, __shfl_xor(mx, o, 64));
-    if (tid == 0) shared_mx = mx;
-  }
+  // the largest score, from the lowest finite float32 (order-free: every score once, clamped copies of the last
+  // changing nothing)
+  float lm = -3.4028234663852886e38f;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) lm = wmax(lm, sv[u]);
+  for (int base = 256 * 16; base < count; base += 256 * 16)  // past 4096 positions: the rest, read once more below
+    for (int u = 0; u < 16; ++u) lm = wmax(lm, scores[min(base + tid + 256 * u, count - 1)]);
+  for (int o = 32; o >= 1; o >>= 1) lm = wmax(lm, __shfl_xor(lm, o, 64));
+  if ((tid & 63) == 0) wave_mx[tid >> 6] = lm;
+  __syncthreads();
+  if (tid == 0) shared_mx = wmax(wmax(wave_mx[0], wave_mx[1]), wmax(wave_mx[2], wave_mx[3]));
   __syncthreads();
   const float mx = shared_mx;
   float *tail = e4 + 4 * q4s;
@@ -274,8 +312,10 @@ __global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
 
 template <int HS, bool HALF>
 hipError_t scores_tokens_hs(const AttnArgs &a, hipStream_t s) {
+  // the kernel's element offsets are 32-bit
+  if ((int64_t)a.seq_len * a.nkv * HS >= (1ll << 32) || (int64_t)a.m * a.q_stride >= (1ll << 32)) return hipErrorInvalidValue;
   const int tiles = (a.pos0 + a.m + TILE - 1) / TILE;
-  const int tt = std::max(1, scores_rows<HS>() / (a.nh / a.nkv));
+  const int tt = std::max(1, SCORE_ROWS / (a.nh / a.nkv));
   hipLaunchKernelGGL((scores_tokens_kernel<HS, HALF>), dim3(tiles, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   return hipGetLastError();
 }
