@@ -200,115 +200,131 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   }
 }
 
-// (C) for many tokens (a prompt block): one block of 256 threads a (kv head, 32 of its columns (16 where hs is not a
-// multiple of 32), 2 * 256 / (columns * mul) tokens), a thread two (token, head, column) ordered sums over the
-// four-position blocks, run side by side (tokens tt and tt + 256 / (columns * mul) of the block, one value read for
-// both): out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)) from LDS, where 128-position chunks of the values (a column's
-// positions side by side, as the cache holds them) and of the weights are staged, the next chunk's loads in flight
-// meanwhile. The block's tokens share every value they read; each stops at its own last four.
-constexpr int TPC = 128;  // positions a chunk
+// (C) for many tokens (a prompt block), products on the matrix core: v_mfma_f32_16x16x1_4b_f32 with a zero
+// accumulator makes 4 x 16 x 16 single products, block b of the four being position 4k + b: p[row][4k + b] *
+// v[4k + b][col], each the correctly rounded float32 product. A lane then holds, for each of its 4 (row, column)
+// outputs, the four products of one four-position block, and adds them as kernels/kernel.ts:448-566 does:
+// out = out + ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), one add a product. A block of 256 threads takes R (token, head) rows
+// (R = 1024 / C) and C columns of one kv head, 4 tiles of 16 x 16, one a wave (the positions are the long dimension
+// and their order is fixed, so the outputs are split as finely as the matrix core allows, for as many waves as can
+// share a CU); the weights and the values of a 32-position chunk are staged in LDS (double buffered: the next chunk's
+// loads in flight). The block's tokens end at different positions: a four-position block past a row's last whole four
+// is not added to it, and the positions past its fours are added one at a time at the end, out = out + p v.
+template <int HS> constexpr int pv_cols() { return HS % 32 == 0 ? 32 : 16; }
+constexpr int TPC = 32;        // positions a chunk
+constexpr int LDP = TPC + 4;   // floats a staged row: 16 rows x 4 positions of a read on distinct banks
 
-template <int HS, bool HALF>
-__global__ __launch_bounds__(256) void pv_tokens_kernel(const AttnArgs a) {
-  constexpr int COLS = HS % 32 == 0 ? 32 : 16;   // columns a block
-  constexpr int TROWS = 256 / COLS;              // (token, head) rows of one pass over the block's threads
-  constexpr int ROWS = 2 * TROWS;                // weight rows a block at most: a thread runs two rows' sums
-  constexpr int TVS = TPC + 4;                   // LDS row of a column's values (16 lanes' float4 on distinct banks)
-  constexpr int VPT = TPC * (COLS / 4) / 256;    // float4 of values a thread a chunk
-  constexpr int WPT = ROWS * (TPC / 4) / 256;    // float4 of weights a thread a chunk
-  __shared__ float vs[2][COLS * TVS];  // [column][position]
-  __shared__ float ps[2][ROWS * TPC];  // [token * mul + head][position]
-  const int tid = threadIdx.x, kh = blockIdx.y;
-  const int mul = a.nh / a.nkv, tt_n = max(1, TROWS / mul);  // tokens of one pass; the block takes two passes' worth
-  const int j0 = blockIdx.x * COLS, t0 = blockIdx.z * 2 * tt_n;
-  const int j = tid % COLS, hl = (tid / COLS) % mul, tt = tid / (COLS * mul);
-  // the thread's two sums, tokens t0 + tt and t0 + tt + tt_n of the same head and column: two independent chains,
-  // every value read serves both
-  const bool in = tt < tt_n;
-  const bool chain0 = in && t0 + tt < a.m, chain1 = in && t0 + tt + tt_n < a.m;
-  const int ta = min(t0 + tt, a.m - 1), tb = min(t0 + tt + tt_n, a.m - 1);
-  const int pos0 = first_position(a);
-  const int count_a = pos0 + ta + 1, count4_a = count_a & ~3, count_b = pos0 + tb + 1, count4_b = count_b & ~3;
-  const int last = min(t0 + 2 * tt_n, a.m) - 1;  // the block's last token reads the most positions
-  const int most4 = (pos0 + last + 1) & ~3;
-  const int chunks = (most4 + TPC - 1) / TPC;
-  const int rows = (last - t0 + 1) * mul;  // weight rows of the block
-  float4 v[VPT], w[WPT];
-  // a chunk's loads, from clamped addresses (unconditional; what lies past a token's count4 is never added), and their
-  // stores into LDS: written out as macros, so that v and w stay in registers
-#define PVT_FETCH(c_)                                                                                             \
-  do {                                                                                                            \
-    _Pragma("unroll") for (int u = 0; u < VPT; ++u) {                                                             \
-      const int i = tid + 256 * u, cc = i / (TPC / 4), pos = min((c_) * TPC + 4 * (i % (TPC / 4)), most4 - 4);   \
-      v[u] = cache4<HALF>(a.vcache, (int64_t)(kh * HS + j0 + cc) * a.vstride + pos);                              \
-    }                                                                                                             \
-    _Pragma("unroll") for (int u = 0; u < WPT; ++u) {                                                             \
-      const int i = tid + 256 * u;                                                                                \
-      const int r = min(i / (TPC / 4), rows - 1), pos = min((c_) * TPC + 4 * (i % (TPC / 4)), most4 - 4);       \
-      w[u] = *reinterpret_cast<const float4 *>(a.scores + ((int64_t)(t0 + r / mul) * a.nh + kh * mul + r % mul) * \
-                                                              a.seq_len + pos);                                   \
-    }                                                                                                             \
-  } while (0)
-#define PVT_STAGE(buf_)                                                                                           \
-  do {                                                                                                            \
-    _Pragma("unroll") for (int u = 0; u < VPT; ++u) {                                                             \
-      const int i = tid + 256 * u;                                                                                \
-      *reinterpret_cast<float4 *>(vs[(buf_)] + (i / (TPC / 4)) * TVS + 4 * (i % (TPC / 4))) = v[u];               \
-    }                                                                                                             \
-    _Pragma("unroll") for (int u = 0; u < WPT; ++u) {                                                             \
-      reinterpret_cast<float4 *>(ps[(buf_)])[tid + 256 * u] = w[u]; /* every row, the block's or clamped copies */ \
-    }                                                                                                             \
-  } while (0)
-  if (chunks > 0) {
-    PVT_FETCH(0);
-    PVT_STAGE(0);
-  }
-  __syncthreads();
-  float acc0 = 0.0f, acc1 = 0.0f;
-  for (int c = 0; c < chunks; ++c) {
-    PVT_FETCH(c + 1);  // the next chunk's loads fly while this one is added (after the last: clamped, unused)
-    const float *vc = vs[c & 1] + j * TVS;
-    const float *pa = ps[c & 1] + (tt * mul + hl) * TPC;
-    const float *pb = ps[c & 1] + ((tt + tt_n) * mul + hl) * TPC;
-    const int na = chain0 ? max(0, min(TPC, count4_a - c * TPC)) >> 2 : 0;
-    const int nb = chain1 ? max(0, min(TPC, count4_b - c * TPC)) >> 2 : 0;
-    const int both = min(na, nb);
-    int b = 0;
-    for (; b < both; ++b) {
-      const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * b);
-      const float4 wa = *reinterpret_cast<const float4 *>(pa + 4 * b);
-      const float4 wb = *reinterpret_cast<const float4 *>(pb + 4 * b);
-      acc0 = acc0 + ((wa.x * vv.x + wa.y * vv.y) + (wa.z * vv.z + wa.w * vv.w));
-      acc1 = acc1 + ((wb.x * vv.x + wb.y * vv.y) + (wb.z * vv.z + wb.w * vv.w));
-    }
-    for (int e = b; e < na; ++e) {  // the earlier token's own positions (only where the later one has no sum)
-      const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * e);
-      const float4 wa = *reinterpret_cast<const float4 *>(pa + 4 * e);
-      acc0 = acc0 + ((wa.x * vv.x + wa.y * vv.y) + (wa.z * vv.z + wa.w * vv.w));
-    }
-    for (int e = b; e < nb; ++e) {  // the later token's positions past the earlier one's
-      const float4 vv = *reinterpret_cast<const float4 *>(vc + 4 * e);
-      const float4 wb = *reinterpret_cast<const float4 *>(pb + 4 * e);
-      acc1 = acc1 + ((wb.x * vv.x + wb.y * vv.y) + (wb.z * vv.z + wb.w * vv.w));
-    }
-    PVT_STAGE((c + 1) & 1);  // the other buffer: its last readers passed the previous barrier
-    __syncthreads();
-  }
-#undef PVT_FETCH
-#undef PVT_STAGE
-  const int64_t vcol = (int64_t)(kh * HS + j0 + j) * a.vstride;
-  if (chain0) {
-    const float *pt = a.scores + ((int64_t)ta * a.nh + kh * mul + hl) * a.seq_len;
-    for (int p = count4_a; p < count_a; ++p) acc0 = acc0 + pt[p] * cache1<HALF>(a.vcache, vcol + p);
-    a.out[(int64_t)ta * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc0;
-  }
-  if (chain1) {
-    const float *pt = a.scores + ((int64_t)tb * a.nh + kh * mul + hl) * a.seq_len;
-    for (int p = count4_b; p < count_b; ++p) acc1 = acc1 + pt[p] * cache1<HALF>(a.vcache, vcol + p);
-    a.out[(int64_t)tb * a.out_stride + (kh * mul + hl) * HS + j0 + j] = acc1;
-  }
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void pin4(float (&x)[4]) {
+  asm volatile("" : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
 }
 
+// (at most 128 VGPRs a lane: the MFMA then writes VGPRs, with no copies out of AGPRs)
+template <int HS, bool HALF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void pv_tokens_kernel(const AttnArgs a) {
+  constexpr int C = pv_cols<HS>(), R = 1024 / C, CT = C / 16;  // columns, rows, column tiles of a block
+  constexpr int NP = R * TPC / 4 / 256;                       // float4 of weights a thread stages (1 or 2)
+  static_assert(NP >= 1 && NP <= 2 && C * TPC / 4 <= 256, "pv staging shape");
+  __shared__ float ps[2][R * LDP];  // weights [row][position]
+  __shared__ float vs[2][C * LDP];  // values [column][position]
+  const int kh = blockIdx.y, j0 = blockIdx.x * C, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;  // the lane's position in a four (its operands) and row/column in a tile
+  const int trow = (wave / CT) * 16, tcol = (wave % CT) * 16;  // the wave's tile
+  const int mul = a.nh / a.nkv, tt_n = max(1, R / mul);
+  const int t0 = blockIdx.z * tt_n, last = min(t0 + tt_n, a.m) - 1;
+  const int pos0 = first_position(a);
+  const int most4 = (pos0 + last + 1) & ~3;   // the block's last token's whole fours: every four any row adds
+  const int least4 = (pos0 + t0 + 1) & ~3;    // the first token's: every row adds the fours below it
+  const int chunks = (most4 + TPC - 1) / TPC;
+  // staging loads: weights of rows tid / 8 (+ 32) (token t0 + r / mul clamped to the block's last, head
+  // kh * mul + r % mul), values of column tid / 8, float4 tid % 8 of the chunk; positions clamped below most4 (loaded,
+  // never added). Written out as macros with named registers, so that the staged values stay in registers.
+  const float *prow0, *prow1 = nullptr;
+  {
+    auto row_of = [&](int r) {
+      const int t = min(t0 + r / mul, last), hh = kh * mul + r % mul;
+      return a.scores + ((int64_t)t * a.nh + hh) * a.seq_len + 4 * (tid % 8);
+    };
+    prow0 = row_of(tid / 8);
+    if constexpr (NP > 1) prow1 = row_of(tid / 8 + 32);
+  }
+  const int64_t vrow = (int64_t)(kh * HS + j0 + min(tid, C * TPC / 4 - 1) / 8) * a.vstride + 4 * (tid % 8);
+  float4 pf0, pf1, vf0;
+#define PV_FETCH(c_)                                                                                               \
+  do {                                                                                                             \
+    const int po = min((c_) * TPC, most4 - 4 - 4 * (tid % 8));                                                    \
+    pf0 = *reinterpret_cast<const float4 *>(prow0 + po);                                                           \
+    if constexpr (NP > 1) pf1 = *reinterpret_cast<const float4 *>(prow1 + po);                                      \
+    vf0 = cache4<HALF>(a.vcache, vrow + po);                                                                       \
+  } while (0)
+#define PV_STAGE(buf_)                                                                                             \
+  do {                                                                                                             \
+    float *pd = ps[(buf_)] + (tid / 8) * LDP + 4 * (tid % 8);                                                      \
+    *reinterpret_cast<float4 *>(pd) = pf0;                                                                         \
+    if constexpr (NP > 1) *reinterpret_cast<float4 *>(pd + 32 * LDP) = pf1;                                        \
+    if (tid < C * TPC / 4) *reinterpret_cast<float4 *>(vs[(buf_)] + (tid / 8) * LDP + 4 * (tid % 8)) = vf0;         \
+  } while (0)
+  // the lane's outputs: rows trow + g * 4 + q, q < 4, column tcol + lane % 16; a row's whole fours
+  int nb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = trow + g * 4 + q, t = min(t0 + r / mul, last);
+    nb[q] = ((pos0 + t + 1) & ~3) >> 2;
+  }
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const v16f zero = {};
+  if (chunks > 0) {
+    PV_FETCH(0);
+    PV_STAGE(0);
+  }
+  __syncthreads();
+  for (int c = 0; c < chunks; ++c) {
+    const bool more = c + 1 < chunks;  // uniform
+    if (more) PV_FETCH(c + 1);
+    const float *pb = ps[c & 1] + (trow + l16) * LDP + g, *vb = vs[c & 1] + (tcol + l16) * LDP + g;
+    const int b0 = c * (TPC / 4);  // the chunk's first four, from position 0
+    if ((c + 1) * TPC <= least4) {  // every row of the block adds every four of the chunk (uniform)
+#pragma unroll
+      for (int k = 0; k < TPC / 4; ++k) {
+        const v16f d = __builtin_amdgcn_mfma_f32_16x16x1f32(pb[4 * k], vb[4 * k], zero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = acc[q] + ((d[q] + d[4 + q]) + (d[8 + q] + d[12 + q]));
+        pin4(acc);
+      }
+    } else {  // each row adds the fours below its own last whole four (the fours past most4: staged, never added)
+#pragma unroll
+      for (int k = 0; k < TPC / 4; ++k) {
+        const v16f d = __builtin_amdgcn_mfma_f32_16x16x1f32(pb[4 * k], vb[4 * k], zero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float sum = acc[q] + ((d[q] + d[4 + q]) + (d[8 + q] + d[12 + q]));
+          acc[q] = b0 + k < nb[q] ? sum : acc[q];
+        }
+        pin4(acc);
+      }
+    }
+    if (more) {
+      PV_STAGE((c + 1) & 1);  // the other buffer: its last readers passed the previous barrier
+      __syncthreads();
+    }
+  }
+#undef PV_FETCH
+#undef PV_STAGE
+  // each row's positions past its fours, one at a time, then the outputs
+  const int col = j0 + tcol + l16;
+  const int64_t vcol = (int64_t)(kh * HS + col) * a.vstride;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = trow + g * 4 + q, tt = r / mul, t = t0 + tt;
+    if (tt >= tt_n || t >= a.m) continue;
+    const int count = pos0 + t + 1, hh = kh * mul + r % mul;
+    const float *pt = a.scores + ((int64_t)t * a.nh + hh) * a.seq_len;
+    float o = acc[q];
+    for (int p = count & ~3; p < count; ++p) o = o + pt[p] * cache1<HALF>(a.vcache, vcol + p);
+    a.out[(int64_t)t * a.out_stride + hh * HS + col] = o;
+  }
+}
 
 template <int HS, bool HALF>
 hipError_t scores_tokens_hs(const AttnArgs &a, hipStream_t s) {
@@ -334,9 +350,9 @@ hipError_t softmax_pv_hs(const AttnArgs &a, hipStream_t s) {
     }
   }
   hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
-  constexpr int COLS = HS % 32 == 0 ? 32 : 16;
-  const int tt = 2 * std::max(1, 256 / COLS / (a.nh / a.nkv));  // tokens a block: two sums a thread
-  hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / COLS, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
+  constexpr int C = pv_cols<HS>();
+  const int tt = std::max(1, (1024 / C) / (a.nh / a.nkv));  // tokens a block
+  hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / C, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
