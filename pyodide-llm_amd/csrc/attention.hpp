@@ -39,5 +39,6 @@ constexpr int ALDS = 160 * 1024 - 256;  // LDS a block may take (gfx950: 160 KiB
 hipError_t launch_scores_tokens(const AttnArgs &a, hipStream_t s);
 hipError_t launch_softmax_pv(const AttnArgs &a, hipStream_t s);
 size_t softmax_lds(int count);
+size_t softmax4_lds(int count);
 
 }  // namespace ple

@@ -200,6 +200,59 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
   }
 }
 
+// (B') one wave a (token, head) row, four rows (heads h4 * 4 ..) a block: grid (ceil(nh / 4), m), block 256. The same
+// steps as (B) inside one wave (its largest, the exponentials into the wave's own LDS rows, the four ordered sums by
+// four of its lanes, the weights), with no block barrier: a row takes a wave, not a block, so more rows share a CU
+// while their sums run. For contexts whose four rows of exponentials fit the LDS (softmax4_lds).
+__global__ __launch_bounds__(256) void softmax4_kernel(const AttnArgs a) {
+  extern __shared__ float e4all[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x * 4 + wave, t = blockIdx.y;
+  if (h >= a.nh) return;  // (uniform over the wave; no block barrier follows)
+  const int count = first_position(a) + t + 1, count4 = count & ~3, q4 = count4 >> 2, q4s = chain_rowstride(q4);
+  float *e4 = e4all + wave * (4 * q4s + 4), *tail = e4 + 4 * q4s;
+  float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
+  // the largest score, from the lowest finite float32 (order-free): lane maxima, rotations inside 16-lane rows
+  // (DPP), the four rows' values by readlane
+  float lm = -3.4028234663852886e38f;
+  for (int i = lane; i < count; i += 64) lm = wmax(lm, scores[i]);
+  {
+    int src = __float_as_int(lm);
+    lm = wmax(lm, __int_as_float(__builtin_amdgcn_update_dpp(src, src, 0x128, 0xF, 0xF, false)));  // row_ror:8
+    src = __float_as_int(lm);
+    lm = wmax(lm, __int_as_float(__builtin_amdgcn_update_dpp(src, src, 0x124, 0xF, 0xF, false)));  // row_ror:4
+    src = __float_as_int(lm);
+    lm = wmax(lm, __int_as_float(__builtin_amdgcn_update_dpp(src, src, 0x122, 0xF, 0xF, false)));  // row_ror:2
+    src = __float_as_int(lm);
+    lm = wmax(lm, __int_as_float(__builtin_amdgcn_update_dpp(src, src, 0x121, 0xF, 0xF, false)));  // row_ror:1
+    src = __float_as_int(lm);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(src, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(src, 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(src, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(src, 48));
+    lm = wmax(wmax(r0, r1), wmax(r2, r3));
+  }
+  const float mx = lm;
+  for (int i = lane; i < count; i += 64) {
+    const float d = scores[i] - mx;
+    if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
+    else tail[i - count4] = fexp(d);
+  }
+  wave_sync_lds();
+  float part = 0.0f;
+  if (lane < 4) part = lds_chain(e4 + lane * q4s, q4, 0.0f);
+  // ((l0 + l1) + l2) + l3, then the tail in order (every lane computes it from the four lanes' sums)
+  const float p0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0));
+  const float p1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 1));
+  const float p2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 2));
+  const float p3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 3));
+  float sum = ((p0 + p1) + p2) + p3;
+  for (int i = 0; i < count - count4; ++i) sum = sum + tail[i];
+  const float inv = 1.0f / sum;
+  for (int i = lane; i < count; i += 64) {
+    const float e = i < count4 ? e4[(i & 3) * q4s + (i >> 2)] : tail[i - count4];
+    scores[i] = e * inv;
+  }
+}
+
 // (C) for many tokens (a prompt block), products on the matrix core: v_mfma_f32_16x16x1_4b_f32 with a zero
 // accumulator makes 4 x 16 x 16 single products, block b of the four being position 4k + b: p[row][4k + b] *
 // v[4k + b][col], each the correctly rounded float32 product. A lane then holds, for each of its 4 (row, column)
@@ -349,7 +402,21 @@ hipError_t softmax_pv_hs(const AttnArgs &a, hipStream_t s) {
       sized = true;
     }
   }
-  hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
+  const size_t lds4 = softmax4_lds(a.pos0 + a.m);
+  if (lds4 <= (size_t)ALDS) {
+    if (lds4 > 64 * 1024) {
+      static bool sized4 = false;  // once a process: let the kernel take LDS past 64 KiB
+      if (!sized4) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&softmax4_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, ALDS);
+        if (e != hipSuccess) return e;
+        sized4 = true;
+      }
+    }
+    hipLaunchKernelGGL(softmax4_kernel, dim3((a.nh + 3) / 4, a.m), dim3(256), lds4, s, a);
+  } else {
+    hipLaunchKernelGGL(softmax_kernel, dim3(a.nh, a.m), dim3(256), lds_b, s, a);
+  }
   constexpr int C = pv_cols<HS>();
   const int tt = std::max(1, (1024 / C) / (a.nh / a.nkv));  // tokens a block
   hipLaunchKernelGGL((pv_tokens_kernel<HS, HALF>), dim3(HS / C, a.nkv, (a.m + tt - 1) / tt), dim3(256), 0, s, a);
@@ -388,6 +455,8 @@ hipError_t softmax_pv_by_hs(const AttnArgs &a, hipStream_t s) {
 }  // namespace
 
 size_t softmax_lds(int count) { return sizeof(float) * (size_t)(4 * chain_rowstride((count & ~3) / 4) + 4); }
+// four rows of softmax_lds (softmax4_kernel)
+size_t softmax4_lds(int count) { return 4 * softmax_lds(count); }
 
 hipError_t launch_scores_tokens(const AttnArgs &a, hipStream_t s) {
   return a.half ? scores_tokens_by_hs<true>(a, s) : scores_tokens_by_hs<false>(a, s);
