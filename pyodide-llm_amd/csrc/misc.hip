@@ -132,6 +132,41 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(int8_t *xq, float *xs
   quantize_group(o, xq + (int64_t)t * xq_stride, xs + (int64_t)t * xs_stride, j, g, bias);
 }
 
+// the same, four values a lane (float4 loads, four bytes stored at once): a group of 32 is 8 lanes, its largest
+// magnitude by the lanes' own maxima and three DPP steps (xor 1, xor 2, the mirror across the two quads), so that the
+// group's scale and its reciprocal are computed by 8 lanes instead of 32. For rows whose strides keep the vectors
+// aligned (launch_swiglu_quant checks).
+__global__ __launch_bounds__(256) void swiglu_quant4_kernel(int8_t *xq, float *xs, float *out, const float *h1,
+                                                            const float *h3, int32_t m, int32_t n, int32_t h_stride,
+                                                            int32_t xq_stride, int32_t xs_stride, int32_t bias) {
+  const int groups = n / GS;
+  const int64_t gid = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  if (gid >= (int64_t)m * groups) return;  // (whole 8-lane groups leave together)
+  const int t = (int)(gid / groups), g = (int)(gid % groups), j = g * GS + 4 * (threadIdx.x & 7);
+  const float4 v = *reinterpret_cast<const float4 *>(h1 + (int64_t)t * h_stride + j);
+  const float4 w = *reinterpret_cast<const float4 *>(h3 + (int64_t)t * h_stride + j);
+  float4 o;
+  o.x = v.x / (1.0f + vexp(-v.x)) * w.x;
+  o.y = v.y / (1.0f + vexp(-v.y)) * w.y;
+  o.z = v.z / (1.0f + vexp(-v.z)) * w.z;
+  o.w = v.w / (1.0f + vexp(-v.w)) * w.w;
+  if (out) *reinterpret_cast<float4 *>(out + (int64_t)t * h_stride + j) = o;
+  // quantize_x of the group (common.hpp quantize_group, over 8 lanes)
+  float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(o.x), __builtin_fabsf(o.y)),
+                            __builtin_fmaxf(__builtin_fabsf(o.z), __builtin_fabsf(o.w)));
+  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, true)));
+  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, true)));
+  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x141, 0xF, 0xF, true)));
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  const float scale = a / qmax;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  const uint32_t q = (uint32_t)(uint8_t)quant_value(o.x, inv, bias) | ((uint32_t)(uint8_t)quant_value(o.y, inv, bias) << 8) |
+                     ((uint32_t)(uint8_t)quant_value(o.z, inv, bias) << 16) |
+                     ((uint32_t)(uint8_t)quant_value(o.w, inv, bias) << 24);
+  *reinterpret_cast<uint32_t *>(xq + (int64_t)t * xq_stride + j) = q;
+  if ((threadIdx.x & 7) == 0) xs[(int64_t)t * xs_stride + g] = scale;
+}
+
 // valueAt (public/forward.js:672-696): f32(int8 or unpacked int6 value * the scale of its group)
 __device__ __forceinline__ float value_at(const uint8_t *table, const float *scales, int64_t at, int32_t group,
                                           int32_t six) {
@@ -352,8 +387,15 @@ hipError_t launch_swiglu_quant(int8_t *xq, float *xs, float *out, const float *h
                                int32_t n, int32_t h_stride, int32_t xq_stride, int32_t xs_stride, int32_t bias,
                                hipStream_t s) {
   const int64_t groups = (int64_t)m * (n / GS);
-  hipLaunchKernelGGL(swiglu_quant_kernel, dim3(blocks_for(groups, 8)), dim3(256), 0, s, xq, xs, out, h1, h3, m, n,
-                     h_stride, xq_stride, xs_stride, bias);
+  const bool aligned = h_stride % 4 == 0 && xq_stride % 4 == 0 && reinterpret_cast<uintptr_t>(h1) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(h3) % 16 == 0 && reinterpret_cast<uintptr_t>(xq) % 4 == 0 &&
+                       (!out || reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  if (aligned)
+    hipLaunchKernelGGL(swiglu_quant4_kernel, dim3(blocks_for(groups, 32)), dim3(256), 0, s, xq, xs, out, h1, h3, m, n,
+                       h_stride, xq_stride, xs_stride, bias);
+  else
+    hipLaunchKernelGGL(swiglu_quant_kernel, dim3(blocks_for(groups, 8)), dim3(256), 0, s, xq, xs, out, h1, h3, m, n,
+                       h_stride, xq_stride, xs_stride, bias);
   return hipGetLastError();
 }
 
