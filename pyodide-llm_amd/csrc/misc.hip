@@ -132,10 +132,39 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(int8_t *xq, float *xs
   quantize_group(o, xq + (int64_t)t * xq_stride, xs + (int64_t)t * xs_stride, j, g, bias);
 }
 
-// the same, four values a lane (float4 loads, four bytes stored at once): a group of 32 is 8 lanes, its largest
-// magnitude by the lanes' own maxima and three DPP steps (xor 1, xor 2, the mirror across the two quads), so that the
-// group's scale and its reciprocal are computed by 8 lanes instead of 32. For rows whose strides keep the vectors
-// aligned (launch_swiglu_quant checks).
+// quantize_x of one group of 32 held four values a lane by its 8 lanes (aligned, all present): the largest magnitude
+// by the lanes' own maxima and three DPP steps (xor 1, xor 2, the mirror across the two quads), the scale and its
+// reciprocal as quantize_group computes them, four bytes stored at xq[j..j+3]
+__device__ __forceinline__ void quantize_group4(float4 o, int8_t *xq, float *xs, int j, int g, int32_t bias) {
+  float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(o.x), __builtin_fabsf(o.y)),
+                            __builtin_fmaxf(__builtin_fabsf(o.z), __builtin_fabsf(o.w)));
+  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, true)));
+  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, true)));
+  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x141, 0xF, 0xF, true)));
+  const float qmax = bias == 0 ? 127.0f : 63.0f;
+  const float scale = a / qmax;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  const uint32_t q = (uint32_t)(uint8_t)quant_value(o.x, inv, bias) | ((uint32_t)(uint8_t)quant_value(o.y, inv, bias) << 8) |
+                     ((uint32_t)(uint8_t)quant_value(o.z, inv, bias) << 16) |
+                     ((uint32_t)(uint8_t)quant_value(o.w, inv, bias) << 24);
+  *reinterpret_cast<uint32_t *>(xq + j) = q;
+  if ((threadIdx.x & 7) == 0) xs[g] = scale;
+}
+
+// the same as quantize_kernel four values a lane (rows whose strides keep the vectors aligned)
+__global__ __launch_bounds__(256) void quantize4_kernel(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n,
+                                                        int32_t x_stride, int32_t xq_stride, int32_t xs_stride,
+                                                        int32_t bias) {
+  const int groups = n / GS;
+  const int64_t gid = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  if (gid >= (int64_t)m * groups) return;  // whole 8-lane groups leave together
+  const int t = (int)(gid / groups), g = (int)(gid % groups), j = g * GS + 4 * (threadIdx.x & 7);
+  quantize_group4(*reinterpret_cast<const float4 *>(x + (int64_t)t * x_stride + j), xq + (int64_t)t * xq_stride,
+                  xs + (int64_t)t * xs_stride, j, g, bias);
+}
+
+// swiglu_quant_kernel four values a lane (float4 loads, quantize_group4): a group's scale and its reciprocal are
+// computed by 8 lanes instead of 32. For rows whose strides keep the vectors aligned (launch_swiglu_quant checks).
 __global__ __launch_bounds__(256) void swiglu_quant4_kernel(int8_t *xq, float *xs, float *out, const float *h1,
                                                             const float *h3, int32_t m, int32_t n, int32_t h_stride,
                                                             int32_t xq_stride, int32_t xs_stride, int32_t bias) {
@@ -151,20 +180,7 @@ __global__ __launch_bounds__(256) void swiglu_quant4_kernel(int8_t *xq, float *x
   o.z = v.z / (1.0f + vexp(-v.z)) * w.z;
   o.w = v.w / (1.0f + vexp(-v.w)) * w.w;
   if (out) *reinterpret_cast<float4 *>(out + (int64_t)t * h_stride + j) = o;
-  // quantize_x of the group (common.hpp quantize_group, over 8 lanes)
-  float a = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(o.x), __builtin_fabsf(o.y)),
-                            __builtin_fmaxf(__builtin_fabsf(o.z), __builtin_fabsf(o.w)));
-  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, true)));
-  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, true)));
-  a = __builtin_fmaxf(a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x141, 0xF, 0xF, true)));
-  const float qmax = bias == 0 ? 127.0f : 63.0f;
-  const float scale = a / qmax;
-  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
-  const uint32_t q = (uint32_t)(uint8_t)quant_value(o.x, inv, bias) | ((uint32_t)(uint8_t)quant_value(o.y, inv, bias) << 8) |
-                     ((uint32_t)(uint8_t)quant_value(o.z, inv, bias) << 16) |
-                     ((uint32_t)(uint8_t)quant_value(o.w, inv, bias) << 24);
-  *reinterpret_cast<uint32_t *>(xq + (int64_t)t * xq_stride + j) = q;
-  if ((threadIdx.x & 7) == 0) xs[(int64_t)t * xs_stride + g] = scale;
+  quantize_group4(o, xq + (int64_t)t * xq_stride, xs + (int64_t)t * xs_stride, j, g, bias);
 }
 
 // valueAt (public/forward.js:672-696): f32(int8 or unpacked int6 value * the scale of its group)
@@ -366,8 +382,14 @@ int blocks_for(int64_t items, int64_t per_block, int64_t cap = 1 << 20) {
 hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n, int32_t x_stride,
                            int32_t xq_stride, int32_t xs_stride, int32_t bias, hipStream_t s) {
   const int64_t groups = (int64_t)m * (n / GS);
-  hipLaunchKernelGGL(quantize_kernel, dim3(blocks_for(groups, 8)), dim3(256), 0, s, xq, xs, x, m, n, x_stride,
-                     xq_stride, xs_stride, bias);
+  const bool aligned = x_stride % 4 == 0 && xq_stride % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(xq) % 4 == 0;
+  if (aligned)
+    hipLaunchKernelGGL(quantize4_kernel, dim3(blocks_for(groups, 32)), dim3(256), 0, s, xq, xs, x, m, n, x_stride,
+                       xq_stride, xs_stride, bias);
+  else
+    hipLaunchKernelGGL(quantize_kernel, dim3(blocks_for(groups, 8)), dim3(256), 0, s, xq, xs, x, m, n, x_stride,
+                       xq_stride, xs_stride, bias);
   return hipGetLastError();
 }
 
