@@ -226,6 +226,47 @@ def test_long_decode_attention(name, half_kv, attend, monkeypatch):
     eng.release()
 
 
+PROMPT_HEADS = {
+    # every head size the prompt kernels take, with 1, 2, 4 and 8 query heads a kv head: the score kernel's 32- or
+    # 16-dimension chunks and its token rows a block (64 / heads a kv head), the weighted-value kernel's 32- or
+    # 16-column tiles
+    "hs16_mul8": dict(dim=256, hidden_dim=64, n_heads=16, n_kv_heads=2, head_size=16),
+    "hs48_mul1": dict(dim=96, hidden_dim=64, n_heads=2, n_kv_heads=2, head_size=48),
+    "hs64_mul2": dict(dim=128, hidden_dim=64, n_heads=2, n_kv_heads=1, head_size=64),
+    "hs96_mul2": dict(dim=192, hidden_dim=64, n_heads=2, n_kv_heads=1, head_size=96),
+    "hs128_mul4": dict(dim=256, hidden_dim=64, n_heads=4, n_kv_heads=1, head_size=128),
+    "hs256_mul2": dict(dim=512, hidden_dim=64, n_heads=4, n_kv_heads=2, head_size=256),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PROMPT_HEADS))
+@pytest.mark.parametrize("half_kv", [0, 1])
+def test_prompt_kernels_every_head_size(name, half_kv):
+    """prompt blocks of more than 8 tokens (the score, softmax and weighted-value kernels of many tokens a launch),
+    a second block starting past the first's 64-position tiles and ragged ends, then decode steps: the cache (the
+    second layer's keys and values carry every prompt token's first-layer attention) and the logits against the
+    oracle to the bit"""
+    cfg = ol.config(**{**PROMPT_HEADS[name], "n_layers": 2, "vocab_size": 320, "seq_len": 200,
+                       "shared_classifier": 1, "half_kv": half_kv})
+    tensors, size = ol.places(cfg)
+    ck = ol.synth_checkpoint(cfg, tensors, size, seed=13)
+    cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, 10000.0)
+    tokens = [int(t) for t in np.random.default_rng(14).integers(0, cfg.vocab_size, size=175)]
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=100)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=100)
+    for at, end in ((0, 93), (93, 171)):
+        eng.forwardMany(tokens[at:end], at)
+        ref.run(tokens[at:end], at, False)
+    kv, (k, v) = eng.keysAndValues(0, 171), ref.kv(0, 171)
+    assert same_bits(kv["keys"], k.reshape(-1)) and same_bits(kv["values"], v.reshape(-1))
+    for pos in range(171, 175):
+        eng.forward(tokens[pos], pos, True)
+        ref.run([tokens[pos]], pos, True)
+        assert same_bits(eng.logits(), ref.logits()), pos
+    eng.release()
+
+
 @pytest.mark.parametrize("piece", [3, 5, 8])
 def test_prompt_in_small_pieces_equals_one_at_a_time(piece):
     """prompt pieces of up to 8 tokens run the decode attention with several tokens a launch"""
