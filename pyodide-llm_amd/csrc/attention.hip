@@ -504,7 +504,22 @@ bool attention_quantizes(const AttnArgs &a) {
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
   if (!attention_supported(a.hs, a.nh, a.nkv)) return hipErrorInvalidValue;
-  return a.half ? launch_half<true>(a, s) : launch_half<false>(a, s);
+  // pieces of equal size (each past DECODE_TOKENS when m is past ATTN_ROWS), one after another on the stream
+  const int pieces = a.dpos ? 1 : (a.m + ATTN_ROWS - 1) / ATTN_ROWS, size = (a.m + pieces - 1) / pieces;
+  for (int at = 0; at < a.m; at += size) {
+    AttnArgs p = a;
+    p.q = a.q + (int64_t)at * a.q_stride;
+    p.out = a.out + (int64_t)at * a.out_stride;
+    p.pos0 = a.pos0 + at;
+    p.m = std::min(size, a.m - at);
+    if (p.xq) {
+      p.xq = a.xq + (int64_t)at * a.xq_stride;
+      p.xs = a.xs + (int64_t)at * a.xs_stride;
+    }
+    const hipError_t e = a.half ? launch_half<true>(p, s) : launch_half<false>(p, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace ple

@@ -138,8 +138,8 @@ struct AttnArgs {
   const void *kcache, *vcache;  // keys [seq_len][kv_dim] (a position's row), values [kv_dim][vstride] (a column's)
   float *out;
   int32_t out_stride;
-  float *scores;  // [m][nh][seq_len]
-  float *tilemax; // [m][nh][seq_len / 64 + 1]
+  float *scores;  // [min(m, ATTN_ROWS)][nh][seq_len]
+  float *tilemax; // [min(m, ATTN_ROWS)][nh][seq_len / 64 + 1]
   int32_t nh, nkv, hs, pos0, m, seq_len, half, vstride;
   // the first position in device memory (a replayed decode step), or null: pos0; with it, pos0 is only the largest
   // first position the launch may see (grid and LDS sizes)
@@ -151,6 +151,10 @@ struct AttnArgs {
   // decode launches take the prompt's separate softmax and weighted-value kernels, as past the fused kernel's LDS
   int32_t split;
 };
+// a launch of more tokens runs them in pieces of at most ATTN_ROWS that reuse the score rows: a piece's score matrix
+// (ATTN_ROWS x nh x its context, 134 MB at 32 heads and 2048 positions) written and read back through the 256 MB
+// MALL, where a whole 1024- or 2048-token pass's would spill to HBM
+constexpr int32_t ATTN_ROWS = 512;
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 // the head sizes and grouping the attention kernels take (hs in {16, 32, 48, 64, 96, 128, 256}, nh / nkv <= 8)
 bool attention_supported(int32_t hs, int32_t nh, int32_t nkv);
