@@ -11,12 +11,13 @@
 // every (row, token, group), so the kernel is bound by the VALU, not by the MFMA pipe: one MFMA a group a tile against
 // 64 VALU instructions.
 //
-// Tiling: a block of 256 threads (4 waves, one a SIMD) makes 64 rows x 64 tokens; each K step stages 4 groups (128
+// Tiling: a block of 256 threads (4 waves, one a SIMD) makes 64 rows x 128 tokens; each K step stages 4 groups (128
 // bytes of K: one group for each lane chain) of the block's weights, activations (centred: q - 64) and scales in LDS,
-// double buffered: the next step's global loads are in flight while the current one is computed. A wave makes one
-// 32 x 32 MFMA tile: 4 chains x 16 accumulators a lane. The register and LDS footprint lets three blocks share a CU,
-// so that while one block waits at its barrier or for its MFMA results the others' float32 work fills the VALU (with
-// one block of 8 waves a CU, every barrier and every MFMA latency left the VALU idle).
+// double buffered: the next step's global loads are in flight while the current one is computed. A wave makes two
+// 32 x 32 MFMA tiles side by side (32 rows x 64 tokens: the weight operand and the 16 row scales a lane read once for
+// both): 2 x 4 chains x 16 accumulators a lane, two waves a SIMD (two blocks a CU). Two tiles a wave at two waves a
+// SIMD issue this pattern's float32 work faster than one tile a wave at three (measured: 14.3k against 10.1k group
+// tiles a µs), the two tiles' independent instructions filling what one wave's dependent ones leave idle.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -24,9 +25,8 @@ namespace ple {
 namespace {
 
 constexpr int BR = 64;             // weight rows a block
-constexpr int BT = 64;             // tokens a block
-constexpr int NT = 256;            // threads a block: 2 x 2 waves of 32 x 32 tiles
-constexpr int NB = 2;              // MFMAs issued together before their float32 work
+constexpr int BT = 128;            // tokens a block
+constexpr int NT = 256;            // threads a block: 2 x 2 waves of 32 rows x 64 tokens
 constexpr int KS = 4;              // groups a K step: one for each lane chain
 constexpr int ROWB = KS * 32 + 16; // LDS bytes of one row of a stage (128 and 16 of padding against bank conflicts)
 
@@ -53,13 +53,14 @@ __device__ __forceinline__ SegRow seg_row(const MatArgs &a, int row) {
 }
 
 // what one thread loads of a K step: one (row, group) of the weights (int8: 32 bytes; int6: the 24-byte group) with its
-// scale, one (token, group) of the activations with its scale. Registers between the global load and the LDS store.
+// scale, two (token, group)s of the activations (tokens rt and rt + 64) with their scales. Registers between the
+// global load and the LDS store.
 template <bool SIX>
 struct Fetch {
   uint32_t w[SIX ? 6 : 8];
   float wsv;
-  uint4 x[2];
-  float xsv;
+  uint4 x[4];
+  float xsv[2];
 };
 
 template <bool SIX, bool SUMS>
@@ -79,12 +80,13 @@ __device__ __forceinline__ void fetch(Fetch<SIX> &f, const MatArgs &a, int r0, i
     f.w[4] = v1.x; f.w[5] = v1.y; f.w[6] = v1.z; f.w[7] = v1.w;
   }
   f.wsv = SUMS ? 0.0f : s.ws[(int64_t)s.r * G + g];
-  {
-    const int t = min(t0 + (tid >> 2), a.m - 1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = min(t0 + h * 64 + (tid >> 2), a.m - 1);
     const uint4 *p = reinterpret_cast<const uint4 *>(a.xq + (int64_t)t * a.xq_stride + (int64_t)g * 32);
-    f.x[0] = p[0];
-    f.x[1] = p[1];
-    f.xsv = SUMS ? 0.0f : a.xs[(int64_t)t * a.xs_stride + g];
+    f.x[2 * h] = p[0];
+    f.x[2 * h + 1] = p[1];
+    f.xsv[h] = SUMS ? 0.0f : a.xs[(int64_t)t * a.xs_stride + g];
   }
 }
 
@@ -105,10 +107,13 @@ __device__ __forceinline__ void store(Stage &st, const Fetch<SIX> &f, int tid) {
     d[1] = {f.w[4], f.w[5], f.w[6], f.w[7]};
   }
   st.ws[gi * BR + rt] = f.wsv;
-  uint4 *e = reinterpret_cast<uint4 *>(st.b + rt * ROWB + gi * 32);
-  e[0] = centre16(f.x[0]);
-  e[1] = centre16(f.x[1]);
-  st.xs[gi * BT + rt] = f.xsv;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint4 *e = reinterpret_cast<uint4 *>(st.b + (h * 64 + rt) * ROWB + gi * 32);
+    e[0] = centre16(f.x[2 * h]);
+    e[1] = centre16(f.x[2 * h + 1]);
+    st.xs[gi * BT + h * 64 + rt] = f.xsv[h];
+  }
 }
 
 // The MFMA's accumulator starts at MAGIC (the bits of 1.5 * 2^23), so that it ends at MAGIC + S_g: for |S_g| < 2^22
@@ -118,16 +123,20 @@ __device__ __forceinline__ void store(Stage &st, const Fetch<SIX> &f, int tid) {
 constexpr int MAGIC = 0x4B400000;
 constexpr float MAGIC_F = 12582912.0f;
 
-// p = f32(S) * f32(ws * xs) for the 16 outputs of a lane in one MFMA tile (R = MAGIC + S): rows (v / 4) * 8 +
-// (lane / 32) * 4 + v % 4 of the tile, the token lane % 32
-__device__ __forceinline__ void products(const v16i &R, const float *ws_rows, float xsv, float p[16]) {
+// acc += f32(S) * f32(ws * xs) for the 16 outputs of a lane in each of its two MFMA tiles (R = MAGIC + S): rows
+// (v / 4) * 8 + (lane / 32) * 4 + v % 4 of the tiles, the tokens lane % 32 (x0) and 32 + lane % 32 (x1)
+__device__ __forceinline__ void products2(const v16i &R0, const v16i &R1, const float *ws_rows, float x0, float x1,
+                                          float (&acc0)[16], float (&acc1)[16]) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const float4 w4 = *reinterpret_cast<const float4 *>(ws_rows + q * 8);
-    p[q * 4 + 0] = (__int_as_float(R[q * 4 + 0]) - MAGIC_F) * (w4.x * xsv);
-    p[q * 4 + 1] = (__int_as_float(R[q * 4 + 1]) - MAGIC_F) * (w4.y * xsv);
-    p[q * 4 + 2] = (__int_as_float(R[q * 4 + 2]) - MAGIC_F) * (w4.z * xsv);
-    p[q * 4 + 3] = (__int_as_float(R[q * 4 + 3]) - MAGIC_F) * (w4.w * xsv);
+    const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = q * 4 + i;
+      acc0[v] = acc0[v] + (__int_as_float(R0[v]) - MAGIC_F) * (w[i] * x0);
+      acc1[v] = acc1[v] + (__int_as_float(R1[v]) - MAGIC_F) * (w[i] * x1);
+    }
   }
 }
 
@@ -151,12 +160,12 @@ __device__ __forceinline__ void write_sums(const MatArgs &a, const v16i &S, int 
 }
 
 // with SUMS the kernel writes the exact int32 group sums S_g to a.sums [m][rows][G] instead (one segment)
-// (three waves a SIMD: the register budget that keeps the MFMA results in VGPRs, no AGPR copies)
+// (two waves a SIMD: the register budget that keeps the MFMA results in VGPRs, no AGPR copies)
 template <bool SIX, bool SUMS>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void gemm_kernel(const MatArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(const MatArgs a) {
   __shared__ Stage stage[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave & 1, wt = wave >> 1;  // the wave's 32 rows and 32 tokens of the block
+  const int wr = wave & 1, wt = wave >> 1;  // the wave's 32 rows and 64 tokens of the block
   // block b runs on XCD b % 8; the (row block, token block) pairs, row-block major, are dealt to the XCDs in 8
   // contiguous ranges, so that the token blocks of one row block run one after another on one XCD and its weights
   // come from that XCD's L2 after the first (dealt round-robin, every XCD would read every row block's weights)
@@ -166,21 +175,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void ge
   const int r0 = (idx / tbn) * BR, t0 = (idx % tbn) * BT;
   const int G = a.k / 32, G4 = G & ~3, steps = G4 / KS, tail = G - G4;
 
-  float acc[KS][16];
+  float acc[2][KS][16];
 #pragma unroll
-  for (int c = 0; c < KS; ++c)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[c][v] = 0.0f;
+    for (int c = 0; c < KS; ++c)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[h][c][v] = 0.0f;
   // the accumulators' start: 0 for the group sums themselves, MAGIC for the float32 path (products)
   const int c0 = SUMS ? 0 : MAGIC;
   const v16i start = {c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0, c0};
 
-  // the operands of this lane in a stage: weights row wr*32 + lane%32, activations token wt*32 + lane%32, 16 bytes
-  // of each group at (lane / 32) * 16 (A and B take the same k bytes, so the sum is the group's)
+  // the operands of this lane in a stage: weights row wr*32 + lane%32, activations tokens wt*64 + lane%32 and 32 later,
+  // 16 bytes of each group at (lane / 32) * 16 (A and B take the same k bytes, so the sum is the group's)
   const int a_off = (wr * 32 + (lane & 31)) * ROWB + (lane >> 5) * 16;
-  const int b_off = (wt * 32 + (lane & 31)) * ROWB + (lane >> 5) * 16;
+  const int b_off = (wt * 64 + (lane & 31)) * ROWB + (lane >> 5) * 16;
   const int ws_off = wr * 32 + (lane >> 5) * 4;
-  const int xs_off = wt * 32 + (lane & 31);
+  const int xs_off = wt * 64 + (lane & 31);
 
   Fetch<SIX> f;
   const int total = steps + (tail ? 1 : 0);
@@ -195,36 +206,30 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void ge
     // below the stores): its groups are clamped into the row, and past the last stage what it stores goes to the
     // buffer no later read takes (the tail's stage is a real one: total > steps)
     fetch<SIX, SUMS>(f, a, r0, t0, (s + 1) * KS, G, tid);
-    // NB MFMAs issued together, then their float32 work: each group's products start as its MFMA ends while the
-    // later ones still run (and the other blocks of the CU use the VALU meanwhile)
+    // a group's two MFMAs issued together, then their float32 work
 #pragma unroll
-    for (int g0 = 0; g0 < KS; g0 += NB) {
-      v16i S[NB];
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + (g0 + u) * 32);
-        const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + (g0 + u) * 32);
-        S[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, start, 0, 0, 0);
-      }
+    for (int gi = 0; gi < KS; ++gi) {
+      const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
+      const v4i b0 = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
+      const v4i b1 = *reinterpret_cast<const v4i *>(st.b + b_off + 32 * ROWB + gi * 32);
+      const v16i S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, start, 0, 0, 0);
+      const v16i S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, start, 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const int gi = g0 + u;
-        if constexpr (SUMS) {
-          write_sums(a, S[u], r0 + wr * 32, t0 + wt * 32, s * KS + gi, G, lane);
-        } else {
-          float p[16];
-          products(S[u], st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[gi][v] = acc[gi][v] + p[v];
-        }
+      if constexpr (SUMS) {
+        write_sums(a, S0, r0 + wr * 32, t0 + wt * 64, s * KS + gi, G, lane);
+        write_sums(a, S1, r0 + wr * 32, t0 + wt * 64 + 32, s * KS + gi, G, lane);
+      } else {
+        products2(S0, S1, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], st.xs[gi * BT + xs_off + 32], acc[0][gi],
+                  acc[1][gi]);
       }
     }
     // the next stage's stores wait for its global loads: kept after the products (the compiler would move them,
     // and their waits, above the float32 work that hides the loads' latency)
     if constexpr (!SUMS) {
 #pragma unroll
-      for (int c = 0; c < KS; ++c) pin16(acc[c]);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int c = 0; c < KS; ++c) pin16(acc[h][c]);
       asm volatile("" ::: "memory");
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -233,51 +238,57 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(3))) void ge
   }
 
   // ((l0 + l1) + l2) + l3, then the tail groups in order
-  float out[16];
+  float out[2][16];
 #pragma unroll
-  for (int v = 0; v < 16; ++v) out[v] = ((acc[0][v] + acc[1][v]) + acc[2][v]) + acc[3][v];
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) out[h][v] = ((acc[h][0][v] + acc[h][1][v]) + acc[h][2][v]) + acc[h][3][v];
   if (tail) {
     const Stage &st = stage[steps & 1];
 #pragma unroll
     for (int gi = 0; gi < KS - 1; ++gi) {
       if (gi < tail) {
         const v4i av = *reinterpret_cast<const v4i *>(st.a + a_off + gi * 32);
-        const v4i bv = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
-        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, start, 0, 0, 0);
+        const v4i b0 = *reinterpret_cast<const v4i *>(st.b + b_off + gi * 32);
+        const v4i b1 = *reinterpret_cast<const v4i *>(st.b + b_off + 32 * ROWB + gi * 32);
+        const v16i S0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b0, start, 0, 0, 0);
+        const v16i S1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, b1, start, 0, 0, 0);
         if constexpr (SUMS) {
-          write_sums(a, S, r0 + wr * 32, t0 + wt * 32, G4 + gi, G, lane);
+          write_sums(a, S0, r0 + wr * 32, t0 + wt * 64, G4 + gi, G, lane);
+          write_sums(a, S1, r0 + wr * 32, t0 + wt * 64 + 32, G4 + gi, G, lane);
         } else {
-          float p[16];
-          products(S, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], p);
-#pragma unroll
-          for (int v = 0; v < 16; ++v) out[v] = out[v] + p[v];
+          products2(S0, S1, st.ws + gi * BR + ws_off, st.xs[gi * BT + xs_off], st.xs[gi * BT + xs_off + 32], out[0],
+                    out[1]);
         }
       }
     }
   }
 
   if constexpr (SUMS) return;
-  // y[t][r] = out (or y + out): the lane's token, its 16 rows in 4 runs of 4
-  const int t = t0 + wt * 32 + (lane & 31);
-  if (t >= a.m) return;
+  // y[t][r] = out (or y + out): the lane's two tokens, its 16 rows in 4 runs of 4
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int row = r0 + wr * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-    if (row >= a.total_rows) continue;
-    const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
-    int si = 0, r = row;
-    if (a.nseg > 2 && row >= n0 + n1) {
-      si = 2;
-      r = row - n0 - n1;
-    } else if (a.nseg > 1 && row >= n0) {
-      si = 1;
-      r = row - n0;
+  for (int h = 0; h < 2; ++h) {
+    const int t = t0 + wt * 64 + h * 32 + (lane & 31);
+    if (t >= a.m) continue;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int row = r0 + wr * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      if (row >= a.total_rows) continue;
+      const int n0 = a.seg[0].rows, n1 = a.seg[1].rows;
+      int si = 0, r = row;
+      if (a.nseg > 2 && row >= n0 + n1) {
+        si = 2;
+        r = row - n0 - n1;
+      } else if (a.nseg > 1 && row >= n0) {
+        si = 1;
+        r = row - n0;
+      }
+      float *y = (si == 2 ? a.seg[2].y : si == 1 ? a.seg[1].y : a.seg[0].y);
+      const int stride = (si == 2 ? a.seg[2].y_stride : si == 1 ? a.seg[1].y_stride : a.seg[0].y_stride);
+      const int accumulate = (si == 2 ? a.seg[2].accumulate : si == 1 ? a.seg[1].accumulate : a.seg[0].accumulate);
+      float *dst = y + (int64_t)t * stride + r;
+      *dst = accumulate ? *dst + out[h][v] : out[h][v];
     }
-    float *y = (si == 2 ? a.seg[2].y : si == 1 ? a.seg[1].y : a.seg[0].y);
-    const int stride = (si == 2 ? a.seg[2].y_stride : si == 1 ? a.seg[1].y_stride : a.seg[0].y_stride);
-    const int accumulate = (si == 2 ? a.seg[2].accumulate : si == 1 ? a.seg[1].accumulate : a.seg[0].accumulate);
-    float *dst = y + (int64_t)t * stride + r;
-    *dst = accumulate ? *dst + out[v] : out[v];
   }
 }
 
