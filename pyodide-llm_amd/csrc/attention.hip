@@ -35,6 +35,11 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
   const int kvdim = a.nkv * HS, mul = a.nh / a.nkv;
   const int np = min(TILE, count - p0);
   constexpr int NL = (TILE * C4 + 255) / 256;  // float4 of keys a thread, requested together
+  constexpr int NQ = (MAXMUL * C4 + 255) / 256;  // float4 of the queries a thread, requested with them
+  const float *q = a.q + (int64_t)t * a.q_stride + (int64_t)kh * mul * HS;
+  float4 qr[NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) qr[u] = *reinterpret_cast<const float4 *>(q + 4 * min((int)threadIdx.x + u * 256, mul * C4 - 1));
   float4 kr4[NL];
 #pragma unroll
   for (int u = 0; u < NL; ++u) {
@@ -42,13 +47,15 @@ __global__ __launch_bounds__(256) void scores_kernel(const AttnArgs a) {
     kr4[u] = cache4<HALF>(a.kcache, (int64_t)(p0 + p) * kvdim + kh * HS + 4 * c);
   }
 #pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int i = threadIdx.x + u * 256;
+    if (i < mul * C4) *reinterpret_cast<float4 *>(qs + 4 * i) = qr[u];
+  }
+#pragma unroll
   for (int u = 0; u < NL; ++u) {
     const int i = threadIdx.x + u * 256, p = i / C4, c = i % C4;
     if (p < np) *reinterpret_cast<float4 *>(ks + p * LD + 4 * c) = kr4[u];
   }
-  const float *q = a.q + (int64_t)t * a.q_stride + (int64_t)kh * mul * HS;
-  for (int i = threadIdx.x; i < mul * C4; i += 256)
-    *reinterpret_cast<float4 *>(qs + 4 * i) = *reinterpret_cast<const float4 *>(q + 4 * i);
   __syncthreads();
   const float isq = 1.0f / __builtin_sqrtf((float)HS);
   float *scores = a.scores + (int64_t)t * a.nh * a.seq_len;
