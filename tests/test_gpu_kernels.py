@@ -79,7 +79,8 @@ def test_int8_decode_bits(k, rows):
     assert same_bits(gl.matmul(xq, xs, w, ws, rows, k, 64, 0), ol.matmul(xq, xs, w, ws, rows, k, 64, 0))
 
 
-GEMM_CASES = [(k, rows, m) for k in (32, 96, 288, 1056, 4096) for rows, m in ((37, 9), (64, 130), (130, 200))]
+GEMM_CASES = [(k, rows, m) for k in (32, 96, 288, 1056, 4096)
+              for rows, m in ((37, 9), (64, 96), (37, 128), (64, 130), (130, 200))]
 
 
 @pytest.mark.parametrize("six", [0, 1])
