@@ -53,18 +53,21 @@ export function weightsMemory(size, { shared = false } = {}) {
 }
 
 /** footprint (public/forward.js:270): the bytes the forward pass holds besides the checkpoint. Here they are device
- * bytes: the keys and values of the whole context (no growth steps), the RoPE tables, one prompt block's activations
- * and scores, the logits. header: [dim, hidden, layers, heads, kvHeads, signedVocab, seqLen] as the file's. */
-export function footprint(header, size, { halfKV = false, head_dim = 0, promptBlock = PROMPT_BLOCK } = {}) {
+ * bytes: the keys and values of the whole context (no growth steps), the RoPE tables, one pass's activations (up to
+ * 1024 prompt tokens with relaxed matmuls, 16 without) and the scores of up to 512 of its tokens (the attention's
+ * pieces), the logits and the sampler's buffers. header: [dim, hidden, layers, heads, kvHeads, signedVocab, seqLen] as the file's. */
+export function footprint(header, size, { relaxed = true, halfKV = false, head_dim = 0, promptBlock = PROMPT_BLOCK } = {}) {
   const [dim, hidden, layers, heads, kvHeads, signedVocab, seqLen] = header;
   const vocab = Math.abs(signedVocab), headSize = head_dim || dim / heads;
   const kvDim = kvHeads * headSize, qDim = heads * headSize, wide = Math.max(dim, qDim, hidden);
   const half = halfKV && kvHeads >= heads;
   // keys by position, values by column (each column's positions rounded up to 64)
   const keys = layers * (seqLen + Math.ceil(seqLen / 64) * 64) * kvDim * (half ? 2 : 4);
-  const chunk = Math.min(promptBlock, 16);
-  const frames = chunk * (4 * (2 * dim + qDim + 2 * kvDim + 2 * hidden) + wide + wide / 8 + 4 * heads * seqLen);
-  return keys + 2 * seqLen * headSize * 2 + frames + vocab * 4 + 2 ** 20;
+  const chunk = Math.min(promptBlock, relaxed ? 1024 : 16), rows = Math.min(chunk, 512);
+  const frames = chunk * (4 * (dim + Math.max(dim, qDim) + qDim + 2 * kvDim + 2 * hidden) + wide + wide / 8) +
+    rows * 4 * heads * (seqLen + Math.floor(seqLen / 64) + 1);
+  // the logits, the sampler's probabilities and indices; 1 MiB for the small buffers and the regions' alignment
+  return keys + 2 * seqLen * headSize * 2 + frames + vocab * 12 + 2 ** 20;
 }
 
 /** keysInHalf (public/forward.js:326): float16 keys and values where every head has its own (a grouped-query model's

@@ -47,6 +47,8 @@ write("values.bin", kv.values);
 const history = [1, ...prompt, ...ids];
 const sampled = engine.generateMany(token, pos, history.slice(-64), history.length, 2, 0.8, 0.9, 1.3, [0.5, 0.25], []);
 const memoryBytes = engine.memoryBytes();
+const footprint = F.footprint(Array.from(new Int32Array(header.buffer, header.byteOffset, 7)), job.size,
+  { relaxed: job.relaxed, halfKV: !!plan.half_kv, promptBlock: engine.promptBlock });
 
 // one token at a time through forward(), the logits of the last into the bound array
 const second = outside.start(plan);
@@ -87,6 +89,6 @@ addon.close(raw);
 
 Promise.all([engine.release(), second.release()]).then((released) => {
   console.log(JSON.stringify({ ids, backend: engine.backend, promptBlock: engine.promptBlock, tokenBlock: engine.tokenBlock,
-    memoryBytes, sampled: sampled === undefined ? null : Array.from(sampled), released, threw, short,
+    memoryBytes, footprint, sampled: sampled === undefined ? null : Array.from(sampled), released, threw, short,
     header: Array.from(header) }));
 });

@@ -96,3 +96,5 @@ def test_node_host_matches_the_oracle(name, tmp_path):
     assert out["short"] == ["TypeError"] * 4  # the addon refuses output arrays shorter than it writes
     assert out["header"] == list(ck[:28])
     assert out["memoryBytes"] > size
+    # footprint() (public/forward.js:270) bounds what the engine holds besides the checkpoint, to within 2 MiB
+    assert size + out["footprint"] >= out["memoryBytes"] > size + out["footprint"] - (2 << 20)
