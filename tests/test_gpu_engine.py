@@ -267,6 +267,31 @@ def test_prompt_kernels_every_head_size(name, half_kv):
     eng.release()
 
 
+@pytest.mark.parametrize("name", ["hs16_mul8", "hs256_mul2"])
+def test_prompt_pass_in_attention_pieces(name):
+    """a 1090-token prompt: a pass of 1024 tokens whose attention runs as two pieces of 512 that reuse the score rows,
+    then a pass of 66; the cache and the decode steps after it against the oracle to the bit"""
+    cfg = ol.config(**{**PROMPT_HEADS[name], "n_layers": 2, "vocab_size": 320, "seq_len": 1200,
+                       "shared_classifier": 1})
+    tensors, size = ol.places(cfg)
+    ck = ol.synth_checkpoint(cfg, tensors, size, seed=15)
+    cos, sin = ol.rope_tables(cfg.seq_len, cfg.head_size, 10000.0)
+    tokens = [int(t) for t in np.random.default_rng(16).integers(0, cfg.vocab_size, size=1094)]
+    pk = package()
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=1100)
+    assert eng.promptBlock == 1100
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=1100)
+    eng.forwardMany(tokens[:1090], 0)
+    ref.run(tokens[:1090], 0, False)
+    kv, (k, v) = eng.keysAndValues(0, 1090), ref.kv(0, 1090)
+    assert same_bits(kv["keys"], k.reshape(-1)) and same_bits(kv["values"], v.reshape(-1))
+    for pos in range(1090, 1094):
+        eng.forward(tokens[pos], pos, True)
+        ref.run([tokens[pos]], pos, True)
+        assert same_bits(eng.logits(), ref.logits()), pos
+    eng.release()
+
+
 @pytest.mark.parametrize("piece", [3, 5, 8])
 def test_prompt_in_small_pieces_equals_one_at_a_time(piece):
     """prompt pieces of up to 8 tokens run the decode attention with several tokens a launch"""
