@@ -151,6 +151,82 @@ __device__ __forceinline__ void quantize_group4(float4 o, int8_t *xq, float *xs,
   if ((threadIdx.x & 7) == 0) xs[g] = scale;
 }
 
+// rmsnorm + quantize_x of many tokens (a prompt pass), one token a block of 256 threads: the same steps and order as
+// rmsnorm_quant_kernel, with each of the four ordered sums of squares in one wave's registers (lane s holds the sum's
+// values 16 s .. 16 s + 15, zeros past the count; round s starts every lane from the running sum and hands lane s's
+// result on as a scalar), so that eight tokens share a CU (the 1024-thread blocks of rmsnorm_quant_kernel left
+// fourteen of their sixteen waves idle through the sums). Rows of whole groups of 32, at most 4096 values.
+constexpr int RT_SEG = 16;              // values a lane of a sum
+constexpr int RT_LANE = RT_SEG + 4;     // floats a lane's segment takes in LDS: 16-byte reads of 16 lanes on distinct banks
+constexpr int RT_ROW = 64 * RT_LANE;    // floats a sum's row
+constexpr int RT_MOST = 4 * 64 * RT_SEG;  // values a token at most
+constexpr int RT_TOKENS = 8;            // tokens a launch from which rmsnorm_tokens_kernel takes it
+__global__ __launch_bounds__(256) void rmsnorm_tokens_kernel(int8_t *xq, float *xs, float *out, const float *x,
+                                                             const float *w, int32_t n, int32_t x_stride,
+                                                             int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
+                                                             float eps, int32_t bias) {
+  __shared__ float sq[4 * RT_ROW];
+  __shared__ float part[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q4 = n >> 2, nseg = (q4 + RT_SEG - 1) / RT_SEG;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x + (int64_t)t * x_stride);
+  const float4 *w4 = reinterpret_cast<const float4 *>(w);
+  // float4 j4 = tid + 256 u of the token and of the weights, requested at once (clamped: loaded, never used past q4)
+  float4 xr[4], wr[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int j4 = min(tid + 256 * u, q4 - 1);
+    xr[u] = x4[j4];
+    wr[u] = w4[j4];
+  }
+  // the squares into the four sums' rows (sum k: x[4 j4 + k]^2 as its value j4), zeros up to the last whole segment
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int j4 = tid + 256 * u, at = (j4 / RT_SEG) * RT_LANE + j4 % RT_SEG;
+    if (j4 < q4) {
+      sq[at] = xr[u].x * xr[u].x;
+      sq[RT_ROW + at] = xr[u].y * xr[u].y;
+      sq[2 * RT_ROW + at] = xr[u].z * xr[u].z;
+      sq[3 * RT_ROW + at] = xr[u].w * xr[u].w;
+    } else if (j4 < nseg * RT_SEG) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sq[k * RT_ROW + at] = 0.0f;
+    }
+  }
+  __syncthreads();
+  {
+    // wave k: sum k over its lanes' segments (lanes past the last read the first; what they add is never used)
+    const float4 *seg = reinterpret_cast<const float4 *>(sq + wave * RT_ROW + (lane < nseg ? lane : 0) * RT_LANE);
+    const float4 v0 = seg[0], v1 = seg[1], v2 = seg[2], v3 = seg[3];
+    float run = 0.0f;
+    for (int r = 0; r < nseg; ++r) {
+      float acc = run;
+      acc = acc + v0.x; acc = acc + v0.y; acc = acc + v0.z; acc = acc + v0.w;
+      acc = acc + v1.x; acc = acc + v1.y; acc = acc + v1.z; acc = acc + v1.w;
+      acc = acc + v2.x; acc = acc + v2.y; acc = acc + v2.z; acc = acc + v2.w;
+      acc = acc + v3.x; acc = acc + v3.y; acc = acc + v3.z; acc = acc + v3.w;
+      run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), r));
+    }
+    if (lane == 0) part[wave] = run;
+  }
+  __syncthreads();
+  // ((l0 + l1) + l2) + l3 (no tail: n % 4 == 0), s = f32(1 / f32(sqrt(f32(ss / n) + eps))), by every thread
+  const float ss = ((part[0] + part[1]) + part[2]) + part[3];
+  const float sv = 1.0f / __builtin_sqrtf(ss / (float)n + eps);
+  int8_t *q = xq + (int64_t)t * xq_stride;
+  float *sc = xs + (int64_t)t * xs_stride;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int j4 = tid + 256 * u;
+    if (j4 < q4) {  // whole groups of 32: the 8 lanes of a group take this branch together
+      const float4 o = make_float4(wr[u].x * (sv * xr[u].x), wr[u].y * (sv * xr[u].y), wr[u].z * (sv * xr[u].z),
+                                   wr[u].w * (sv * xr[u].w));
+      if (out) *reinterpret_cast<float4 *>(out + (int64_t)t * out_stride + 4 * j4) = o;
+      quantize_group4(o, q, sc, 4 * j4, j4 >> 3, bias);
+    }
+  }
+}
+
 // the same as quantize_kernel four values a lane (rows whose strides keep the vectors aligned)
 __global__ __launch_bounds__(256) void quantize4_kernel(int8_t *xq, float *xs, const float *x, int32_t m, int32_t n,
                                                         int32_t x_stride, int32_t xq_stride, int32_t xs_stride,
@@ -396,6 +472,14 @@ hipError_t launch_quantize(int8_t *xq, float *xs, const float *x, int32_t m, int
 hipError_t launch_rmsnorm_quant(int8_t *xq, float *xs, float *out, const float *x, const float *w, int32_t m,
                                 int32_t n, int32_t x_stride, int32_t xq_stride, int32_t xs_stride, int32_t out_stride,
                                 float eps, int32_t bias, hipStream_t s, const L2Fetch *fetch) {
+  const bool aligned = x_stride % 4 == 0 && xq_stride % 4 == 0 && (!out || out_stride % 4 == 0) &&
+                       reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(xq) % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  if (m >= RT_TOKENS && n % GS == 0 && n <= RT_MOST && aligned) {
+    hipLaunchKernelGGL(rmsnorm_tokens_kernel, dim3(m), dim3(256), 0, s, xq, xs, out, x, w, n, x_stride, xq_stride,
+                       xs_stride, out_stride, eps, bias);
+    return hipGetLastError();
+  }
   const size_t lds = sizeof(float) * (size_t)(2 * n + 4 * norm_rowstride((n & ~3) >> 2) + 16);
   // one token: 4 blocks share its groups (more tokens fill the chip by themselves)
   const int split = m < 64 ? 4 : 1;
