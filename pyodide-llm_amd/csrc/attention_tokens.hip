@@ -204,6 +204,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const AttnArgs a) {
 // steps as (B) inside one wave (its largest, the exponentials into the wave's own LDS rows, the four ordered sums by
 // four of its lanes, the weights), with no block barrier: a row takes a wave, not a block, so more rows share a CU
 // while their sums run. For contexts whose four rows of exponentials fit the LDS (softmax4_lds).
+constexpr int SM4_HELD = 32;  // scores a lane holds (rows of up to 2048 positions read once)
 __global__ __launch_bounds__(256) void softmax4_kernel(const AttnArgs a) {
   extern __shared__ float e4all[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -214,8 +215,16 @@ __global__ __launch_bounds__(256) void softmax4_kernel(const AttnArgs a) {
   float *scores = a.scores + ((int64_t)t * a.nh + h) * a.seq_len;
   // the largest score, from the lowest finite float32 (order-free): lane maxima, rotations inside 16-lane rows
   // (DPP), the four rows' values by readlane
+  // the row's first 64 * SM4_HELD scores held in registers from the maximum's pass to the exponentials' (a uniform
+  // test a load, so that a short row requests only what it has)
+  float held[SM4_HELD];
+#pragma unroll
+  for (int u = 0; u < SM4_HELD; ++u) held[u] = 64 * u < count ? scores[min(lane + 64 * u, count - 1)] : 0.0f;
   float lm = -3.4028234663852886e38f;
-  for (int i = lane; i < count; i += 64) lm = wmax(lm, scores[i]);
+#pragma unroll
+  for (int u = 0; u < SM4_HELD; ++u)
+    if (64 * u < count) lm = wmax(lm, held[u]);  // a clamped copy of the last score changes no maximum
+  for (int i = lane + 64 * SM4_HELD; i < count; i += 64) lm = wmax(lm, scores[i]);
   {
     int src = __float_as_int(lm);
     lm = wmax(lm, __int_as_float(__builtin_amdgcn_update_dpp(src, src, 0x128, 0xF, 0xF, false)));  // row_ror:8
@@ -231,7 +240,16 @@ __global__ __launch_bounds__(256) void softmax4_kernel(const AttnArgs a) {
     lm = wmax(wmax(r0, r1), wmax(r2, r3));
   }
   const float mx = lm;
-  for (int i = lane; i < count; i += 64) {
+#pragma unroll
+  for (int u = 0; u < SM4_HELD; ++u) {
+    const int i = lane + 64 * u;
+    if (i < count) {
+      const float d = held[u] - mx;
+      if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
+      else tail[i - count4] = fexp(d);
+    }
+  }
+  for (int i = lane + 64 * SM4_HELD; i < count; i += 64) {
     const float d = scores[i] - mx;
     if (i < count4) e4[(i & 3) * q4s + (i >> 2)] = vexp(d);
     else tail[i - count4] = fexp(d);
