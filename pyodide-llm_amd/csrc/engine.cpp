@@ -420,7 +420,8 @@ int32_t open_common(const he_config *cfg, const he_tensor *tensors, uint64_t siz
   e->size = size;
   e->max_block = max_block;
   // the tokens of one pass through the layers: a prompt block up to 1024 (the attention runs them in pieces of
-  // ATTN_ROWS; measured at the 8B shape: 512 a pass 19.5k prompt tok/s, 1024 19.6k, 2048 18.5k)
+  // ATTN_ROWS; measured at the 8B shape: 512 a pass 19.5k prompt tok/s, 1024 19.6k, 2048 18.5k; with the two-tile
+  // GEMM 1024 20.5k, 2048 0.3% more for twice the activations)
   e->chunk = std::min(max_block, e->c.relaxed ? 1024 : 16);
   HIP_TRY(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
   if ((rc = plan_regions(e))) return rc;
