@@ -647,22 +647,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   float *wsl = xsl + G16 + wave * R * G16;             // this wave's rows' weight scales
   float *P = xsl + G16 + WAVES * R * G16 + wave * R * lay.stride;  // this wave's products
   const int row0 = min((blockIdx.x * WAVES + wave) * R, a.total_rows - 1);
+  // every load of the block, in the order their uses come: the token's activations and their scales (staged first),
+  // the rows' scales, the rows; unconditional loads from clamped (always valid) addresses (the staging waits only for
+  // the first, and each wave step only for its own rows)
+  constexpr int XL = (NS * 4096 / 16 + 255) / 256;
+  constexpr int XSV = (NS * 128 + 255) / 256;
+  uint4 xv[XL];
+  float sv[XSV];
+#pragma unroll
+  for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
+#pragma unroll
+  for (int u = 0; u < XSV; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
   uint4 wr[R][NS][3];
   float4 sr[R][SV];
+  const uint8_t *wrow[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const RowAt at = row_at(a, min(row0 + i, a.total_rows - 1));  // rows past the end: the last again, unused
-    const uint8_t *w = at.w + (int64_t)at.r * G * 24;
+    wrow[i] = at.w + (int64_t)at.r * G * 24;
     const float *ws = at.ws + (int64_t)at.r * G;
-    // unconditional loads from clamped (always valid) addresses: groups 2 * pair and 2 * pair + 1 of the step
-#pragma unroll
-    for (int u = 0; u < NS; ++u) {
-      const int pair = min(u * 64 + lane, (G - 2) >> 1);  // G is even where it matters; an odd G's last pair clamps
-      const uint4 *p = reinterpret_cast<const uint4 *>(w + (int64_t)pair * 48);
-      wr[i][u][0] = p[0];
-      wr[i][u][1] = p[1];
-      wr[i][u][2] = p[2];
-    }
 #pragma unroll
     for (int u = 0; u < SV; ++u) {
       const int f = min(4 * (lane + 64 * u), G16 - 4);
@@ -673,27 +676,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       }
     }
   }
+  // groups 2 * pair and 2 * pair + 1 of each wave step
+#pragma unroll
+  for (int u = 0; u < NS; ++u)
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int pair = min(u * 64 + lane, (G - 2) >> 1);  // G is even where it matters; an odd G's last pair clamps
+      const uint4 *p = reinterpret_cast<const uint4 *>(wrow[i] + (int64_t)pair * 48);
+      wr[i][u][0] = p[0];
+      wr[i][u][1] = p[1];
+      wr[i][u][2] = p[2];
+    }
   __builtin_amdgcn_sched_barrier(0);
-  {
-    constexpr int XL = (NS * 4096 / 16 + 255) / 256;
-    uint4 xv[XL];
-    float sv[SV * 4 / 4 + 1];
 #pragma unroll
-    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
+  for (int u = 0; u < XL; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    if (i < K / 16)
+      reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
+                                                    centre4(xv[u].w));
+  }
 #pragma unroll
-    for (int u = 0; u < SV * 4 / 4 + 1; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
-#pragma unroll
-    for (int u = 0; u < XL; ++u) {
-      const int i = threadIdx.x + 256 * u;
-      if (i < K / 16)
-        reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
-                                                      centre4(xv[u].w));
-    }
-#pragma unroll
-    for (int u = 0; u < SV * 4 / 4 + 1; ++u) {
-      const int i = threadIdx.x + 256 * u;
-      if (i < G) xsl[i] = sv[u];
-    }
+  for (int u = 0; u < XSV; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    if (i < G) xsl[i] = sv[u];
   }
 #pragma unroll
   for (int i = 0; i < R; ++i)
@@ -769,6 +774,7 @@ hipError_t launch_decode6(const MatArgs &a, hipStream_t s) {
   if (steps <= 1) return launch_gemv6<4, 1>(a, s);
   if (steps <= 2) return launch_gemv6<2, 2>(a, s);
   if (steps <= 4) return launch_gemv6<1, 4>(a, s);
+  if (steps <= 5) return launch_gemv6<1, 5>(a, s);
   if (steps <= 6) return launch_gemv6<1, 6>(a, s);
   return hipErrorInvalidValue;
 }
