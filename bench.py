@@ -41,6 +41,9 @@ TRAFFIC = {
     "llama3-8b": {"bytes_per_pass": round((2 * (32 * (13900 + 9304 + 64600 + 32500) + 288700)
                                            + (32 * (48.63 + 16 + 112 + 32) + 502.3)) * 1024),
                   "source": "profiles/decode_gemv_llama3-8b.md"},
+    "qwen25-7b-int6": {"bytes_per_pass": round((2 * (28 * (7172 + 5580 + 58120 + 29260) + 233000)
+                                                + (28 * (30.32 + 14 + 148.1 + 28) + 594.6)) * 1024),
+                       "source": "profiles/decode_gemv6_qwen25-7b-int6.md"},
 }
 
 MODELS = {
@@ -312,7 +315,13 @@ def brief(rec):
         out["roofline"] = {"bound": "hbm", "achieved": round(rec["gemv"]["gb_s"], 1), "peak": HBM_PEAK_GBS,
                            "unit": "GB/s", "frac": round(rec["gemv"]["gb_s"] / HBM_PEAK_GBS, 4),
                            "kernel": "decode GEMV on int6 rows (every matmul of a decode step, m = 1, back to back)",
-                           "bytes_per_weight": 0.875}
+                           "bytes_per_weight": 0.875,
+                           "launches_per_pass": int(rec["gemv"]["launches_per_pass"]),
+                           "us_per_launch": round(1e3 * rec["gemv"]["ms_per_pass"] / rec["gemv"]["launches_per_pass"], 3)}
+        traffic = TRAFFIC.get(rec["model"])
+        if traffic:
+            out["roofline"]["traffic"] = round(traffic["bytes_per_pass"] / rec["gemv"]["launches_per_pass"])
+            out["roofline"]["traffic_source"] = traffic["source"]
     else:
         out["note"] = ("the weights fit the 256 MB MALL: effective_gb_s is the step's matmul bytes at the decode rate "
                        "(cache-resident, not an HBM figure)")
