@@ -634,8 +634,12 @@ __global__ __launch_bounds__(64 * PW) void gemvp_kernel(const MatArgs a) {
 // gemv1_kernel, with a lane taking two consecutive groups of 24 bytes (48 bytes, three 16-byte loads) of each of its
 // wave's R rows, 128 groups a wave step, widened to int8 in registers (kernels/six.ts) next to their use.
 // NS: wave steps, NS * 128 groups >= K / 32.
-template <int R, int NS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv6_kernel(const MatArgs a) {
+// SRC: 0 the activations from xq / xs; 1 the float32 token (a.xf); 2 a.xf after rmsnorm with a.xnorm
+// W: waves a block (the float32 token's blocks take 16, so that quantize_x of the token is 4 values a thread)
+template <int R, int NS, int SRC, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 4))) void gemv6_kernel(const MatArgs a) {
+  constexpr bool F32 = SRC != 0;
+  constexpr int NT = 64 * W;
   constexpr int SV = (NS * 128 + 255) / 256;  // float4 of a row's scales a lane
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -645,19 +649,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   uint32_t *xl = reinterpret_cast<uint32_t *>(smem);   // K bytes of centred activations
   float *xsl = smem + K / 4;                           // G scales of the activations
   float *wsl = xsl + G16 + wave * R * G16;             // this wave's rows' weight scales
-  float *P = xsl + G16 + WAVES * R * G16 + wave * R * lay.stride;  // this wave's products
-  const int row0 = min((blockIdx.x * WAVES + wave) * R, a.total_rows - 1);
+  float *P = xsl + G16 + W * R * G16 + wave * R * lay.stride;  // this wave's products
+  const int row0 = min((blockIdx.x * W + wave) * R, a.total_rows - 1);
   // every load of the block, in the order their uses come: the token's activations and their scales (staged first),
   // the rows' scales, the rows; unconditional loads from clamped (always valid) addresses (the staging waits only for
   // the first, and each wave step only for its own rows)
-  constexpr int XL = (NS * 4096 / 16 + 255) / 256;
-  constexpr int XSV = (NS * 128 + 255) / 256;
+  constexpr int XL = (NS * 4096 / 16 + NT - 1) / NT;
+  constexpr int XSV = (NS * 128 + NT - 1) / NT;
+  constexpr int FU = F32 ? (NS * 4096 + NT - 1) / NT : 1;
   uint4 xv[XL];
   float sv[XSV];
+  float fx[FU], fw[FU];
+  if constexpr (F32) {
+    static_assert(NS == 1, "the float32 token is held a thread at a time");
+    load_f32<FU, SRC == 2, NT>(a, fx, fw);
+  } else {
 #pragma unroll
-  for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + 256 * u, K / 16 - 1)];
+    for (int u = 0; u < XL; ++u) xv[u] = reinterpret_cast<const uint4 *>(a.xq)[min((int)threadIdx.x + NT * u, K / 16 - 1)];
 #pragma unroll
-  for (int u = 0; u < XSV; ++u) sv[u] = a.xs[min((int)threadIdx.x + 256 * u, G - 1)];
+    for (int u = 0; u < XSV; ++u) sv[u] = a.xs[min((int)threadIdx.x + NT * u, G - 1)];
+  }
   uint4 wr[R][NS][3];
   float4 sr[R][SV];
   const uint8_t *wrow[R];
@@ -688,17 +699,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       wr[i][u][2] = p[2];
     }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (F32) {
+    stage_from_f32<FU, SRC == 2, NT>(a, fx, fw, reinterpret_cast<uint8_t *>(xl), xsl, P - wave * R * lay.stride);
+  } else {
 #pragma unroll
-  for (int u = 0; u < XL; ++u) {
-    const int i = threadIdx.x + 256 * u;
-    if (i < K / 16)
-      reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
-                                                    centre4(xv[u].w));
-  }
+    for (int u = 0; u < XL; ++u) {
+      const int i = threadIdx.x + NT * u;
+      if (i < K / 16)
+        reinterpret_cast<uint4 *>(xl)[i] = make_uint4(centre4(xv[u].x), centre4(xv[u].y), centre4(xv[u].z),
+                                                      centre4(xv[u].w));
+    }
 #pragma unroll
-  for (int u = 0; u < XSV; ++u) {
-    const int i = threadIdx.x + 256 * u;
-    if (i < G) xsl[i] = sv[u];
+    for (int u = 0; u < XSV; ++u) {
+      const int i = threadIdx.x + NT * u;
+      if (i < G) xsl[i] = sv[u];
+    }
   }
 #pragma unroll
   for (int i = 0; i < R; ++i)
@@ -708,7 +723,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
     }
   __syncthreads();
-  if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
+  if ((blockIdx.x * W + wave) * R >= a.total_rows) return;  // (after the block's barrier)
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     if (u < steps) {
@@ -758,20 +773,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   store_row(a, row0 + lane, sum, lane < R && row0 + lane < a.total_rows);
 }
 
-template <int R, int NS>
+template <int R, int NS, int W = WAVES>
 hipError_t launch_gemv6(const MatArgs &a, hipStream_t s) {
+  if (a.xf && (NS > 1 || a.k % 32)) return hipErrorInvalidValue;
   const int waves = (a.total_rows + R - 1) / R;
-  const int blocks = (waves + WAVES - 1) / WAVES;
+  const int blocks = (waves + W - 1) / W;
   const size_t g16 = ((a.k / GS) + 3) & ~3;
-  const size_t lds = (size_t)a.k + sizeof(float) * g16 * (1 + WAVES * R) +
-                     sizeof(float) * WAVES * R * (size_t)row_layout(a.k, true).stride;
-  hipLaunchKernelGGL((gemv6_kernel<R, NS>), dim3(blocks), dim3(64 * WAVES), lds, s, a);
+  const size_t head = (size_t)a.k + sizeof(float) * g16 * (1 + W * R);
+  size_t products = sizeof(float) * W * R * (size_t)row_layout(a.k, true).stride;
+  if (a.xf) products = std::max(products, sizeof(float) * 4 * (size_t)chain_rowstride(a.k / 4));  // the squares
+  const size_t lds = head + products;
+  if constexpr (NS == 1) {
+    if (a.xf) {
+      if (a.xnorm) hipLaunchKernelGGL((gemv6_kernel<R, NS, 2, W>), dim3(blocks), dim3(64 * W), lds, s, a);
+      else hipLaunchKernelGGL((gemv6_kernel<R, NS, 1, W>), dim3(blocks), dim3(64 * W), lds, s, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((gemv6_kernel<R, NS, 0, W>), dim3(blocks), dim3(64 * W), lds, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_decode6(const MatArgs &a, hipStream_t s) {
   const int steps = (a.k / GS + 127) / 128;  // 3 KiB steps of a row
-  if (steps <= 1) return launch_gemv6<4, 1>(a, s);
+  // the float32 token: 16 rows a block as the 4 waves of 4 rows, but 16 waves of one row (8 of two where the q/k/v
+  // epilogue takes rows in pairs), so that quantize_x of the token is 4 values a thread
+  if (steps <= 1) {
+    if (!a.xf) return launch_gemv6<4, 1>(a, s);
+    return a.qkv.on ? launch_gemv6<2, 1, 8>(a, s) : launch_gemv6<1, 1, 16>(a, s);
+  }
+  if (a.xf) return hipErrorInvalidValue;
   if (steps <= 2) return launch_gemv6<2, 2>(a, s);
   if (steps <= 4) return launch_gemv6<1, 4>(a, s);
   if (steps <= 5) return launch_gemv6<1, 5>(a, s);
@@ -923,7 +954,11 @@ int32_t gemv_tokens(int32_t k, bool relaxed) {
   return m < 1 ? 0 : (m > 8 ? 8 : m);
 }
 
-bool decode_takes_f32(int32_t k, bool six, bool relaxed) { return !six && relaxed && k <= 4 * 1024 && k % 32 == 0; }
+bool decode_takes_f32(int32_t k, bool six, bool relaxed) {
+  // int8 rows up to 4 KiB; int6 rows of one wave step (an even count of groups, up to 128)
+  if (six) return relaxed && k <= 4 * 1024 && k % 64 == 0;
+  return relaxed && k <= 4 * 1024 && k % 32 == 0;
+}
 
 bool decode_persistent(int32_t k, bool six, bool relaxed) { return !six && relaxed && k > 1024 && k <= 4 * 1024; }
 
