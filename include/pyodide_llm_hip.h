@@ -109,7 +109,9 @@ const char *he_last_error(void);
 
 /* start(plan) (public/forward.js:571-590, createForward :626): uploads `size` bytes of checkpoint (host memory) to the
  * device, the RoPE tables plan.derived.freq_cis_real/imag ([seq_len][head_size/2] float32, host), and makes the
- * KV cache for the whole context. max_block: the most tokens one he_forward_many call takes (promptBlock). */
+ * KV cache for the whole context. max_block: the most tokens one he_forward_many call takes (promptBlock).
+ * seq_len may be at most 40,704 positions (HE_E_ARG past it): a (token, head)'s exponentials are held in one
+ * workgroup's 160 KiB of LDS for their ordered sum (kernels/kernel.ts:499-520). */
 int32_t he_open(const he_config *cfg, const he_tensor *tensors, const void *checkpoint, uint64_t size,
                 const float *rope_cos, const float *rope_sin, int32_t max_block, he_engine **out);
 
@@ -230,12 +232,13 @@ int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t coun
 int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
                   void *stream);
 
-/* No counterpart in the reference: hk_sample for callers that cannot allocate device memory (code under HIP graph
- * capture, serving loops and harnesses that forbid hipMalloc). The same draw as hk_sample, token for token, with the
+/* No counterpart in the reference: hk_sample for callers that cannot allocate device memory (serving loops and
+ * harnesses that forbid hipMalloc). The same draw as hk_sample, token for token, with the
  * sampler's scratch (n probabilities and n token indices, the token and the largest logit) in a static device array of
  * the library, which every GPU it runs on holds until the process ends; n <= HK_SAMPLE_STATIC_MOST, else HE_E_ARG.
  * It allocates nothing. Every call on one GPU uses that GPU's one array: calls that overlap on one GPU (two streams,
- * two threads) race, and the caller must order them. Blocks until done. */
+ * two threads) race, and the caller must order them. Blocks until done: it copies the token to the host and waits
+ * for the stream, so a stream under graph capture is refused (HE_E_ARG) before anything is launched. */
 #define HK_SAMPLE_STATIC_MOST 262144
 int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
                          void *stream);

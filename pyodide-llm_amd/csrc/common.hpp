@@ -236,6 +236,15 @@ __device__ __forceinline__ float chain4_registers(const float *base, int stride,
   return chain32_registers(base + (tid >> 5) * stride, 32, tid & 31);
 }
 
+// a barrier of the workgroup over its LDS only: each wave's LDS accesses complete first (lgkmcnt), but not its global
+// loads in flight, which a barrier with a workgroup fence of every address space waits for (on gfx9 one counter,
+// vmcnt, holds a wave's loads and stores alike). No global store before it may be read after it by another wave.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();

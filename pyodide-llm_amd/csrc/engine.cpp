@@ -1406,10 +1406,15 @@ int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float
   if (!logits || !token || n < 1 || !(temperature > 0.0f)) return fail(HE_E_ARG, "hk_sample_static: bad arguments");
   if (n > HK_SAMPLE_STATIC_MOST)
     return fail(HE_E_ARG, "hk_sample_static takes at most HK_SAMPLE_STATIC_MOST (262144) logits");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // the token comes back to the host and the stream is waited for: neither may be recorded into a graph
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(s, &capture));
+  if (capture != hipStreamCaptureStatusNone)
+    return fail(HE_E_ARG, "hk_sample_static: the stream is under graph capture (the token is copied to the host)");
   uint8_t *base = nullptr;
   const int32_t rc = sample_scratch(&base);
   if (rc) return rc;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int32_t *out = reinterpret_cast<int32_t *>(base + SAMPLE_TOKEN_AT);
   HIP_TRY(launch_sample(reinterpret_cast<const float *>(logits), n, temperature, topp, random,
                         reinterpret_cast<float *>(base), reinterpret_cast<int32_t *>(base + SAMPLE_INDEX_AT), out,

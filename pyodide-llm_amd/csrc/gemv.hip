@@ -270,11 +270,11 @@ __device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&x
       const int j = tid + NT * u;
       if (j < K) sq[(j & 3) * qs + (j >> 2)] = xv[u] * xv[u];
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) sval = 1.0f / __builtin_sqrtf((((part[0] + part[1]) + part[2]) + part[3]) / (float)K + a.eps);
-    __syncthreads();
+    lds_barrier();
     sc = sval;
   }
   // every group's maximum, scale and values computed unconditionally (positions past K repeat the last one and are
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       const int f = 4 * (lane + 64 * u);
       if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
     }
-  __syncthreads();
+  lds_barrier();
   if ((blockIdx.x * WAVES + wave) * R >= a.total_rows) return;  // (after the block's barrier)
   // fully unrolled (no early exit), so that wr stays in registers
 #pragma unroll
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(64 * PW) void gemvp_kernel(const MatArgs a) {
       if (i < G) xsl[i] = sv[u];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (group >= ngroups) return;  // (after the block's barrier; no barrier follows)
   finish_rows<R, NS>(rows, a, group, xl, xsl, wsl, P, lane);
   for (group += nwv; group < ngroups; group += nwv) {
@@ -722,7 +722,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(1, 4))) 
       const int f = 4 * (lane + 64 * u);
       if (f < G16) *reinterpret_cast<float4 *>(wsl + i * G16 + f) = sr[i][u];
     }
-  __syncthreads();
+  lds_barrier();
   if ((blockIdx.x * W + wave) * R >= a.total_rows) return;  // (after the block's barrier)
 #pragma unroll
   for (int u = 0; u < NS; ++u) {

@@ -7,6 +7,8 @@
   through the MFMA GEMM equals one token at a time through the GEMV, replayed steps equal eager ones.
 - Qwen2.5-7B shape, int6 (hidden 3584, 28 q / 4 kv heads, q/k/v biases, SwiGLU 18944, vocab 152064): two layers
   against the oracle over a 1024-token prompt and 256 greedy steps; all 28 layers against the engine itself.
+- Both whole models (all 32 / 28 layers) against the oracle too: a 128-token prompt and 32 replayed greedy steps, so
+  that every tensor of the checkpoint, past 2 GiB and up to the classifier near its end, is checked to the bit.
 - The 150M shape (hidden 512, 12 layers, 8 heads, SwiGLU 2048, vocab 99487, float16 cache): the whole model against
   the oracle, a 512-token prompt and 256 greedy steps.
 - A Llama form wider than 1024 (the width where rmsnorm runs as its own launch and carries the L2 fills) with no,
@@ -105,6 +107,22 @@ def test_qwen25_7b_int6_widths_two_layers_against_the_oracle():
     seven q heads a kv head)"""
     cfg, tensors, ck, cos, sin = model(QWEN25_7B_INT6, THETA["qwen25-7b-int6"], seed=4, n_layers=2)
     against_the_oracle(cfg, tensors, ck, cos, sin, 1024, 256, seed=22)
+
+
+def test_llama3_8b_whole_model_against_the_oracle():
+    """all 32 layers of the Llama-3-8B shape (8.45 GB: every layer's tensors past 2 GiB, the classifier near 7.9 GB)
+    against the oracle: a 128-token prompt through forwardMany (the MFMA GEMM), then 32 replayed greedy steps; every
+    token, the last logits and the whole cache to the bit (tests/forward-check.mjs:422-462 holds whole models the
+    same way)"""
+    cfg, tensors, ck, cos, sin = model(LLAMA3_8B, THETA["llama3-8b"], seed=7)
+    against_the_oracle(cfg, tensors, ck, cos, sin, 128, 32, seed=25)
+
+
+def test_qwen25_7b_int6_whole_model_against_the_oracle():
+    """all 28 layers of the Qwen2.5-7B shape in int6 (6.2 GB) against the oracle: a 128-token prompt, then 32
+    replayed greedy steps; tokens, last logits and cache to the bit"""
+    cfg, tensors, ck, cos, sin = model(QWEN25_7B_INT6, THETA["qwen25-7b-int6"], seed=8)
+    against_the_oracle(cfg, tensors, ck, cos, sin, 128, 32, seed=26)
 
 
 def test_150m_whole_model_against_the_oracle():

@@ -47,10 +47,32 @@ def test_largest_size_and_special_logits():
 
 
 def test_refuses_more_logits_than_its_array_holds():
+    # a device buffer of as many logits as the call names: were the size check ever to come after the launch, the
+    # sampler would read valid memory and the test fail on its return code, never fault
     pk = package()
-    x = np.zeros(4, dtype=np.float32)
+    x = upload(np.zeros(MOST + 1, dtype=np.float32))
     token = ctypes.c_int32(0)
-    rc = pk.library().hk_sample_static(ctypes.c_void_p(x.ctypes.data), MOST + 1, 1.0, 0.9, 0.5, ctypes.byref(token),
-                                       None)
+    rc = pk.library().hk_sample_static(x.ptr, MOST + 1, 1.0, 0.9, 0.5, ctypes.byref(token), None)
     assert rc == pk.hip_engine.HE_E_ARG
     assert b"262144" in pk.library().he_last_error()
+
+
+def test_refuses_a_stream_under_graph_capture():
+    # the token is copied to the host and the stream waited for, which a capture cannot record: refused before any
+    # launch, and the capture ends cleanly
+    from gpu_lib import hip, hip_check
+    pk = package()
+    h = hip()
+    stream, graph = ctypes.c_void_p(), ctypes.c_void_p()
+    hip_check(h.hipStreamCreate(ctypes.byref(stream)))
+    x = upload(np.zeros(64, dtype=np.float32))
+    token = ctypes.c_int32(7)
+    hip_check(h.hipStreamBeginCapture(stream, 2))  # hipStreamCaptureModeRelaxed
+    rc = pk.library().hk_sample_static(x.ptr, 64, 1.0, 0.9, 0.5, ctypes.byref(token), stream)
+    hip_check(h.hipStreamEndCapture(stream, ctypes.byref(graph)))
+    if graph:
+        hip_check(h.hipGraphDestroy(graph))
+    hip_check(h.hipStreamDestroy(stream))
+    assert rc == pk.hip_engine.HE_E_ARG
+    assert b"capture" in pk.library().he_last_error()
+    assert token.value == 7
