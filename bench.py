@@ -215,7 +215,7 @@ def measure(pk, name, steps=None, warmup=8, prompt_len=None, detail=False, cpu=T
     steps = steps if steps is not None else spec["decode"]
     prompt_len = prompt_len if prompt_len is not None else spec["prompt"]
     cfg = pk.config(**spec["cfg"])
-    if prompt_len + warmup + steps + PROFILED_STEPS > cfg.seq_len:
+    if prompt_len + warmup + steps + PROFILED_STEPS + 1 > cfg.seq_len:
         raise SystemExit("the prompt and the steps do not fit the context")
     tensors, size = pk.places(cfg)
     cos, sin = pk.rope_tables(cfg.seq_len, cfg.head_size, spec["theta"])
@@ -238,24 +238,60 @@ def measure(pk, name, steps=None, warmup=8, prompt_len=None, detail=False, cpu=T
     block = eng.tokenBlock
     ids = []
 
-    def decode(n):
+    def decode(n, stops):
+        # greedy steps as generate() asks for them, stop_tokens=(BOS,) by default (public/llama2_numpy.py:989); a
+        # stop token returned early only makes the next call start from it (the timed steps go on)
         nonlocal token, pos
         done = 0
         while done < n:
-            got = eng.generateMany(token, pos, [], 0, min(block, n - done), 0.0, 0.9, 1.0, [], [])
+            got = eng.generateMany(token, pos, [], 0, min(block, n - done), 0.0, 0.9, 1.0, [], stops)
             ids.extend(got)
             token, pos, done = got[-1], pos + len(got), done + len(got)
 
-    decode(warmup)
+    decode(warmup, [1])
     hip_sync()
+    start = (token, pos, len(ids))
     t0 = time.perf_counter()
-    decode(steps)
+    decode(steps, [1])
     hip_sync()
     decode_s = time.perf_counter() - t0
     rec = {"model": name, "dtype": "int6" if cfg.six else "int8", "kv_cache": "f16" if cfg.half_kv else "f32",
            "prompt_tokens": prompt_len, "decode_tokens": steps, "warmup": warmup,
            "tok_s": steps / decode_s, "ms_per_step": 1e3 * decode_s / steps, "prefill_tok_s": prompt_len / prefill_s,
            "setup_s": setup_s}
+    if detail:
+        # the same steps from the same position again without stop tokens (the cache rows get the same bits), then
+        # sampled steps (the draw and the penalty on the device, the caller's random numbers) from there too
+        end = (token, pos, list(ids))
+        token, pos = start[0], start[1]
+        t0 = time.perf_counter()
+        decode(steps, [])
+        hip_sync()
+        rec["no_stops_tok_s"] = steps / (time.perf_counter() - t0)
+        assert ids[start[2] + steps:] == end[2][start[2]:], "the steps without stop tokens chose other tokens"
+        del ids[start[2] + steps:]
+        rec["sampled"] = {}
+        for temperature, topp, penalty in ((0.8, 1.0, 1.1), (0.8, 0.9, 1.1)):
+            token, pos = start[0], start[1]
+            history = ([1] + prompt + ids[:start[2]])[-64:]
+            r = np.random.default_rng(3)
+            done, declined = 0, False
+            t0 = time.perf_counter()
+            while done < steps:
+                count = min(block, steps - done)
+                got = eng.generateMany(token, pos, history[-64:], len(history), count, temperature, topp, penalty,
+                                       list(r.random(count)), [1])
+                if not got:
+                    declined = True  # the caller's own step would follow (its nucleus is larger than the device sorts)
+                    break
+                history += got
+                token, pos, done = got[-1], pos + len(got), done + len(got)
+            hip_sync()
+            elapsed = time.perf_counter() - t0
+            rec["sampled"][f"t{temperature}_p{topp}_r{penalty}"] = {
+                "temperature": temperature, "topp": topp, "penalty": penalty, "stops": [1], "steps": done,
+                "tok_s": round(done / elapsed, 3) if done else None, "declined": declined}
+        token, pos = end[0], end[1]
 
     # the roofline's kernel: every decode matmul of a step (m = 1, the engine's weights, every layer, the classifier)
     # back to back between one HIP event pair on the engine's stream, 4 passes
@@ -264,6 +300,15 @@ def measure(pk, name, steps=None, warmup=8, prompt_len=None, detail=False, cpu=T
                    "gb_s": gemv_bytes / (gemv_ms * 1e-3) / 1e9}
     # the weights a decode step streams at the measured step rate
     rec["effective_gb_s"] = gemv_bytes * rec["tok_s"] / 1e9
+    # the whole step against HBM: every matmul's bytes and the cache rows the attention reads (keys and values of
+    # every position up to the step's, at the timed steps' mean position)
+    kv_bytes = 2.0 * cfg.n_layers * (prompt_len + warmup + steps / 2.0 + 1) * cfg.n_kv_heads * cfg.head_size * \
+        (2 if cfg.half_kv else 4)
+    step_bytes = gemv_bytes + kv_bytes
+    rec["step_roofline"] = {"bound": "hbm", "bytes_per_step": round(step_bytes), "kv_bytes_per_step": round(kv_bytes),
+                            "achieved": round(step_bytes * rec["tok_s"] / 1e9, 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(step_bytes * rec["tok_s"] / 1e9 / HBM_PEAK_GBS, 4),
+                            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / step_bytes, 1)}
     if detail:
         # decode steps timed kernel by kind (a HIP event pair around every launch on the engine's stream), at the
         # positions the run reached
@@ -357,6 +402,8 @@ def main():
     ceiling_gbs = read_ceiling(pk)
     pairs_s, _ = valu_ceiling(pk)
     mfma_ops_s = mfma_ceiling(pk)
+    rec["step_roofline"]["read_ceiling_gb_s"] = round(ceiling_gbs, 1)
+    rec["step_roofline"]["frac_of_read_ceiling"] = round(rec["step_roofline"]["achieved"] / ceiling_gbs, 4)
     others = {}
     if not args.only:
         for name in OTHERS:
@@ -388,10 +435,12 @@ def main():
         "dtype": rec["dtype"],
         "data": "synthetic (random-init weights N(0,0.02) quantized by the reference's rules; random prompt ids)",
         "config": {"workload": f"{cfg_name}-shape {rec['dtype']} greedy decode at batch 1 after a "
-                               f"{rec['prompt_tokens']}-token prefill",
+                               f"{rec['prompt_tokens']}-token prefill, stop token BOS as generate() asks",
                    "model": cfg_name, "prompt_tokens": rec["prompt_tokens"], "decode_tokens": rec["decode_tokens"],
                    "kv_cache": rec["kv_cache"], "order": "exact (the reference's float32 order)"},
         "prefill_tok_s": round(rec["prefill_tok_s"], 2),
+        "no_stops_tok_s": round(rec["no_stops_tok_s"], 3),
+        "sampled": rec["sampled"],
         "gemv_hbm_gb_s": round(gemv_gbs, 1),
         "effective_gb_s": round(rec["effective_gb_s"], 1),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -417,6 +466,7 @@ def main():
                      "valu_f32_ops_t_s": round(valu_ops_s / 1e12, 2),
                      "mfma_i8_top_s": round(mfma_ops_s / 1e12, 1),
                      "source": "hk_read_ceiling, hk_valu_ceiling, hk_mfma_ceiling (kernels/ceilings.ts on the device)"},
+        "step_roofline": rec["step_roofline"],
         "gemv_by_matrix": rec["gemv_by_matrix"],
         "profile_ms": rec["profile_ms"],
         "profiled_step_ms": rec["profiled_step_ms"],

@@ -144,7 +144,12 @@ int32_t he_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int3
  * (penalized where the penalty applied) stay readable with he_logits. Returns HE_E_NOTFINITE where a step's largest
  * logit is not finite (nothing of that step is in ids). *n_ids may be less than count without a stop token where a
  * step's nucleus holds more tokens than the device sorts (more than 8192): the caller takes that step itself, and
- * *n_ids = 0 is the reference's "the GPU did not take them" (undefined). */
+ * *n_ids = 0 is the reference's "the GPU did not take them" (undefined).
+ * With at most 8 stop tokens (public/forward.js STOPS_MOST) the steps after the first are replayed from a captured
+ * graph of one step, every choice (greedy, penalty, draw, stop) made on the device and the tokens read back once a
+ * round (16 steps with stop tokens, 64 without): where a step ends the call, the round's later replays still run,
+ * and their cache rows, past the positions of the ids returned, hold what the next step at those positions
+ * overwrites. */
 int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, const int32_t *history, int32_t n_history,
                          int32_t length, int32_t count, float temperature, float topp, float penalty,
                          const double *randoms, int32_t n_randoms, const int32_t *stops, int32_t n_stops, int32_t *ids,

@@ -163,8 +163,14 @@ struct he_engine {
   float *step_values = nullptr;                       // their logits
   int32_t *host_ids = nullptr, *host_state = nullptr;  // pinned
   float *host_values = nullptr;                       // pinned
-  hipGraphExec_t graph = nullptr;
-  bool graph_tried = false;
+  // the captured step graphs by kind (STEP_GREEDY, STEP_PENALIZED, STEP_SAMPLED, STEP_SAMPLED | STEP_PENALIZED)
+  hipGraphExec_t graph[4] = {};
+  bool graph_tried[4] = {};
+  // a call's settings (device, and its pinned host copy); the logits of the step that ended the last call, where the
+  // round's later replays overwrote its own
+  RunParams *run_params = nullptr, *host_params = nullptr;
+  float *kept_logits = nullptr;
+  bool logits_kept = false;
   // sampled steps: the sampler's scratch, the penalty's window, the token drawn (device); the window (pinned)
   float *sample_probs = nullptr;
   int32_t *sample_index = nullptr, *window = nullptr, *sample_token = nullptr;
@@ -206,18 +212,25 @@ struct he_engine {
 namespace {
 
 constexpr int32_t STEPS_A_ROUND = 64;      // replayed steps between two reads of their tokens
-constexpr int32_t REPETITION_WINDOW = 64;  // the penalty's latest tokens (public/llama2_numpy.py:545)
+constexpr int32_t STOP_ROUND = 16;         // the same where a stop token may end the call early (the round's later
+                                           // replays are then spent for nothing)
+constexpr int32_t REPETITION_WINDOW = RUN_WINDOW;  // the penalty's latest tokens (public/llama2_numpy.py:545)
+static_assert(STEPS_A_ROUND <= RUN_RANDOMS, "a random number for every step of a round");
+// the kinds of replayed step graph
+enum { STEP_GREEDY = 0, STEP_PENALIZED = 1, STEP_SAMPLED = 2 };
 
 void destroy(he_engine *e) {
   if (!e) return;
-  if (e->graph) (void)hipGraphExecDestroy(e->graph);
+  for (hipGraphExec_t g : e->graph)
+    if (g) (void)hipGraphExecDestroy(g);
   void *ptrs[] = {e->blob, e->cos_t, e->sin_t, e->keys, e->vals, e->x, e->xb, e->q, e->k, e->v, e->hb, e->hb2,
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
                   e->best_v, e->best_i, e->state, e->step_ids, e->step_values, e->sample_probs, e->sample_index,
-                  e->window, e->sample_token, e->sample_best, e->before, e->columns, e->picked, e->sink};
+                  e->window, e->sample_token, e->sample_best, e->before, e->columns, e->picked, e->sink,
+                  e->run_params, e->kept_logits};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
-  void *pinned[] = {e->host_ids, e->host_state, e->host_values, e->host_window};
+  void *pinned[] = {e->host_ids, e->host_state, e->host_values, e->host_window, e->host_params};
   for (void *p : pinned)
     if (p) (void)hipHostFree(p);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -363,7 +376,7 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->amax_i, sizeof(int32_t) * 256);
   ALLOC(e->best_v, sizeof(float) * 4);
   ALLOC(e->best_i, sizeof(int32_t) * 4);
-  ALLOC(e->state, sizeof(int32_t) * 4);
+  ALLOC(e->state, sizeof(int32_t) * STATE_WORDS);
   ALLOC(e->step_ids, sizeof(int32_t) * STEPS_A_ROUND);
   ALLOC(e->step_values, sizeof(float) * STEPS_A_ROUND);
   ALLOC(e->sample_probs, sizeof(float) * c.vocab_size);
@@ -372,6 +385,8 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->sample_token, sizeof(int32_t) * 4);
   ALLOC(e->sample_best, sizeof(float) * 4);
   ALLOC(e->sink, sizeof(uint32_t) * 64);
+  ALLOC(e->run_params, sizeof(RunParams));
+  ALLOC(e->kept_logits, sizeof(float) * c.vocab_size);
   {
     // the fills pay where a token's weights come from HBM; a checkpoint that the 256 MB MALL holds whole (with room for
     // the cache and activations) finds them there, and the fill blocks would only add latency
@@ -392,7 +407,8 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
 #undef ALLOC
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_ids), sizeof(int32_t) * STEPS_A_ROUND));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_values), sizeof(float) * STEPS_A_ROUND));
-  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_state), sizeof(int32_t) * 4));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_state), sizeof(int32_t) * (STATE_WORDS + 2)));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_params), sizeof(RunParams)));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&e->host_window), sizeof(int32_t) * REPETITION_WINDOW));
   return HE_OK;
 }
@@ -766,6 +782,7 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
         return launch_add_columns(e->logits, e->columns, e->picked, c.n_outliers, c.vocab_size, s);
       }));
     e->have_logits = true;
+    e->logits_kept = false;
   }
   return HE_OK;
 }
@@ -872,10 +889,12 @@ int32_t he_forward_many(he_engine *e, const int32_t *tokens, int32_t count, int3
 }
 
 namespace {
-// the graph of one greedy decode step (the caller has run at least one step eagerly, so that every launch's one-time
-// set-up is done): captured with positions bounded by seq_len - 1 and read from state[0]
-void build_graph(he_engine *e) {
-  e->graph_tried = true;
+// the graph of one decode step of a kind (the caller has run at least one step eagerly, so that every launch's one-time
+// set-up is done): captured with positions bounded by seq_len - 1 and read from state[STATE_POS]: the forward pass with
+// logits, the penalty over the window in device memory (STEP_PENALIZED), the greedy choice or the draw with the call's
+// settings and the round's random number (STEP_SAMPLED), then the step's end (launch_step_end)
+void build_graph(he_engine *e, int kind) {
+  e->graph_tried[kind] = true;
   // PYODIDE_LLM_HIP_GRAPH=0 keeps every step eager (a kernel-trace profiler that does not follow graph launches)
   const char *env = std::getenv("PYODIDE_LLM_HIP_GRAPH");
   if (env && env[0] == '0') return;
@@ -886,19 +905,28 @@ void build_graph(he_engine *e) {
   if (err == hipSuccess) {
     rc = run_chunk(e, nullptr, 1, e->c.seq_len - 1, true);
     if (rc == HE_OK) {
-      hipError_t le = launch_argmax(e->best_i, e->best_v, e->logits, e->c.vocab_size, e->amax_v, e->amax_i, e->stream);
+      const int32_t n = e->c.vocab_size;
+      hipError_t le = hipSuccess;
+      if (kind & STEP_PENALIZED) le = launch_penalize_steps(e->logits, e->window, e->state, e->run_params, e->stream);
+      const bool drawn = (kind & STEP_SAMPLED) != 0;
       if (le == hipSuccess)
-        le = launch_advance(e->tokens, e->state, e->best_i, e->best_v, e->step_ids, e->step_values, e->stream);
+        le = drawn ? launch_sample_steps(e->logits, n, e->run_params, e->state, e->sample_probs, e->sample_index,
+                                         e->sample_token, e->sample_best, e->stream)
+                   : launch_argmax(e->best_i, e->best_v, e->logits, n, e->amax_v, e->amax_i, e->stream);
+      if (le == hipSuccess)
+        le = launch_step_end(e->logits, n, e->kept_logits, e->tokens, e->state, drawn ? e->sample_token : e->best_i,
+                             drawn ? e->sample_best : e->best_v, e->step_ids, e->step_values, e->window,
+                             e->run_params, e->stream);
       if (le != hipSuccess) rc = HE_E_HIP;
     }
     const hipError_t end = hipStreamEndCapture(e->stream, &g);
     if (err == hipSuccess) err = end;
   }
   e->replayable = false;
-  if (err == hipSuccess && rc == HE_OK && g) err = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+  if (err == hipSuccess && rc == HE_OK && g) err = hipGraphInstantiate(&e->graph[kind], g, nullptr, nullptr, 0);
   if (g) (void)hipGraphDestroy(g);
   if (err != hipSuccess || rc != HE_OK) {
-    e->graph = nullptr;  // the steps stay eager
+    e->graph[kind] = nullptr;  // the steps stay eager
     (void)hipGetLastError();
   }
 }
@@ -977,50 +1005,82 @@ int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, const int32_t
       if (stops[j] == id) return true;
     return false;
   };
-  if (temperature > 0.0f || penalty != 1.0f)
+  // more stop tokens than a replayed call takes (public/forward.js STOPS_MOST): every step eager
+  if (n_stops > RUN_STOPS_MOST)
     return sampled_steps(e, token, pos, history, n_history, count, temperature, topp, penalty, randoms, is_stop, ids,
                          n_ids);
+  const int kind = (temperature > 0.0f ? STEP_SAMPLED : STEP_GREEDY) | (penalty != 1.0f ? STEP_PENALIZED : 0);
+  // the penalty's window: the latest of history, then the tokens this call chooses
+  std::vector<int32_t> window(history + std::max(0, n_history - REPETITION_WINDOW), history + n_history);
   int32_t done = 0;
-  // greedy: eager steps until the graph exists (the first step of an engine's first call builds it)
-  while (done < count && !e->graph) {
-    int32_t best = 0;
-    float value = 0.0f;
-    const int32_t rc = eager_step(e, token, pos + done, &best, &value);
+  // eager steps until the kind's graph exists (the first step of an engine's first call of a kind builds it)
+  while (done < count && !e->graph[kind]) {
+    const int32_t before = *n_ids;
+    const int32_t rc = sampled_steps(e, token, pos + done, window.data(), (int32_t)window.size(), 1, temperature,
+                                     topp, penalty, randoms ? randoms + done : nullptr, is_stop, ids, n_ids);
     if (rc) return rc;
-    if (!std::isfinite(value)) return fail(HE_E_NOTFINITE, "the largest logit is not finite");
-    ids[(*n_ids)++] = best;
-    token = best;
+    if (*n_ids == before) return HE_OK;  // declined: the caller takes the step
+    token = ids[*n_ids - 1];
+    window.push_back(token);
+    if ((int32_t)window.size() > REPETITION_WINDOW) window.erase(window.begin());
     ++done;
-    if (is_stop(best)) return HE_OK;
-    if (!e->graph_tried) build_graph(e);
+    if (is_stop(token)) return HE_OK;
+    if (!e->graph_tried[kind]) build_graph(e, kind);
   }
-  // replayed steps, a round of up to STEPS_A_ROUND at a time: without stop tokens the round runs back to back and its
-  // tokens are read once at its end; with them, each step's token is read before the next step starts
-  while (done < count) {
-    const int32_t n = std::min(STEPS_A_ROUND, count - done);
-    e->host_state[0] = token;
-    e->host_state[1] = pos + done;
-    e->host_state[2] = 0;
-    HIP_TRY(hipMemcpyAsync(e->tokens, e->host_state, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
-    HIP_TRY(hipMemcpyAsync(e->state, e->host_state + 1, 2 * sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
-    for (int32_t i = 0; i < n; ++i) {
-      HIP_TRY(hipGraphLaunch(e->graph, e->stream));
-      if (n_stops == 0 && i + 1 < n) continue;
-      const int32_t from = n_stops == 0 ? 0 : i, k = i + 1 - from;
-      HIP_TRY(hipMemcpyAsync(e->host_ids + from, e->step_ids + from, sizeof(int32_t) * k, hipMemcpyDeviceToHost,
-                             e->stream));
-      HIP_TRY(hipMemcpyAsync(e->host_values + from, e->step_values + from, sizeof(float) * k, hipMemcpyDeviceToHost,
-                             e->stream));
-      HIP_TRY(hipStreamSynchronize(e->stream));
-      for (int32_t j = from; j <= i; ++j) {
-        if (!std::isfinite(e->host_values[j])) return fail(HE_E_NOTFINITE, "the largest logit is not finite");
-        ids[(*n_ids)++] = e->host_ids[j];
-        if (is_stop(e->host_ids[j])) return HE_OK;
+  if (done == count) return HE_OK;
+  // replayed steps, a round at a time, with the call's settings, stop tokens and window in device memory: the round's
+  // tokens are read once at its end, and the first step that ends the call (a stop token, a declined draw, a largest
+  // logit that is not finite) is known from state[STATE_HALTED]; the round's replays after it are spent for nothing
+  // (their cache rows lie past the call's positions, rewritten by whatever step takes those positions next), its
+  // logits kept apart for he_logits. Rounds are shorter where stop tokens may end the call.
+  RunParams &hp = *e->host_params;
+  hp.temperature = temperature;
+  hp.topp = topp;
+  hp.penalty = penalty;
+  hp.n_stops = n_stops;
+  for (int32_t j = 0; j < RUN_STOPS_MOST; ++j) hp.stops[j] = j < n_stops ? stops[j] : -1;
+  const int32_t w = (int32_t)window.size();
+  if (w > 0) {
+    std::memcpy(e->host_window, window.data(), sizeof(int32_t) * w);
+    HIP_TRY(hipMemcpyAsync(e->window, e->host_window, sizeof(int32_t) * w, hipMemcpyHostToDevice, e->stream));
+  }
+  const int32_t round = n_stops > 0 ? STOP_ROUND : STEPS_A_ROUND;
+  int32_t *hs = e->host_state;
+  for (bool first = true; done < count; first = false) {
+    const int32_t n = std::min(round, count - done);
+    for (int32_t i = 0; i < RUN_RANDOMS; ++i) hp.randoms[i] = temperature > 0.0f && i < n ? randoms[done + i] : 0.0;
+    hs[STATE_WORDS] = token;
+    hs[STATE_POS] = pos + done;
+    hs[STATE_STEP] = 0;
+    hs[STATE_HALTED] = 0;
+    hs[STATE_WINDOW] = w;  // (uploaded with the first round only: the device appends to the window from then on)
+    hs[STATE_HEAD] = 0;
+    HIP_TRY(hipMemcpyAsync(e->tokens, hs + STATE_WORDS, sizeof(int32_t), hipMemcpyHostToDevice, e->stream));
+    HIP_TRY(hipMemcpyAsync(e->state, hs, sizeof(int32_t) * (first ? STATE_HEAD + 1 : STATE_HALTED + 1),
+                           hipMemcpyHostToDevice, e->stream));
+    HIP_TRY(hipMemcpyAsync(e->run_params, &hp, sizeof(RunParams), hipMemcpyHostToDevice, e->stream));
+    for (int32_t i = 0; i < n; ++i) HIP_TRY(hipGraphLaunch(e->graph[kind], e->stream));
+    HIP_TRY(hipMemcpyAsync(e->host_ids, e->step_ids, sizeof(int32_t) * n, hipMemcpyDeviceToHost, e->stream));
+    HIP_TRY(hipMemcpyAsync(e->host_values, e->step_values, sizeof(float) * n, hipMemcpyDeviceToHost, e->stream));
+    HIP_TRY(hipMemcpyAsync(hs + STATE_WORDS + 1, e->state + STATE_HALTED, sizeof(int32_t), hipMemcpyDeviceToHost,
+                           e->stream));
+    HIP_TRY(hipStreamSynchronize(e->stream));
+    const int32_t halted = hs[STATE_WORDS + 1];
+    for (int32_t j = 0; j < (halted ? halted : n); ++j) {
+      const int32_t id = e->host_ids[j];
+      if (halted && j == halted - 1) {
+        e->logits_kept = true;
+        if (id == SAMPLE_NOT_FINITE || !std::isfinite(e->host_values[j]))
+          return fail(HE_E_NOTFINITE, "the largest logit is not finite");
+        if (id != SAMPLE_DECLINED) ids[(*n_ids)++] = id;  // the stop token, last
+        return HE_OK;  // (declined: the caller takes that step)
       }
+      ids[(*n_ids)++] = id;
     }
     token = ids[*n_ids - 1];
     done += n;
   }
+  e->logits_kept = false;
   return HE_OK;
 }
 
@@ -1136,7 +1196,8 @@ int32_t he_profile_matmul(he_engine *e, int32_t which, int32_t rounds, double *m
 int32_t he_logits(he_engine *e, float *out) {
   if (!e || !out) return fail(HE_E_ARG, "a required pointer is null");
   if (!e->have_logits) return fail(HE_E_STATE, "no step with logits has run");
-  HIP_TRY(hipMemcpyAsync(out, e->logits, sizeof(float) * e->c.vocab_size, hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipMemcpyAsync(out, e->logits_kept ? e->kept_logits : e->logits, sizeof(float) * e->c.vocab_size,
+                         hipMemcpyDeviceToHost, e->stream));
   HIP_TRY(hipStreamSynchronize(e->stream));
   return HE_OK;
 }

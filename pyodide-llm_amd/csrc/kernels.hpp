@@ -190,12 +190,36 @@ hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, 
 // the nucleus where 0 < topp < 1; *out_token is the token, SAMPLE_NOT_FINITE where the largest logit is not finite,
 // or SAMPLE_DECLINED where the nucleus holds more tokens than one block sorts. probs, index: scratch of n each.
 constexpr int32_t SAMPLE_NOT_FINITE = -1, SAMPLE_DECLINED = -2;
+constexpr int32_t SAMPLE_MOST = 262144;  // logits a draw takes at most
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
                          int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
-// the end of a replayed decode step: its token and value into ids / values at state[1], the token as the next step's
-// input (tokens[0]), state[0] (the position) and state[1] (the step) advanced
-hipError_t launch_advance(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
-                          float *values, hipStream_t s);
+// ---- replayed decode steps (a captured graph of one step, replayed a round at a time) ----
+// the step's state in device memory: the position, the step of the round, the halting step + 1 (0: none yet), the
+// penalty window's count and its oldest entry once full
+enum { STATE_POS = 0, STATE_STEP, STATE_HALTED, STATE_WINDOW, STATE_HEAD, STATE_WORDS = 8 };
+constexpr int32_t RUN_STOPS_MOST = 8;   // stop tokens a replayed call takes (public/forward.js STOPS_MOST)
+constexpr int32_t RUN_WINDOW = 64;      // the penalty's latest tokens (public/llama2_numpy.py:545)
+constexpr int32_t RUN_RANDOMS = 64;     // random numbers of a round (its steps at most)
+// the settings of a call's replayed steps, in device memory: one captured graph takes every call's
+struct RunParams {
+  double randoms[RUN_RANDOMS];  // the round's random numbers, step i's at i
+  float temperature, topp, penalty;
+  int32_t n_stops;
+  int32_t stops[RUN_STOPS_MOST];
+};
+// a step's draw (as launch_sample) with the call's temperature and top-p and the round's random number of the step
+hipError_t launch_sample_steps(const float *logits, int32_t n, const RunParams *params, const int32_t *state,
+                               float *probs, int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
+// the call's penalty over the window's state[STATE_WINDOW] tokens
+hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
+                                 hipStream_t s);
+// the end of a replayed step that chose *token (largest logit *value): where this step ends the call (a stop token,
+// no token, a largest logit that is not finite) and none before it did, its logits into kept and state[STATE_HALTED]
+// = step + 1; its token and value into ids / values at the step, the token into the window and as the next step's
+// input (tokens[0]), the position and the step advanced
+hipError_t launch_step_end(const float *logits, int32_t n, float *kept, int32_t *tokens, int32_t *state,
+                           const int32_t *token, const float *value, int32_t *ids, float *values, int32_t *window,
+                           const RunParams *params, hipStream_t s);
 
 // ---- the other forms (forms.hip) ----
 // layernorm (eps 1e-5) then quantize_x, m tokens; out (optional) the float32 rows; copy (optional, x_stride) x itself

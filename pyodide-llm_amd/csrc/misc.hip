@@ -519,22 +519,6 @@ hipError_t launch_qkv_post(const QkvPost &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-__global__ void advance_kernel(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
-                               float *values) {
-  const int32_t step = state[1], b = *best;
-  ids[step] = b;
-  values[step] = *value;
-  tokens[0] = b;
-  state[0] = state[0] + 1;
-  state[1] = step + 1;
-}
-
-hipError_t launch_advance(int32_t *tokens, int32_t *state, const int32_t *best, const float *value, int32_t *ids,
-                          float *values, hipStream_t s) {
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, tokens, state, best, value, ids, values);
-  return hipGetLastError();
-}
-
 hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, float *scratch_v, int32_t *scratch_i,
                          hipStream_t s) {
   const int blocks = 256;

@@ -24,7 +24,7 @@ namespace {
 
 constexpr int ST = 1024;         // threads of the sampling block
 constexpr int SORT_MOST = 8192;  // nucleus tokens one block sorts (more: the step is declined, SAMPLE_DECLINED)
-constexpr int STAGE = 16384;     // probabilities staged in LDS at a time for the running sums
+constexpr int STAGE = 16384;     // floats of the LDS area the sort and the running sums' staging share
 
 // kernels/kernel.ts:705-719: each distinct token of tokens[0..count) once, value > 0 ? value / penalty : value * penalty
 __global__ __launch_bounds__(64) void penalize_kernel(float *logits, const int32_t *tokens, int32_t count,
@@ -62,12 +62,76 @@ __device__ __forceinline__ int block_scan(int c, int *wave_sums, int *total) {
   return wave_sums[wave] + x - c;
 }
 
+// The float64 running sums of the draw are sequential (the reference's order: one add after another in index order),
+// so one thread runs them; these keep its adds from waiting on LDS: 32 values requested at a time as float4.
+constexpr int CP_BLOCK = 256;                     // values between two checkpoints of the running sum
+constexpr int CP_MOST = SAMPLE_MOST / CP_BLOCK;   // checkpoints of the largest vocabulary
+constexpr int WIDE = STAGE / 2;                   // float64 values staged in LDS at a time for the total
+static_assert(WIDE % CP_BLOCK == 0, "a staged chunk holds whole checkpoint blocks");
+
+// acc + v[0] + v[1] + ... + v[len-1] in float64, in order; with cp, cp[cp0 + i / CP_BLOCK] = the sum before value i
+// for every i that is a multiple of CP_BLOCK (v: the values already widened to float64 by the whole block, 16-byte
+// aligned, so that the one thread's instructions are the adds alone)
+__device__ __forceinline__ double sum_f64(const double *v, int len, double acc, double *cp, int cp0) {
+  const double2 *v2 = reinterpret_cast<const double2 *>(v);
+  int i = 0;
+  for (; i + 32 <= len; i += 32) {
+    if (cp && i % CP_BLOCK == 0) cp[cp0 + i / CP_BLOCK] = acc;
+    double2 a[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) a[u] = v2[i / 2 + u];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      acc += a[u].x;
+      acc += a[u].y;
+    }
+  }
+  if (cp && i < len && i % CP_BLOCK == 0) cp[cp0 + i / CP_BLOCK] = acc;
+  for (; i < len; ++i) acc += v[i];
+  return acc;
+}
+
+// the first j < len whose running sum acc + v[0] + ... + v[j] (float64, in order) passes target (REACH: reaches it), or
+// -1; *acc_out the sum reached (v 16-byte aligned)
+template <bool REACH = false>
+__device__ __forceinline__ int first_past(const float *v, int len, double acc, double target, double *acc_out) {
+  auto past = [&](double a) { return REACH ? a >= target : a > target; };
+  const float4 *v4 = reinterpret_cast<const float4 *>(v);
+  int i = 0;
+  for (; i + 32 <= len; i += 32) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = v4[i / 4 + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float x[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc += (double)x[k];
+        if (past(acc)) {
+          *acc_out = acc;
+          return i + 4 * u + k;
+        }
+      }
+    }
+  }
+  for (; i < len; ++i) {
+    acc += (double)v[i];
+    if (past(acc)) {
+      *acc_out = acc;
+      return i;
+    }
+  }
+  *acc_out = acc;
+  return -1;
+}
+
 // (p, token) pairs: a before b where p is larger, or equal and the token smaller
 __device__ __forceinline__ bool before(float pa, int ia, float pb, int ib) { return pa > pb || (pa == pb && ia < ib); }
 
-__global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t n, float temperature, float topp,
-                                                    double random, float *probs, int32_t *index, int32_t *out_token,
-                                                    float *out_best) {
+__device__ __forceinline__ void sample_block(const float *logits, int32_t n, float temperature, float topp,
+                                             double random, float *probs, int32_t *index, int32_t *out_token,
+                                             float *out_best) {
   __shared__ float4 area[SORT_MOST / 2];  // the sort's probabilities then tokens; the running sums' staging
   float *const sp = reinterpret_cast<float *>(area);
   int *const si = reinterpret_cast<int *>(area) + SORT_MOST;
@@ -76,8 +140,8 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
   __shared__ float shared_best, shared_top;
   __shared__ int shared_count, shared_likely, shared_token;
   __shared__ double shared_total, shared_cutoff;
+  __shared__ double checkpoints[CP_MOST];  // the running sum of the kept p before every CP_BLOCK of them
   static_assert(STAGE <= 2 * SORT_MOST, "the staging area is the sort's");
-  float *const stage = reinterpret_cast<float *>(area);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // the largest logit (order-free: wmax keeps a NaN and puts +0 above -0)
@@ -103,21 +167,30 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
   const bool nucleus = topp > 0 && topp < 1;
   const float floor_ = nucleus ? best - temperature * 16.118095f : -3.4028234663852886e38f;
 
-  // kept: v - best for v >= floor in index order (each thread a contiguous run of the vocabulary), then p
-  const int seg = (n + ST - 1) / ST, lo = min(n, tid * seg), hi = min(n, lo + seg);
+  // kept: v - best for v >= floor in index order, then p. Each wave takes a contiguous run of the vocabulary, 64
+  // values a step side by side: the count of its run, a block scan over the waves, then the kept values' places in
+  // order (the lanes below in the step, the steps before)
+  const int wrun = ((n + ST / 64 - 1) / (ST / 64) + 63) & ~63, wlo = min(n, wave * wrun), whi = min(n, wlo + wrun);
+  const uint64_t below = (1ull << lane) - 1;
   int c = 0;
-  for (int i = lo; i < hi; ++i) c += logits[i] >= floor_;
-  int k = block_scan(c, wi, &shared_count);
+  for (int i = wlo + lane; i < whi; i += 64) c += logits[i] >= floor_;
+  for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
+  int k = block_scan(lane == 0 ? c : 0, wi, &shared_count);
+  k = __shfl(k, 0, 64);
   const int count = shared_count, simd = count & ~3;
   const float inverse = 1.0f / temperature;
-  for (int i = lo; i < hi; ++i) {
-    const float v = logits[i];
-    if (v >= floor_) {
+  for (int i0 = wlo; i0 < whi; i0 += 64) {
+    const int i = i0 + lane;
+    const float v = i < whi ? logits[i] : 0.0f;
+    const bool keep = i < whi && v >= floor_;
+    const uint64_t mask = __ballot(keep);
+    if (keep) {
+      const int at = k + __popcll(mask & below);
       const float d = v - best;
-      probs[k] = k < simd ? vexp(d * inverse) : fexp(d / temperature);
-      index[k] = i;
-      ++k;
+      probs[at] = at < simd ? vexp(d * inverse) : fexp(d / temperature);
+      index[at] = i;
     }
+    k += __popcll(mask);
   }
   __syncthreads();
 
@@ -127,13 +200,13 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
   for (int o = 32; o >= 1; o >>= 1) t = __builtin_fmaxf(t, __shfl_xor(t, o, 64));
   if (lane == 0) wf[wave] = t;
   double total = 0.0;
-  for (int base = 0; base < count; base += STAGE) {
-    const int len = min(STAGE, count - base);
+  double *const wide = reinterpret_cast<double *>(area);  // a chunk of the p widened to float64 (exactly)
+  for (int base = 0; base < count; base += WIDE) {
+    const int len = min(WIDE, count - base);
     __syncthreads();
-    for (int j = tid; j < len; j += ST) stage[j] = probs[base + j];
+    for (int j = tid; j < len; j += ST) wide[j] = (double)probs[base + j];
     __syncthreads();
-    if (tid == 0)
-      for (int j = 0; j < len; ++j) total += (double)stage[j];
+    if (tid == 0) total = sum_f64(wide, len, total, checkpoints, base / CP_BLOCK);
   }
   if (tid == 0) {
     float x = wf[0];
@@ -145,29 +218,21 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
   total = shared_total;
 
   if (!nucleus) {
-    // the running sum in index order up to the first that passes random * total
-    const double target = random * total;
-    double cumulative = 0.0;
-    int token = -1;
-    for (int base = 0; base < count && token < 0; base += STAGE) {
-      const int len = min(STAGE, count - base);
-      __syncthreads();
-      for (int j = tid; j < len; j += ST) stage[j] = probs[base + j];
-      __syncthreads();
-      if (tid == 0) {
-        for (int j = 0; j < len; ++j) {
-          cumulative += (double)stage[j];
-          if (cumulative > target) {
-            shared_token = base + j;
-            break;
-          }
-        }
-        if (!(cumulative > target)) shared_token = -1;
-      }
-      __syncthreads();
-      token = shared_token;
-    }
+    // the running sum in index order up to the first that passes random * total: the block of CP_BLOCK where it
+    // passes, from the checkpoints (the sum never decreases: every p >= 0), then that block's adds again from its
+    // checkpoint (the same adds, the same bits)
     if (tid == 0) {
+      const double target = random * total;
+      const int blocks = (count + CP_BLOCK - 1) / CP_BLOCK;
+      int b = 0;
+      while (b < blocks && (b + 1 < blocks ? checkpoints[b + 1] : total) <= target) ++b;
+      int token = -1;
+      if (b < blocks) {
+        double reached = 0.0;
+        const int j = first_past(probs + b * CP_BLOCK, min(CP_BLOCK, count - b * CP_BLOCK), checkpoints[b], target,
+                                 &reached);
+        if (j >= 0) token = b * CP_BLOCK + j;
+      }
       *out_token = index[token >= 0 ? token : count - 1];
       *out_best = best;
     }
@@ -182,10 +247,14 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
   }
   __syncthreads();
   const double cutoff = shared_cutoff;
-  const int kseg = (count + ST - 1) / ST, klo = min(count, tid * kseg), khi = min(count, klo + kseg);
+  // the kept p >= cutoff, in order: a wave a contiguous run, as above
+  const int krun = ((count + ST / 64 - 1) / (ST / 64) + 63) & ~63, klo = min(count, wave * krun),
+            khi = min(count, klo + krun);
   int lc = 0;
-  for (int j = klo; j < khi; ++j) lc += (double)probs[j] >= cutoff;
-  int at = block_scan(lc, wi, &shared_likely);
+  for (int j = klo + lane; j < khi; j += 64) lc += (double)probs[j] >= cutoff;
+  for (int o = 32; o >= 1; o >>= 1) lc += __shfl_xor(lc, o, 64);
+  int at = block_scan(lane == 0 ? lc : 0, wi, &shared_likely);
+  at = __shfl(at, 0, 64);
   const int likely = shared_likely;
   if (likely > SORT_MOST) {
     if (tid == 0) {
@@ -194,13 +263,17 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
     }
     return;
   }
-  for (int j = klo; j < khi; ++j) {
-    const float p = probs[j];
-    if ((double)p >= cutoff) {
-      sp[at] = p;
-      si[at] = index[j];
-      ++at;
+  for (int j0 = klo; j0 < khi; j0 += 64) {
+    const int j = j0 + lane;
+    const float p = j < khi ? probs[j] : 0.0f;
+    const bool keep = j < khi && (double)p >= cutoff;
+    const uint64_t mask = __ballot(keep);
+    if (keep) {
+      const int to = at + __popcll(mask & below);
+      sp[to] = p;
+      si[to] = index[j];
     }
+    at += __popcll(mask);
   }
   int size = 1;
   while (size < likely) size <<= 1;
@@ -230,32 +303,119 @@ __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t
     }
   }
   if (tid == 0) {
+    // the nucleus: the running sum from the most probable up to the first that reaches topp * total; then the draw
+    // within it
     const double limit = (double)topp * total;
     double mass = 0.0;
-    int last = likely - 1;
-    for (int j = 0; j < likely; ++j) {
-      mass += (double)sp[j];
-      if (mass >= limit) {
-        last = j;
-        break;
-      }
-    }
+    int last = first_past<true>(sp, likely, 0.0, limit, &mass);
+    if (last < 0) last = likely - 1;
     const double target = random * mass;
-    double cumulative = 0.0;
-    int token = si[last];
-    for (int j = 0; j <= last; ++j) {
-      cumulative += (double)sp[j];
-      if (cumulative > target) {
-        token = si[j];
-        break;
-      }
-    }
-    *out_token = token;
+    double reached = 0.0;
+    const int j = first_past(sp, last + 1, 0.0, target, &reached);
+    *out_token = si[j >= 0 ? j : last];
     *out_best = best;
   }
 }
 
+__global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t n, float temperature, float topp,
+                                                    double random, float *probs, int32_t *index, int32_t *out_token,
+                                                    float *out_best) {
+  sample_block(logits, n, temperature, topp, random, probs, index, out_token, out_best);
+}
+
+// ---- the sampled steps of a replayed graph: settings, random numbers and the penalty's window in device memory ----
+
+// a step's draw: the temperature and top-p of the call, the round's random number of this step (state[STATE_STEP])
+__global__ __launch_bounds__(ST) void sample_steps_kernel(const float *logits, int32_t n, const RunParams *params,
+                                                          const int32_t *state, float *probs, int32_t *index,
+                                                          int32_t *out_token, float *out_best) {
+  sample_block(logits, n, params->temperature, params->topp, params->randoms[state[STATE_STEP]], probs, index,
+               out_token, out_best);
+}
+
+// the penalty of the call over the window's state[STATE_WINDOW] tokens (in any order: each distinct one once)
+__global__ __launch_bounds__(64) void penalize_steps_kernel(float *logits, const int32_t *window, const int32_t *state,
+                                                           const RunParams *params) {
+  const int i = threadIdx.x, count = state[STATE_WINDOW];
+  if (i >= count) return;
+  const int32_t t = window[i];
+  for (int j = 0; j < i; ++j)
+    if (window[j] == t) return;  // a repeat: its first occurrence takes it
+  const float penalty = params->penalty, v = logits[t];
+  logits[t] = v > 0 ? v / penalty : v * penalty;
+}
+
+// whether the step that chose `token` with largest logit `value` ends the call: a token that is not one (the draw's
+// SAMPLE_NOT_FINITE or SAMPLE_DECLINED), a largest logit that is not finite, or a stop token
+__device__ __forceinline__ bool halts(int32_t token, float value, const RunParams *params) {
+  if (token < 0 || !__builtin_isfinite(value)) return true;
+  const int ns = params->n_stops;
+  for (int j = 0; j < RUN_STOPS_MOST; ++j)
+    if (j < ns && params->stops[j] == token) return true;
+  return false;
+}
+
+// the logits of the step that ends the call, kept (the replays after it in the round overwrite the step's own)
+__global__ __launch_bounds__(256) void keep_halting_kernel(const float *logits, int32_t n, float *kept,
+                                                           const int32_t *token, const float *value,
+                                                           const int32_t *state, const RunParams *params) {
+  if (state[STATE_HALTED] != 0 || !halts(*token, *value, params)) return;  // (the same for every block)
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    kept[i] = logits[i];
+}
+
+// the end of a replayed step: its token and largest logit into ids / values at the step, the halting step noted
+// (state[STATE_HALTED] = step + 1, the first one only), the token appended to the penalty's window (a ring of
+// REPETITION_WINDOW once full), the token made the next step's input (a valid one after a step that chose none), the
+// position and the step advanced
+__global__ void advance_steps_kernel(int32_t *tokens, int32_t *state, const int32_t *token, const float *value,
+                                     int32_t *ids, float *values, int32_t *window, const RunParams *params) {
+  const int32_t step = state[STATE_STEP], b = *token;
+  const float v = *value;
+  ids[step] = b;
+  values[step] = v;
+  if (state[STATE_HALTED] == 0 && halts(b, v, params)) state[STATE_HALTED] = step + 1;
+  if (b >= 0) {
+    const int32_t count = state[STATE_WINDOW];
+    if (count < RUN_WINDOW) {
+      window[count] = b;
+      state[STATE_WINDOW] = count + 1;
+    } else {
+      const int32_t head = state[STATE_HEAD];
+      window[head] = b;
+      state[STATE_HEAD] = head + 1 == RUN_WINDOW ? 0 : head + 1;
+    }
+  }
+  tokens[0] = b >= 0 ? b : 0;
+  state[STATE_POS] = state[STATE_POS] + 1;
+  state[STATE_STEP] = step + 1;
+}
+
 }  // namespace
+
+hipError_t launch_sample_steps(const float *logits, int32_t n, const RunParams *params, const int32_t *state,
+                               float *probs, int32_t *index, int32_t *out_token, float *out_best, hipStream_t s) {
+  if (n < 1 || n > SAMPLE_MOST) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sample_steps_kernel, dim3(1), dim3(ST), 0, s, logits, n, params, state, probs, index, out_token,
+                     out_best);
+  return hipGetLastError();
+}
+
+hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
+                                 hipStream_t s) {
+  hipLaunchKernelGGL(penalize_steps_kernel, dim3(1), dim3(RUN_WINDOW), 0, s, logits, window, state, params);
+  return hipGetLastError();
+}
+
+hipError_t launch_step_end(const float *logits, int32_t n, float *kept, int32_t *tokens, int32_t *state,
+                           const int32_t *token, const float *value, int32_t *ids, float *values, int32_t *window,
+                           const RunParams *params, hipStream_t s) {
+  const int blocks = (int)std::min<int64_t>(128, ((int64_t)n + 1023) / 1024);
+  hipLaunchKernelGGL(keep_halting_kernel, dim3(blocks), dim3(256), 0, s, logits, n, kept, token, value, state, params);
+  hipLaunchKernelGGL(advance_steps_kernel, dim3(1), dim3(1), 0, s, tokens, state, token, value, ids, values, window,
+                     params);
+  return hipGetLastError();
+}
 
 hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, float penalty, hipStream_t s) {
   if (count < 1) return hipSuccess;
@@ -266,7 +426,7 @@ hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, 
 
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
                          int32_t *index, int32_t *out_token, float *out_best, hipStream_t s) {
-  if (n < 1 || !(temperature > 0)) return hipErrorInvalidValue;
+  if (n < 1 || n > SAMPLE_MOST || !(temperature > 0)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(ST), 0, s, logits, n, temperature, topp, random, probs, index,
                      out_token, out_best);
   return hipGetLastError();

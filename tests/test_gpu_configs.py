@@ -125,6 +125,32 @@ def test_qwen25_7b_int6_whole_model_against_the_oracle():
     against_the_oracle(cfg, tensors, ck, cos, sin, 128, 32, seed=26)
 
 
+def test_llama3_8b_widths_replayed_draws_with_a_stop_token():
+    """two layers of the Llama-3-8B shape, sampled steps on the device over the 128256-token vocabulary (temperature 0.8,
+    no nucleus, penalty 1.1) and greedy steps with the penalty, each in replayed calls that a stop token ends: every
+    token and the halting step's logits against the oracle's steps"""
+    from steps import oracle_steps
+    cfg, tensors, ck, cos, sin = model(LLAMA3_8B, THETA["llama3-8b"], seed=9, n_layers=2)
+    rng = np.random.default_rng(27)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=64)]
+    eng = package().open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    for temperature, topp, penalty in ((0.8, 1.0, 1.1), (0.0, 0.9, 1.1)):
+        eng.forwardMany([1] + prompt[:-1], 0)
+        ref.run([1] + prompt[:-1], 0, False)
+        history = [1] + prompt
+        randoms = list(rng.random(40))
+        want, logits = oracle_steps(ref, list(history), len(prompt), 40, temperature, topp, penalty, randoms)
+        stop = want[25]
+        first = want.index(stop)
+        got = eng.generateMany(history[-1], len(prompt), history[-64:], len(history), 40, temperature, topp, penalty,
+                               randoms if temperature > 0.0 else [], [stop, 1])
+        assert got == want[:want.index(1) + 1 if 1 in want[:first] else first + 1]
+        assert same_bits(eng.logits(), logits[len(got) - 1])
+    eng.release()
+    ref.close()
+
+
 def test_150m_whole_model_against_the_oracle():
     """the 150M shape, every layer: a 512-token prompt and 256 greedy steps, float16 cache"""
     cfg, tensors, ck, cos, sin = model(LLM_150M, THETA["llm150m"], seed=5)

@@ -352,6 +352,44 @@ def test_replayed_steps_with_stops_and_eager_steps_between(name):
     eng.release()
 
 
+@pytest.mark.parametrize("name", sorted(MODELS))
+@pytest.mark.parametrize("temperature, topp, penalty", [(0.8, 1.0, 1.1), (0.0, 0.9, 1.3)])
+def test_replayed_draws_with_stop_tokens(name, temperature, topp, penalty):
+    """generateMany's replayed steps with a stop token, a draw and a penalty (the call's settings, the round's random
+    numbers and the penalty's window in device memory): a call ends at the step that took the stop token, with that
+    step's (penalized) logits, though the round's later replays ran; the next calls go on from there, one of them over
+    more steps than a stop-token round (16), so that the window and the random numbers cross rounds. Tokens and logits
+    against the oracle's steps to the bit."""
+    from steps import oracle_steps
+    cfg, tensors, ck, cos, sin, _ = build(name)
+    rng = np.random.default_rng(int(100 * temperature + 10 * penalty))
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, size=10)]
+    total = min(46, cfg.seq_len - len(prompt))
+    randoms = list(rng.random(total)) if temperature > 0.0 else [0.0] * total
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    ref.run([1] + prompt[:-1], 0, False)
+    history = [1] + prompt
+    want, want_logits = oracle_steps(ref, list(history), len(prompt), total, temperature, topp, penalty, randoms)
+    eng = package().open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    eng.forwardMany([1] + prompt[:-1], 0)
+    stop = want[13]
+    first = want.index(stop)
+    unseen = [t for t in range(cfg.vocab_size) if t not in want][:3]
+    done, pos = 0, len(prompt)
+    for count, stops in ((30, [stop] + unseen), (6, []), (total - first - 7, unseen)):
+        r = randoms[done:done + count] if temperature > 0.0 else []
+        got = eng.generateMany(history[-1], pos, history[-64:], len(history), count, temperature, topp, penalty, r,
+                               stops)
+        n = first + 1 if done == 0 else count
+        assert got == want[done:done + n], (done, count)
+        assert same_bits(eng.logits(), want_logits[done + n - 1])
+        history += got
+        done, pos = done + n, pos + n
+    assert done == total
+    eng.release()
+    ref.close()
+
+
 def nucleus_size(logits, temperature, topp):
     """how many tokens the nucleus sort takes (float64 NumPy: the cases here lie far from the device's 8192)"""
     if not 0 < topp < 1:
