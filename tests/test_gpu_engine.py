@@ -453,3 +453,45 @@ def test_sampled_generation_matches_the_oracle(name, temperature, topp, penalty)
     if cfg.vocab_size < 8192:
         assert declined == 0
     eng.release()
+
+
+@pytest.mark.parametrize("name", ["tiny_gqa", "tiny_qwen_int6"])
+def test_prompt_attention_with_subnormal_products(name):
+    """the prompt attention's products on the matrix core (v_mfma_f32_32x32x1_2b_f32 for q.k, v_mfma_f32_16x16x1_4b_f32
+    for p.v, each with a zero accumulator) must give every product's float32 bits, subnormals kept: wq and wk scaled so
+    that q . k's products lie near 1e-39, wv so that the values (and p . v) are subnormal; a 40-token prompt through
+    forwardMany (the prompt kernels) and one more step with logits, cache and logits against the oracle to the bit"""
+    cfg, tensors, ck, cos, sin, _ = build(name)
+    pk = package()
+    ol.sharpen(cfg, tensors, ck, 1.5e-19)  # wq, wk: q and k near 3e-20
+    t = tensors[pk.T["wv"]]
+    n = cfg.n_layers * cfg.n_kv_heads * cfg.head_size * (cfg.dim // 32)
+    scales = np.frombuffer(ck[t.scales:t.scales + 4 * n].tobytes(), dtype=np.float32) * np.float32(5e-39)
+    ck[t.scales:t.scales + 4 * n] = np.frombuffer(scales.astype(np.float32).tobytes(), dtype=np.uint8)
+    for bias, factor in (("bq", 1.5e-19), ("bk", 1.5e-19), ("bv", 5e-39)):  # Qwen2's q/k/v biases alike
+        b = tensors[pk.T[bias]]
+        if b.offset:
+            m = ol.vector_length(cfg, bias)
+            v = np.frombuffer(ck[b.offset:b.offset + 4 * m].tobytes(), dtype=np.float32) * np.float32(factor)
+            ck[b.offset:b.offset + 4 * m] = np.frombuffer(v.astype(np.float32).tobytes(), dtype=np.uint8)
+    rng = np.random.default_rng(31)
+    tokens = [int(x) for x in rng.integers(0, cfg.vocab_size, size=41)]
+    ref = ol.Model(cfg, tensors, ck, cos, sin, max_block=64)
+    ref.run(tokens[:-1], 0, False)
+    ref.run([tokens[-1]], 40, True)
+    eng = pk.open_config(cfg, tensors, ck, cos, sin, max_block=64)
+    eng.forwardMany(tokens[:-1], 0)
+    eng.forward(tokens[-1], 40, True)
+    keys, values = ref.kv(0, 41)
+    kv = eng.keysAndValues(0, 41)
+    assert same_bits(kv["keys"], keys.reshape(-1)), "keys"
+    assert same_bits(kv["values"], values.reshape(-1)), "values"
+    assert same_bits(eng.logits(), ref.logits())
+    # the case is the one meant: many q . k-sized products (k . k of one head) and many values are subnormal
+    tiny = np.finfo(np.float32).tiny
+    k0 = keys[0].reshape(41, cfg.n_kv_heads, cfg.head_size)[:, 0, :]
+    prods = (k0[:, None, :] * k0[None, :, :]).astype(np.float32)
+    assert np.mean((prods != 0) & (np.abs(prods) < tiny)) > 0.2
+    assert np.mean((values != 0) & (np.abs(values) < tiny)) > 0.5
+    eng.release()
+    ref.close()
