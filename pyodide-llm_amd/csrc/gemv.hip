@@ -242,33 +242,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(const MatArgs a) {
 // The activations of a decode launch from the float32 token instead of quantize_x's output, in the block itself (no
 // launch of their own): with a.xnorm, rmsnorm first (kernels/kernel.ts:330-342: the squares in four lanes j % 4 added
 // in order by four threads, hsum ((l0 + l1) + l2) + l3, the tail; s = f32(1 / f32(sqrt(f32(ss / n) + eps)));
-// out = w * (s * x)), then quantize_x with bias 64 (kernels/kernel.ts:129-156) a half-wave a group, stored centred
-// (q - 64) into xl with the group scales into xsl. Every block computes the same bits. Thread tid of the block's NT
-// takes positions tid + NT u (group tid / 32 + NT / 32 u), requested by load_f32 before the rows. MAXU * NT >= K;
-// sq: 4 * chain_rowstride(K / 4) floats of LDS.
+// out = w * (s * x)), then quantize_x with bias 64 (kernels/kernel.ts:129-156), stored centred (q - 64) into xl with the
+// group scales into xsl. Every block computes the same bits. Thread tid of the block's NT takes the MAXU consecutive
+// positions from tid * MAXU (MAXU a divisor of 32 and a multiple of 4; MAXU * NT >= K), requested by load_f32 before
+// the rows as float4; a group of 32 is then 32 / MAXU neighbouring lanes, whose largest magnitude is their own
+// maxima's (DPP within the group's lanes), so that a lane computes one group's scale and its reciprocal, not MAXU of
+// them. sq: 4 * chain_rowstride(K / 4) floats of LDS.
 // NORM (rmsnorm with a.xnorm) is a template argument: a load under a run-time test of the pointer is waited for
 // before the next is requested, which made the token's loads one round trip each.
 template <int MAXU, bool NORM, int NT = 256>
 __device__ __forceinline__ void load_f32(const MatArgs &a, float (&xv)[MAXU], float (&wv)[MAXU]) {
+  static_assert(MAXU % 4 == 0 && 32 % MAXU == 0, "a lane's positions: whole float4, within one group");
 #pragma unroll
-  for (int u = 0; u < MAXU; ++u) {
-    const int j = min((int)threadIdx.x + NT * u, a.k - 1);  // clamped: every load unconditional
-    xv[u] = a.xf[j];
-    if constexpr (NORM) wv[u] = a.xnorm[j];
-    else wv[u] = 1.0f;
+  for (int u = 0; u < MAXU / 4; ++u) {
+    const int j = min((int)threadIdx.x * MAXU + 4 * u, a.k - 4);  // clamped: every load unconditional
+    const float4 x4 = *reinterpret_cast<const float4 *>(a.xf + j);
+    xv[4 * u] = x4.x; xv[4 * u + 1] = x4.y; xv[4 * u + 2] = x4.z; xv[4 * u + 3] = x4.w;
+    if constexpr (NORM) {
+      const float4 w4 = *reinterpret_cast<const float4 *>(a.xnorm + j);
+      wv[4 * u] = w4.x; wv[4 * u + 1] = w4.y; wv[4 * u + 2] = w4.z; wv[4 * u + 3] = w4.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wv[4 * u + e] = 1.0f;
+    }
   }
 }
 template <int MAXU, bool NORM, int NT = 256>
 __device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&xv)[MAXU], const float (&wv)[MAXU],
                                                uint8_t *xl, float *xsl, float *sq) {
   __shared__ float part[4], sval;
-  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = chain_rowstride(q4);
+  constexpr int LG = 32 / MAXU;  // lanes a group
+  const int tid = threadIdx.x, K = a.k, q4 = K >> 2, qs = chain_rowstride(q4), j0 = tid * MAXU;
   float sc = 1.0f;
   if constexpr (NORM) {
+    if (j0 < K) {
 #pragma unroll
-    for (int u = 0; u < MAXU; ++u) {
-      const int j = tid + NT * u;
-      if (j < K) sq[(j & 3) * qs + (j >> 2)] = xv[u] * xv[u];
+      for (int i = 0; i < MAXU; ++i) sq[(i & 3) * qs + ((j0 + i) >> 2)] = xv[i] * xv[i];
     }
     lds_barrier();
     if (tid < 4) part[tid] = lds_chain(sq + tid * qs, q4, 0.0f);
@@ -277,23 +286,31 @@ __device__ __forceinline__ void stage_from_f32(const MatArgs &a, const float (&x
     lds_barrier();
     sc = sval;
   }
-  // every group's maximum, scale and values computed unconditionally (positions past K repeat the last one and are
-  // not stored), so that the MAXU half-wave reductions overlap instead of running one after another
-  float o[MAXU], amax[MAXU];
+  float o[MAXU];
+  float m = 0.0f;
 #pragma unroll
-  for (int u = 0; u < MAXU; ++u) o[u] = NORM ? wv[u] * (sc * xv[u]) : xv[u];
+  for (int i = 0; i < MAXU; ++i) {
+    o[i] = NORM ? wv[i] * (sc * xv[i]) : xv[i];
+    m = __builtin_fmaxf(m, __builtin_fabsf(o[i]));
+  }
+  // the group's largest magnitude (order-free): xor 1 and xor 2 within quads, then the mirror within 8 lanes
+  if constexpr (LG >= 2) m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0xB1, 0xF, 0xF, true)));
+  if constexpr (LG >= 4) m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x4E, 0xF, 0xF, true)));
+  if constexpr (LG >= 8) m = __builtin_fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x141, 0xF, 0xF, true)));
+  const float scale = m / 63.0f;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  uint32_t words[MAXU / 4];
 #pragma unroll
-  for (int u = 0; u < MAXU; ++u) amax[u] = wave_max32(__builtin_fabsf(o[u]));
+  for (int u = 0; u < MAXU / 4; ++u) {
+    uint32_t w = 0;
 #pragma unroll
-  for (int u = 0; u < MAXU; ++u) {
-    const int j = tid + NT * u;
-    const float scale = amax[u] / 63.0f;
-    const float inv = scale > 0 ? 1.0f / scale : 0.0f;
-    const uint8_t q = (uint8_t)(quant_value(o[u], inv, 64) - 64);
-    if (j < K) {  // whole half-waves (K is a multiple of 32)
-      xl[j] = q;
-      if ((tid & 31) == 0) xsl[j >> 5] = scale;
-    }
+    for (int e = 0; e < 4; ++e) w |= (uint32_t)(uint8_t)(quant_value(o[4 * u + e], inv, 64) - 64) << (8 * e);
+    words[u] = w;
+  }
+  if (j0 < K) {  // whole groups (K is a multiple of 32)
+#pragma unroll
+    for (int u = 0; u < MAXU / 4; ++u) reinterpret_cast<uint32_t *>(xl + j0)[u] = words[u];
+    if (tid % LG == 0) xsl[j0 >> 5] = scale;
   }
 }
 
