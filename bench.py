@@ -92,24 +92,30 @@ def copy_calibration(nbytes=1 << 30, reps=4):
     print(json.dumps({"copy_bytes": nbytes, "copies": reps}))
 
 
-def read_ceiling(pk, nbytes=4 << 30, passes=4):
+def read_ceiling(pk, floors=(), nbytes=4 << 30, passes=4):
     """the HBM read bandwidth a plain streaming kernel reaches on this GPU (hk_read_ceiling, the device form of the
     reference's kernels/ceilings.ts read()): 4 GiB (more than the 256 MB MALL holds), the fastest of its launch shapes,
-    GB/s of one pass"""
+    GB/s of one pass; and for each size in `floors` the same kernel's cold read of that many bytes (hk_read_floor:
+    launches back to back, each on the next window of the 4 GiB), mean µs a launch"""
     lib = ctypes.CDLL("libamdhip64.so")
     buf = ctypes.c_void_p()
     if lib.hipMalloc(ctypes.byref(buf), ctypes.c_size_t(nbytes)) != 0:
         raise RuntimeError("hipMalloc failed")
+    us = {}
     try:
         if lib.hipMemset(buf, 1, ctypes.c_size_t(nbytes)) != 0:
             raise RuntimeError("hipMemset failed")
         checksum, ms = ctypes.c_int32(0), ctypes.c_double(0.0)
         pk.hip_engine.check(pk.library().hk_read_ceiling(buf, nbytes, passes, ctypes.byref(checksum), ctypes.byref(ms),
                                                          None))
+        for size in floors:
+            got = ctypes.c_double(0.0)
+            pk.hip_engine.check(pk.library().hk_read_floor(buf, nbytes, size - size % 64, 32, ctypes.byref(got), None))
+            us[size] = got.value
     finally:
         hip_sync()
         lib.hipFree(buf)
-    return nbytes / (ms.value * 1e-3) / 1e9
+    return nbytes / (ms.value * 1e-3) / 1e9, us
 
 
 def valu_ceiling(pk, passes=65536):
@@ -399,7 +405,13 @@ def main():
     rec = measure(pk, args.model, args.steps, args.warmup, args.prompt, detail=True, cpu=not args.no_cpu,
                   node=not args.no_node)
     print("ceilings", file=sys.stderr, flush=True)
-    ceiling_gbs = read_ceiling(pk)
+    by_matrix = rec["gemv_by_matrix"]
+    ceiling_gbs, floor_us = read_ceiling(pk, [m["bytes_per_launch"] for m in by_matrix.values()])
+    for m in by_matrix.values():
+        # one cold read of the matrix's bytes by the plain streaming kernel: the launch's ramp and first loads'
+        # latency included, which a small matrix cannot hide
+        m["stream_floor_us"] = round(floor_us[m["bytes_per_launch"]], 2)
+        m["frac_of_stream_floor"] = round(floor_us[m["bytes_per_launch"]] / m["us_per_launch"], 3)
     pairs_s, _ = valu_ceiling(pk)
     mfma_ops_s = mfma_ceiling(pk)
     rec["step_roofline"]["read_ceiling_gb_s"] = round(ceiling_gbs, 1)

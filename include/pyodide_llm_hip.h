@@ -255,6 +255,13 @@ int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float
  * else HE_E_HIP). *ms is the fastest shape's mean time of a pass (HIP events on the stream). Blocks until done. */
 int32_t hk_read_ceiling(const void *p, int64_t bytes, int32_t passes, int32_t *checksum, double *ms, void *stream);
 
+/* No counterpart in the reference (a measurement beside hk_read_ceiling): the time of one cold streaming read of
+ * `bytes` (a multiple of 64), as a decode matmul's launch reads its matrix: launches back to back, each reading the next
+ * window of `bytes` within the `span` bytes at the device pointer p (a span larger than the 256 MB MALL keeps every
+ * window cold), with hk_read_ceiling's kernel and launch shapes; *us is the fastest shape's mean microseconds a launch
+ * over `passes` launches. It allocates a few KiB. Blocks until done. */
+int32_t hk_read_floor(const void *p, int64_t span, int64_t bytes, int32_t passes, double *us, void *stream);
+
 /* The float32 multiply-add ceiling, kernels/ceilings.ts:27-50 fma(passes, w, x0, step) in every lane of a launch
  * that fills the device (8192 waves of 64): eight accumulators (starting at 0..7), a pass adds w_j * x and w_j * y
  * (w_j = w + {0, 2^-10, 2^-9, 3 * 2^-10}; x from x0, y from x0 + 0.25, both moving by -step a pass) to them, each

@@ -1535,6 +1535,46 @@ int32_t hk_read_ceiling(const void *p, int64_t bytes, int32_t passes, int32_t *c
   return HE_OK;
 }
 
+int32_t hk_read_floor(const void *p, int64_t span, int64_t bytes, int32_t passes, double *us, void *stream) {
+  if (!p || !us || bytes < 64 || bytes % 64 || span < bytes || passes < 1)
+    return fail(HE_E_ARG, "hk_read_floor: bad arguments");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t windows = span / bytes;  // launch i reads window i % windows
+  int32_t most = 1;
+  for (int32_t i = 0; i < read_ceiling_shapes(); ++i) most = std::max(most, read_ceiling_blocks(bytes, i));
+  uint32_t *partial = nullptr;
+  int32_t rc = dev_alloc(&partial, sizeof(uint32_t) * 4 * most);
+  if (rc) return rc;
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t err = hipEventCreate(&a);
+  if (err == hipSuccess) err = hipEventCreate(&b);
+  const uint8_t *base = reinterpret_cast<const uint8_t *>(p);
+  double best = 0;
+  int64_t window = 0;
+  auto next = [&]() { return base + (window++ % windows) * bytes; };
+  // each launch shape: three untimed launches, then `passes` back to back between an event pair, each on the next
+  // window; the fastest shape's mean launch
+  for (int32_t shape = 0; shape < read_ceiling_shapes() && err == hipSuccess; ++shape) {
+    for (int r = 0; r < 3 && err == hipSuccess; ++r) err = launch_read_ceiling(next(), bytes, shape, partial, s);
+    if (err == hipSuccess) err = hipEventRecord(a, s);
+    for (int32_t r = 0; r < passes && err == hipSuccess; ++r) err = launch_read_ceiling(next(), bytes, shape, partial, s);
+    if (err == hipSuccess) err = hipEventRecord(b, s);
+    if (err == hipSuccess) err = hipEventSynchronize(b);
+    float t = 0;
+    if (err == hipSuccess) err = hipEventElapsedTime(&t, a, b);
+    if (err != hipSuccess) break;
+    const double launch_us = 1e3 * (double)t / passes;
+    if (best == 0 || launch_us < best) best = launch_us;
+  }
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(partial);
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_read_floor: ") + hipGetErrorString(err));
+  *us = best;
+  return HE_OK;
+}
+
 int32_t hk_valu_ceiling(int32_t passes, float w, float x0, float step, float *result, double *ms, double *pairs,
                         void *stream) {
   if (!result || !ms || !pairs || passes < 1) return fail(HE_E_ARG, "hk_valu_ceiling: bad arguments");

@@ -104,6 +104,7 @@ def library():
             "hk_sample": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
             "hk_sample_static": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
             "hk_read_ceiling": (I32, [P, ctypes.c_int64, I32, P, P, P]),
+            "hk_read_floor": (I32, [P, ctypes.c_int64, ctypes.c_int64, I32, P, P]),
             "hk_valu_ceiling": (I32, [I32, F, F, F, P, P, P, P]),
             "hk_mfma_ceiling": (I32, [I32, I32, I32, I32, P, P, P, P]),
         }

@@ -157,6 +157,20 @@ def test_read_ceiling_checksum(nbytes, passes):
     assert ms.value > 0
 
 
+def test_read_floor_times_cold_windows():
+    """hk_read_floor times one launch of the read kernel over each next window of the span: a positive time a launch
+    that grows with the bytes read, and arguments it cannot use refused"""
+    span = 64 << 20
+    buf = gl.upload(np.ones(span // 4, dtype=np.uint32))
+    lib = package().library()
+    small, large = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    gl.check(lib.hk_read_floor(buf.ptr, span, 1 << 20, 8, ctypes.byref(small), None))
+    gl.check(lib.hk_read_floor(buf.ptr, span, 32 << 20, 4, ctypes.byref(large), None))
+    assert 0 < small.value < large.value
+    for nbytes, spanned in ((100, span), (1 << 20, 1 << 19)):
+        assert lib.hk_read_floor(buf.ptr, spanned, nbytes, 1, ctypes.byref(small), None) != 0
+
+
 def fma_lane(passes, w, x0, step):
     """kernels/ceilings.ts fma() for one lane in float32, each step rounded (the benchmark page's fmaSum before its
     four-lane sum)"""
