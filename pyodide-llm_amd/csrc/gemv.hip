@@ -811,12 +811,16 @@ hipError_t launch_gemv6(const MatArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+constexpr int32_t SMALL_ROWS6 = 8192;
+
 hipError_t launch_decode6(const MatArgs &a, hipStream_t s) {
   const int steps = (a.k / GS + 127) / 128;  // 3 KiB steps of a row
   // the float32 token: 16 rows a block as the 4 waves of 4 rows, but 16 waves of one row (8 of two where the q/k/v
   // epilogue takes rows in pairs), so that quantize_x of the token is 4 values a thread
   if (steps <= 1) {
-    if (!a.xf) return launch_gemv6<4, 1>(a, s);
+    // from xq: two rows a wave for the small matrices (q/k/v, wo: measured on cold copies at K = 3584, 4 rows a wave
+    // leave too few waves for their few MB: q/k/v 7.0 -> 6.1 µs, wo 5.7 -> 5.4), four for the large
+    if (!a.xf) return a.total_rows <= SMALL_ROWS6 ? launch_gemv6<2, 1>(a, s) : launch_gemv6<4, 1>(a, s);
     return a.qkv.on ? launch_gemv6<2, 1, 8>(a, s) : launch_gemv6<1, 1, 16>(a, s);
   }
   if (a.xf) return hipErrorInvalidValue;
@@ -998,7 +1002,7 @@ int32_t decode_block_rows(int32_t k, int32_t total_rows, bool six, bool relaxed,
   }
   if (k > 24 * 1024 || (k / GS) % 2) return 0;
   const int steps = (k / GS + 127) / 128;
-  if (steps <= 1) return 4 * WAVES;
+  if (steps <= 1) return (!xf && total_rows <= SMALL_ROWS6 ? 2 : 4) * WAVES;
   if (steps <= 2) return 2 * WAVES;
   if (steps <= 6) return WAVES;
   return 0;
