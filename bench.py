@@ -41,8 +41,8 @@ TRAFFIC = {
     "llama3-8b": {"bytes_per_pass": round((2 * (32 * (13900 + 9304 + 64600 + 32500) + 288700)
                                            + (32 * (48.63 + 16 + 112 + 32) + 502.3)) * 1024),
                   "source": "profiles/decode_gemv_llama3-8b.md"},
-    "qwen25-7b-int6": {"bytes_per_pass": round((2 * (28 * (7172 + 5580 + 58120 + 29260) + 233000)
-                                                + (28 * (30.32 + 14 + 148.1 + 28) + 594.6)) * 1024),
+    "qwen25-7b-int6": {"bytes_per_pass": round((2 * (28 * (7180.9 + 5583.0 + 58119.9 + 29261.5) + 232951.8)
+                                                + (28 * (32.1 + 14 + 148.1 + 28) + 594.6)) * 1024),
                        "source": "profiles/decode_gemv6_qwen25-7b-int6.md"},
 }
 
