@@ -18,6 +18,11 @@
 #include "kernels.hpp"
 
 namespace ple {
+#if GEMV_PAD
+extern "C" __global__ void ple_pad_kernel(int *out) {
+  if (out) asm volatile(".fill %0, 4, 0xbf800000" ::"i"(GEMV_PAD / 4));
+}
+#endif
 
 namespace {
 
