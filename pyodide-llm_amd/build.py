@@ -23,6 +23,10 @@ NODE_INCLUDE = "/usr/include/node"
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
              "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function"]
+# the decode step's kernels first in each source's code object (function sections, ordered by the device linker)
+ORDER = os.path.join(CSRC, "decode_order.txt")
+ORDER_FLAGS = ["-ffunction-sections", "-Xoffload-linker", f"--symbol-ordering-file={ORDER}", "-Xoffload-linker",
+               "--no-warn-symbol-ordering"]
 SOURCES = ["gemv.hip", "gemm.hip", "misc.hip", "forms.hip", "attention.hip", "attention_tokens.hip", "sampling.hip",
            "ceilings.hip", "engine.cpp"]
 
@@ -37,7 +41,7 @@ def run(cmd):
 def compile_one(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else ["-x", "hip"]
-    run([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
+    run([HIPCC, *HIP_FLAGS, *ORDER_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 

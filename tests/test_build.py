@@ -52,3 +52,27 @@ def test_no_kernel_uses_scratch(tmp_path):
                     scratch.append((name, int(m.group(1))))
     assert kernels > 100
     assert not scratch, scratch
+
+
+@pytest.mark.skipif(not (os.path.exists(f"{LLVM}/clang-offload-bundler") and shutil.which("objcopy")),
+                    reason="ROCm's clang-offload-bundler or objcopy missing")
+def test_decode_kernels_lead_their_code_objects(tmp_path):
+    """every name of csrc/decode_order.txt is a kernel of the library, and in its code object those named lie first,
+    in the file's order (the device linker's symbol order; a renamed kernel would otherwise drop out of it silently)"""
+    order_file = os.path.join(os.path.dirname(package().hip_engine.LIBRARY), "csrc", "decode_order.txt")
+    wanted = [ln.strip() for ln in open(order_file) if ln.strip() and not ln.startswith("#")]
+    assert len(wanted) == len(set(wanted)) > 10
+    found = set()
+    for co in code_objects(tmp_path):
+        syms = subprocess.run([f"{LLVM}/llvm-readelf", "-sW", str(co)], check=True, stdout=subprocess.PIPE,
+                              text=True).stdout
+        funcs = {}
+        for line in syms.splitlines():
+            f = line.split()
+            if len(f) >= 8 and f[3] == "FUNC" and int(f[2]) > 0:
+                funcs.setdefault(f[7], int(f[1], 16))
+        by_address = [name for name, _ in sorted(funcs.items(), key=lambda kv: kv[1])]
+        here = [name for name in wanted if name in funcs]
+        assert by_address[:len(here)] == here, (co.name, by_address[:len(here)], here)
+        found.update(here)
+    assert found == set(wanted), sorted(set(wanted) - found)
