@@ -539,6 +539,33 @@ hipError_t gemm_launch(he_engine *e, const MatSeg *segs, int nseg, int32_t k, in
   return launch_gemm(a, e->c.six, e->c.relaxed, e->stream);
 }
 
+// the prompt's w1 / w3 GEMM with the SwiGLU in its epilogue, writing quantize_x of its output to gq / gs
+// ([m][widest] bytes, [m][widest / 32] scales)
+hipError_t gemm_glu_launch(he_engine *e, const MatSeg *w13, int32_t k, int32_t m, const int8_t *xq, const float *xs,
+                           int8_t *gq, float *gs) {
+  MatArgs a{};
+  a.nseg = 2;
+  a.seg[0] = w13[0];
+  a.seg[1] = w13[1];
+  a.total_rows = w13[0].rows + w13[1].rows;
+  a.xq = xq;
+  a.xs = xs;
+  a.xq_stride = e->widest;
+  a.xs_stride = e->widest / 32;
+  a.k = k;
+  a.m = m;
+  a.glu = GluOut{gq, gs, e->widest, e->widest / 32, e->bias};
+  return launch_gemm_glu(a, e->c.six, e->stream);
+}
+
+// whether a chunk of m tokens takes the GEMM's SwiGLU epilogue: the w1 / w3 matmul on the GEMM, hidden units in whole
+// groups, and the float32 buffers of h1 / h3 large enough for the quantized output ([chunk][widest] bytes in hb,
+// [chunk][widest / 32] floats in hb2)
+bool glu_in_gemm(const he_engine *e, int32_t m) {
+  const int32_t hidden = e->c.hidden_dim;
+  return use_gemm(e, e->c.dim, m) && hidden % 32 == 0 && e->widest % 4 == 0 && e->widest <= 4 * (int64_t)hidden;
+}
+
 hipError_t matmul(he_engine *e, const MatSeg *segs, int nseg, int32_t k, int32_t m, const int8_t *xq, const float *xs,
                   const F32Source *f32 = nullptr, const QkvFuse *qkv = nullptr, bool persistent = false) {
   if (use_gemm(e, k, m))
@@ -748,9 +775,19 @@ int32_t run_chunk(he_engine *e, const int32_t *tokens, int32_t m, int32_t pos0, 
                                     W, W / 32, 0, c.rms_norm_eps, e->bias, s, &f13);
       }));
     }
+    const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
+    if (glu_in_gemm(e, m)) {
+      // the GEMM finishes the SwiGLU and its quantize_x itself; its bytes and scales go where h1 and h3 would (hb and
+      // hb2 hold [chunk][W] bytes and [chunk][W / 32] floats: glu_in_gemm checks), apart from the w1 / w3 GEMM's
+      // input in xq / xs
+      int8_t *gq = reinterpret_cast<int8_t *>(e->hb);
+      HIP_TRY(timed(e, HE_K_GEMM, matmul_bytes(e, w13, 2, dim, m),
+                    [&] { return gemm_glu_launch(e, w13, dim, m, e->xq, e->xs, gq, e->hb2); }));
+      HIP_TRY(matmul(e, w2, 1, hidden, m, gq, e->hb2));
+      continue;
+    }
     const F32Source ffn_src{e->x, e->vec(HE_T_RMS_FFN, (int64_t)l * dim)};
     HIP_TRY(matmul(e, w13, 2, dim, m, e->xq, e->xs, norm_in_gemv ? &ffn_src : nullptr));
-    const MatSeg w2[1] = {{e->mat(HE_T_W2, l), e->mat_scales(HE_T_W2, l), e->x, dim, dim, 1}};
     HIP_TRY(timed(e, HE_K_ELEMENTWISE, (double)m * hidden * (8 + 1 + 0.125), [&] {
       return launch_swiglu_quant(e->xq, e->xs, nullptr, e->hb, e->hb2, m, hidden, hidden, W, W / 32, e->bias, s);
     }));

@@ -63,12 +63,19 @@ struct Fetch {
   float xsv[2];
 };
 
-template <bool SIX, bool SUMS>
+// (GLU: r0 is the block's first hidden unit; its rows 0-31 are w1's units r0.., rows 32-63 w3's)
+template <bool SIX, bool SUMS, bool GLU>
 __device__ __forceinline__ void fetch(Fetch<SIX> &f, const MatArgs &a, int r0, int t0, int g0, int G, int tid) {
   // rows, groups and tokens past the end clamped: the loads stay unconditional and valid; what they bring is never
   // added
-  const int row = min(r0 + (tid >> 2), a.total_rows - 1), g = min(g0 + (tid & 3), G - 1);
-  const SegRow s = seg_row(a, row);
+  const int g = min(g0 + (tid & 3), G - 1);
+  SegRow s;
+  if constexpr (GLU) {
+    const int r = tid >> 2, unit = min(r0 + (r & 31), a.seg[0].rows - 1);
+    s = r < 32 ? SegRow{a.seg[0].w, a.seg[0].ws, unit} : SegRow{a.seg[1].w, a.seg[1].ws, unit};
+  } else {
+    s = seg_row(a, min(r0 + (tid >> 2), a.total_rows - 1));
+  }
   if constexpr (SIX) {
     const uint2 *p = reinterpret_cast<const uint2 *>(s.w + ((int64_t)s.r * G + g) * 24);
     const uint2 l0 = p[0], l1 = p[1], tops = p[2];
@@ -159,9 +166,53 @@ __device__ __forceinline__ void write_sums(const MatArgs &a, const v16i &S, int 
   }
 }
 
-// with SUMS the kernel writes the exact int32 group sums S_g to a.sums [m][rows][G] instead (one segment)
+// The SwiGLU epilogue (GLU): the block's rows are 32 hidden units of w1 (the waves wr = 0) and the same units of w3
+// (wr = 1), so a lane of wave (0, wt) and the same lane of wave (1, wt) hold h1 and h3 of the same (unit, token) in the
+// same registers. Each wave hands its partner the tile it does not finish through LDS: wave (0, wt) finishes tile 0
+// (tokens 0-31 of its 64), wave (1, wt) tile 1. o = h1 / (1 + vexp(-h1)) * h3 as swiglu_quant4_kernel computes it,
+// then quantize_x of the token's group of 32 units (the block's 32): the largest magnitude over the lane's 16 values
+// and its partner lane's (lane ^ 32, the group's other 16; order-free), the scale and its reciprocal as
+// quantize_group4 makes them, four bytes a run of four units.
+__device__ __forceinline__ void glu_epilogue(const MatArgs &a, float (&out)[2][16], float *xch, int u0, int t0,
+                                             int wave, int lane) {
+  const int wr = wave & 1, wt = wave >> 1;
+  __syncthreads();  // every wave is done reading the stages
+#pragma unroll
+  for (int v = 0; v < 16; ++v) xch[(wave * 16 + v) * 64 + lane] = wr ? out[0][v] : out[1][v];
+  __syncthreads();
+  float o[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const float other = xch[((wave ^ 1) * 16 + v) * 64 + lane];
+    const float h1 = wr ? other : out[0][v], h3 = wr ? out[1][v] : other;
+    o[v] = h1 / (1.0f + vexp(-h1)) * h3;
+  }
+  float amax = __builtin_fabsf(o[0]);
+#pragma unroll
+  for (int v = 1; v < 16; ++v) amax = __builtin_fmaxf(amax, __builtin_fabsf(o[v]));
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
+  const int t = t0 + wt * 64 + wr * 32 + (lane & 31);
+  if (t >= a.m) return;
+  const GluOut &g = a.glu;
+  const float qmax = g.bias == 0 ? 127.0f : 63.0f;
+  const float scale = amax / qmax;
+  const float inv = scale > 0 ? 1.0f / scale : 0.0f;
+  int8_t *q = g.q + (int64_t)t * g.q_stride + u0 + (lane >> 5) * 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t w = (uint32_t)(uint8_t)quant_value(o[4 * r], inv, g.bias) |
+                       ((uint32_t)(uint8_t)quant_value(o[4 * r + 1], inv, g.bias) << 8) |
+                       ((uint32_t)(uint8_t)quant_value(o[4 * r + 2], inv, g.bias) << 16) |
+                       ((uint32_t)(uint8_t)quant_value(o[4 * r + 3], inv, g.bias) << 24);
+    *reinterpret_cast<uint32_t *>(q + r * 8) = w;  // units u0 + 8 r + (lane / 32) * 4 ..
+  }
+  if (lane < 32) g.s[(int64_t)t * g.s_stride + u0 / 32] = scale;
+}
+
+// with SUMS the kernel writes the exact int32 group sums S_g to a.sums [m][rows][G] instead (one segment); with GLU
+// the SwiGLU's quantized output (glu_epilogue)
 // (two waves a SIMD: the register budget that keeps the MFMA results in VGPRs, no AGPR copies)
-template <bool SIX, bool SUMS>
+template <bool SIX, bool SUMS, bool GLU>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(const MatArgs a) {
   __shared__ Stage stage[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -172,7 +223,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void ge
   const int tbn = (a.m + BT - 1) / BT, nblk = gridDim.x;
   const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
   const int idx = xcd * (nblk / 8) + min(xcd, nblk % 8) + j;
-  const int r0 = (idx / tbn) * BR, t0 = (idx % tbn) * BT;
+  const int r0 = (idx / tbn) * (GLU ? BR / 2 : BR), t0 = (idx % tbn) * BT;
   const int G = a.k / 32, G4 = G & ~3, steps = G4 / KS, tail = G - G4;
 
   float acc[2][KS][16];
@@ -196,7 +247,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void ge
   Fetch<SIX> f;
   const int total = steps + (tail ? 1 : 0);
   if (total > 0) {
-    fetch<SIX, SUMS>(f, a, r0, t0, 0, G, tid);
+    fetch<SIX, SUMS, GLU>(f, a, r0, t0, 0, G, tid);
     store<SIX>(stage[0], f, tid);
   }
   __syncthreads();
@@ -205,7 +256,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     // the next stage fetched and stored unconditionally (no branch that would let the compiler move the products
     // below the stores): its groups are clamped into the row, and past the last stage what it stores goes to the
     // buffer no later read takes (the tail's stage is a real one: total > steps)
-    fetch<SIX, SUMS>(f, a, r0, t0, (s + 1) * KS, G, tid);
+    fetch<SIX, SUMS, GLU>(f, a, r0, t0, (s + 1) * KS, G, tid);
     // a group's two MFMAs issued together, then their float32 work
 #pragma unroll
     for (int gi = 0; gi < KS; ++gi) {
@@ -265,6 +316,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void ge
   }
 
   if constexpr (SUMS) return;
+  if constexpr (GLU) {
+    glu_epilogue(a, out, reinterpret_cast<float *>(&stage[0]), r0, t0, wave, lane);
+    return;
+  }
   // y[t][r] = out (or y + out): the lane's two tokens, its 16 rows in 4 runs of 4
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -304,15 +359,33 @@ hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s) 
   const dim3 grid((unsigned)blocks);
   if (a.sums) {
     if (six)
-      gemm_kernel<true, true><<<grid, NT, 0, s>>>(a);
+      gemm_kernel<true, true, false><<<grid, NT, 0, s>>>(a);
     else
-      gemm_kernel<false, true><<<grid, NT, 0, s>>>(a);
+      gemm_kernel<false, true, false><<<grid, NT, 0, s>>>(a);
   } else {
     if (six)
-      gemm_kernel<true, false><<<grid, NT, 0, s>>>(a);
+      gemm_kernel<true, false, false><<<grid, NT, 0, s>>>(a);
     else
-      gemm_kernel<false, false><<<grid, NT, 0, s>>>(a);
+      gemm_kernel<false, false, false><<<grid, NT, 0, s>>>(a);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_glu(const MatArgs &a, bool six, hipStream_t s) {
+  const GluOut &g = a.glu;
+  if (a.m < 1 || a.nseg != 2 || a.sums || !gemm_supported(a.k, true)) return hipErrorInvalidValue;
+  const int hidden = a.seg[0].rows;
+  if (hidden < 32 || hidden % 32 || a.seg[1].rows != hidden || a.total_rows != 2 * hidden) return hipErrorInvalidValue;
+  // the output's 4-byte runs and its scales: every store aligned and inside [m][q_stride] / [m][s_stride]
+  if (!g.q || !g.s || (g.bias != 0 && g.bias != 64) || g.q_stride < hidden || g.q_stride % 4 ||
+      g.s_stride < hidden / 32 || reinterpret_cast<uintptr_t>(g.q) % 4)
+    return hipErrorInvalidValue;
+  const int64_t blocks = (int64_t)(hidden / 32) * ((a.m + BT - 1) / BT);
+  if (blocks > (1ll << 30)) return hipErrorInvalidValue;
+  if (six)
+    gemm_kernel<true, false, true><<<dim3((unsigned)blocks), NT, 0, s>>>(a);
+  else
+    gemm_kernel<false, false, true><<<dim3((unsigned)blocks), NT, 0, s>>>(a);
   return hipGetLastError();
 }
 

@@ -50,6 +50,14 @@ struct L2Fetch {
   int32_t blocks;       // the extra blocks (a multiple of 8; 0: none)
   uint32_t *sink;       // 64 words, written only where the touched words' xor hits a constant (keeps the loads)
 };
+// The prompt's w1 / w3 GEMM finishing the SwiGLU in its epilogue (launch_gemm_glu): seg[0] is w1 and seg[1] w3, the
+// same number of rows (hidden units, a multiple of 32); q / s take quantize_x(bias) of h1 / (1 + vexp(-h1)) * h3, the
+// bytes and scales launch_swiglu_quant makes of the two outputs.
+struct GluOut {
+  int8_t *q;  // [m][q_stride]
+  float *s;   // [m][s_stride]
+  int32_t q_stride, s_stride, bias;
+};
 struct MatArgs {
   MatSeg seg[3];
   int32_t nseg;
@@ -70,6 +78,7 @@ struct MatArgs {
   // one token, rows of 1-4 KiB (decode_persistent): the persistent GEMV, about one block a CU that loops over its
   // rows (no L2Fetch fits it: its blocks take rows in another order)
   int32_t persistent;
+  GluOut glu;  // launch_gemm_glu only
 };
 
 // rows a block of the one-token decode GEMV takes (launch_gemv with m = 1, bias 64, no sums) for rows of k, 0 where
@@ -92,6 +101,8 @@ int32_t gemv_tokens(int32_t k, bool relaxed);
 // prefill GEMM on i8 MFMA, any m (bias 64, int8 or int6): the same bits as launch_gemv per (token, row); with
 // a.sums (one segment) the exact int32 group sums [m][rows][K/32] instead
 hipError_t launch_gemm(const MatArgs &a, bool six, bool relaxed, hipStream_t s);
+// the w1 / w3 GEMM with the SwiGLU and its quantize_x in the epilogue (a.glu; bias 64 weights only)
+hipError_t launch_gemm_glu(const MatArgs &a, bool six, hipStream_t s);
 bool gemm_supported(int32_t k, bool relaxed);
 
 // quantize_x over m rows of n (x_stride apart) into xq (xq_stride) / xs (xs_stride)
