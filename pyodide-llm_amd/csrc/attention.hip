@@ -295,11 +295,12 @@ __global__ __launch_bounds__(Attend<HS>::NT) void attend_kernel(const AttnArgs a
 // (B + C) for a few tokens (decode) whose output the caller quantizes itself: one block of 1024 threads a (token,
 // query head, 16 columns), thread b owning the four-position block b (positions 4b .. 4b+3) of the weighted values.
 // The head's tile maxima and scores are requested at once, the exponentials go into LDS by lane (four rows: positions
-// t % 4 == k), four lanes of wave 0 run the ordered sums; then every thread requests its block's 16 columns x 4
-// values, turns them into the columns' four-position products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), p = e * f32(1 /
-// sum), into LDS rows (one a column), and 16 lanes of wave 0 add their column's products in order, then the tail.
-// (The values are requested after the sums: requested at the start, their arrival slowed the scores' loads and
-// the exponential sum.) Blocks of the query heads that share a kv head's columns go to one XCD, as in attend_kernel.
+// t % 4 == k); then every thread requests its block's 16 columns x 4 values while four lanes of wave 0 run the
+// ordered sums, turns them into the columns' four-position products ((p0 v0 + p1 v1) + (p2 v2 + p3 v3)), p = e *
+// f32(1 / sum), into LDS rows (one a column), and 16 lanes of wave 0 add their column's products in order, then the
+// tail. (The values are requested once the exponentials are in LDS: requested at the start, their arrival slowed the
+// scores' loads and the exponentials.) Blocks of the query heads that share a kv head's columns go to one XCD, as in
+// attend_kernel.
 constexpr int A2_NT = 1024;  // threads a block
 constexpr int A2_AC = 16;    // columns a block
 constexpr int A2_SV = 4;     // scores a thread a pass (4096 positions)
@@ -371,9 +372,17 @@ __global__ __launch_bounds__(A2_NT) void attend2_kernel(const AttnArgs a) {
     }
   }
   __syncthreads();
+  // the first pass's values requested now (clamped into the column: never used past q4): they fly while wave 0 runs
+  // the exponentials' ordered sum (its reads 32 values at a time, so that both fit the registers)
+  float4 v0[AC];
+  {
+    const int bc = max(min(tid, q4 - 1), 0);
+#pragma unroll
+    for (int j = 0; j < AC; ++j) v0[j] = cache4<HALF>(a.vcache, vcol + (int64_t)j * a.vstride + 4 * bc);
+  }
   if (wave == 0) {
     // lanes 0-3: lane k's sum; ((l0 + l1) + l2) + l3, the tail in order, 1 / sum
-    const float part = lane < 4 ? lds_chain(e4 + lane * rs, q4, 0.0f) : 0.0f;
+    const float part = lane < 4 ? lds_chain_h<4>(e4 + lane * rs, q4, 0.0f) : 0.0f;
     const float c1 = __shfl(part, 1, 64), c2 = __shfl(part, 2, 64), c3 = __shfl(part, 3, 64);
     if (lane == 0) {
       float sum = ((part + c1) + c2) + c3;
@@ -383,11 +392,8 @@ __global__ __launch_bounds__(A2_NT) void attend2_kernel(const AttnArgs a) {
   }
   __syncthreads();
   const float inv = shared_inv;
-  for (int b0 = 0; b0 < q4; b0 += NT) {  // (a scalar loop: every thread takes the same passes)
-    const int b = b0 + tid, bc = min(b, q4 - 1);  // clamped: never stored past q4
-    float4 v[AC];
-#pragma unroll
-    for (int j = 0; j < AC; ++j) v[j] = cache4<HALF>(a.vcache, vcol + (int64_t)j * a.vstride + 4 * bc);
+  // block b's products: (p0 v0 + p1 v1) + (p2 v2 + p3 v3) for the 16 columns, into the columns' rows
+  auto products = [&](int b, const float4 (&v)[AC]) {
     if (b < q4) {
       const float p0 = e4[b] * inv, p1 = e4[rs + b] * inv, p2 = e4[2 * rs + b] * inv, p3 = e4[3 * rs + b] * inv;
 #pragma unroll
@@ -396,6 +402,14 @@ __global__ __launch_bounds__(A2_NT) void attend2_kernel(const AttnArgs a) {
         blk[j * rs + b] = (p0 * x.x + p1 * x.y) + (p2 * x.z + p3 * x.w);
       }
     }
+  };
+  products(tid, v0);
+  for (int b0 = NT; b0 < q4; b0 += NT) {  // (a scalar loop: every thread takes the same passes)
+    const int b = b0 + tid, bc = min(b, q4 - 1);  // clamped: never stored past q4
+    float4 v[AC];
+#pragma unroll
+    for (int j = 0; j < AC; ++j) v[j] = cache4<HALF>(a.vcache, vcol + (int64_t)j * a.vstride + 4 * bc);
+    products(b, v);
   }
   __syncthreads();
   if (wave == 0 && lane < AC) {

@@ -165,25 +165,44 @@ __host__ __device__ constexpr int chain_rowstride(int q4) { return ((q4 + 63) & 
 // acc + c[0] + c[1] + ... + c[n-1] in order (every add rounded), the values read from LDS 64 at a time: the second
 // 32's reads fly while the first 32 are added. (No reads carried across iterations: a loop-carried set of registers
 // makes the compiler copy it every iteration, which costs more than the latency it hides.) c 16-byte aligned.
-__device__ __forceinline__ float lds_chain(const float *c, int n, float acc) {
+template <int H = 8>
+__device__ __forceinline__ float lds_chain_h(const float *c, int n, float acc) {
   const float4 *c4 = reinterpret_cast<const float4 *>(c);
   const int n4 = n >> 2;
   int i = 0;
-  for (; i + 16 <= n4; i += 16) {
-    float4 a[8], b[8];
+  for (; i + 2 * H <= n4; i += 2 * H) {
+    float4 a[H], b[H];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = c4[i + u];
+    for (int u = 0; u < H; ++u) a[u] = c4[i + u];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) b[u] = c4[i + 8 + u];
-    acc = add32(acc, a);
-    acc = add32(acc, b);
+    for (int u = 0; u < H; ++u) b[u] = c4[i + H + u];
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+      acc = acc + a[u].x;
+      acc = acc + a[u].y;
+      acc = acc + a[u].z;
+      acc = acc + a[u].w;
+    }
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+      acc = acc + b[u].x;
+      acc = acc + b[u].y;
+      acc = acc + b[u].z;
+      acc = acc + b[u].w;
+    }
   }
-  if (i + 8 <= n4) {
-    float4 a[8];
+  if (i + H <= n4) {
+    float4 a[H];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = c4[i + u];
-    acc = add32(acc, a);
-    i += 8;
+    for (int u = 0; u < H; ++u) a[u] = c4[i + u];
+#pragma unroll
+    for (int u = 0; u < H; ++u) {
+      acc = acc + a[u].x;
+      acc = acc + a[u].y;
+      acc = acc + a[u].z;
+      acc = acc + a[u].w;
+    }
+    i += H;
   }
   for (; i < n4; ++i) {
     const float4 v = c4[i];
@@ -195,6 +214,7 @@ __device__ __forceinline__ float lds_chain(const float *c, int n, float acc) {
   for (int j = n4 << 2; j < n; ++j) acc = acc + c[j];
   return acc;
 }
+__device__ __forceinline__ float lds_chain(const float *c, int n, float acc) { return lds_chain_h<8>(c, n, acc); }
 
 // An ordered sum run from registers by the 32 lanes of a half-wave: 0 + c[0] + c[1] + ... in order, every add
 // rounded, over c = the sum's row of values (16-byte aligned), +0.0 from its count up to 32 * nseg (x + 0 is x for sums
