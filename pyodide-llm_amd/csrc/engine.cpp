@@ -379,7 +379,7 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->state, sizeof(int32_t) * STATE_WORDS);
   ALLOC(e->step_ids, sizeof(int32_t) * STEPS_A_ROUND);
   ALLOC(e->step_values, sizeof(float) * STEPS_A_ROUND);
-  ALLOC(e->sample_probs, sizeof(float) * c.vocab_size);
+  ALLOC(e->sample_probs, sizeof(float) * sample_probs_floats(c.vocab_size));
   ALLOC(e->sample_index, sizeof(int32_t) * c.vocab_size);
   ALLOC(e->window, sizeof(int32_t) * REPETITION_WINDOW);
   ALLOC(e->sample_token, sizeof(int32_t) * 4);
@@ -1415,7 +1415,7 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   float *probs = nullptr, *best = nullptr;
   int32_t *index = nullptr, *out = nullptr;
-  int32_t rc = dev_alloc(&probs, sizeof(float) * n);
+  int32_t rc = dev_alloc(&probs, sizeof(float) * sample_probs_floats(n));
   if (!rc) rc = dev_alloc(&index, sizeof(int32_t) * n);
   if (!rc) rc = dev_alloc(&out, sizeof(int32_t) * 4);
   if (!rc) rc = dev_alloc(&best, sizeof(float) * 4);
@@ -1444,6 +1444,8 @@ namespace ple {
 constexpr size_t SAMPLE_INDEX_AT = 4 * (size_t)HK_SAMPLE_STATIC_MOST, SAMPLE_TOKEN_AT = 8 * (size_t)HK_SAMPLE_STATIC_MOST;
 constexpr size_t SAMPLE_BEST_AT = SAMPLE_TOKEN_AT + 256, SAMPLE_SCRATCH_BYTES = SAMPLE_BEST_AT + 256;
 __device__ __align__(256) uint8_t scratch[SAMPLE_SCRATCH_BYTES];
+static_assert(sample_probs_floats(HK_SAMPLE_STATIC_MOST) == (size_t)HK_SAMPLE_STATIC_MOST,
+              "the probabilities' region holds the sampler's whole chunks");
 }  // namespace ple
 
 namespace {

@@ -199,9 +199,13 @@ hipError_t launch_argmax(int32_t *out, float *value, const float *x, int32_t n, 
 hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, float penalty, hipStream_t s);
 // one token drawn from softmax(logits / temperature) (kernels/kernel.ts:803-868) for random in [0, 1), restricted to
 // the nucleus where 0 < topp < 1; *out_token is the token, SAMPLE_NOT_FINITE where the largest logit is not finite,
-// or SAMPLE_DECLINED where the nucleus holds more tokens than one block sorts. probs, index: scratch of n each.
+// or SAMPLE_DECLINED where the nucleus holds more tokens than one block sorts. probs: scratch of sample_probs_floats(n)
+// (the float64 total reads whole chunks of SAMPLE_CHUNK, using none past n); index: scratch of n.
 constexpr int32_t SAMPLE_NOT_FINITE = -1, SAMPLE_DECLINED = -2;
 constexpr int32_t SAMPLE_MOST = 262144;  // logits a draw takes at most
+constexpr int32_t SAMPLE_CHUNK = 2048;
+constexpr size_t sample_probs_floats(int32_t n) { return ((size_t)n + SAMPLE_CHUNK - 1) / SAMPLE_CHUNK * SAMPLE_CHUNK; }
+static_assert(SAMPLE_MOST % SAMPLE_CHUNK == 0, "the largest vocabulary is whole chunks");
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
                          int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
 // ---- replayed decode steps (a captured graph of one step, replayed a round at a time) ----

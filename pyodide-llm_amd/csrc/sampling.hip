@@ -9,8 +9,9 @@
 //   the most probable (equal ones in index order: the reference's quicksort leaves their order open), their float64
 //   running sum up to the first >= topp * total;
 //   the first token whose running float64 sum passes random * mass, else the last one taken.
-// One block of 1024 threads: the order-free parts (the largest, the filters, the exponentials, the sort) in parallel,
-// the float64 running sums by one thread from LDS in the reference's order.
+// One block of 1024 threads: the order-free parts (the largest, the filters, the exponentials, the sort) in parallel;
+// the float64 total in the reference's order by one wave from registers (sum_wave), the draw's running sums by one
+// thread from the total's checkpoints.
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -24,6 +25,7 @@ namespace {
 
 constexpr int ST = 1024;         // threads of the sampling block
 constexpr int SORT_MOST = 8192;  // nucleus tokens one block sorts (more: the step is declined, SAMPLE_DECLINED)
+constexpr int VU = 8;            // loads of the vocabulary a thread has in flight in the block's passes over it
 constexpr int STAGE = 16384;     // floats of the LDS area the sort and the running sums' staging share
 
 // kernels/kernel.ts:705-719: each distinct token of tokens[0..count) once, value > 0 ? value / penalty : value * penalty
@@ -62,33 +64,72 @@ __device__ __forceinline__ int block_scan(int c, int *wave_sums, int *total) {
   return wave_sums[wave] + x - c;
 }
 
-// The float64 running sums of the draw are sequential (the reference's order: one add after another in index order),
-// so one thread runs them; these keep its adds from waiting on LDS: 32 values requested at a time as float4.
+// The float64 running sums of the draw are sequential (the reference's order: one add after another in index order).
+// The total runs from registers: a dependent float64 add takes about 6 cycles from registers and about twice that
+// when its values come from LDS reads, whose issue then sets the pace.
 constexpr int CP_BLOCK = 256;                     // values between two checkpoints of the running sum
 constexpr int CP_MOST = SAMPLE_MOST / CP_BLOCK;   // checkpoints of the largest vocabulary
-constexpr int WIDE = STAGE / 2;                   // float64 values staged in LDS at a time for the total
-static_assert(WIDE % CP_BLOCK == 0, "a staged chunk holds whole checkpoint blocks");
+constexpr int SEG = 32;                           // values a lane adds in its turn
+constexpr int CHUNK = 64 * SEG;                   // values a wave holds at a time
+static_assert(CHUNK == SAMPLE_CHUNK, "the probabilities' buffers hold whole chunks");
+static_assert(CP_BLOCK % SEG == 0, "a checkpoint falls on a lane's first value");
 
-// acc + v[0] + v[1] + ... + v[len-1] in float64, in order; with cp, cp[cp0 + i / CP_BLOCK] = the sum before value i
-// for every i that is a multiple of CP_BLOCK (v: the values already widened to float64 by the whole block, 16-byte
-// aligned, so that the one thread's instructions are the adds alone)
-__device__ __forceinline__ double sum_f64(const double *v, int len, double acc, double *cp, int cp0) {
-  const double2 *v2 = reinterpret_cast<const double2 *>(v);
-  int i = 0;
-  for (; i + 32 <= len; i += 32) {
-    if (cp && i % CP_BLOCK == 0) cp[cp0 + i / CP_BLOCK] = acc;
-    double2 a[16];
+// the 64-bit value of lane - 1 (lane 0: any), by DPP: a row shift by one, or (EDGE, for a row's first lane) lane 15
+// of the row before
+template <bool EDGE>
+__device__ __forceinline__ double from_lane_below(double x) {
+  constexpr int ctrl = EDGE ? 0x142 : 0x111;  // row_bcast:15, row_shr:1
+  const int lo = __double2loint(x), hi = __double2hiint(x);
+  return __hiloint2double(__builtin_amdgcn_update_dpp(hi, hi, ctrl, 0xF, 0xF, false),
+                          __builtin_amdgcn_update_dpp(lo, lo, ctrl, 0xF, 0xF, false));
+}
+
+// p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), in order, by one wave: lane L holds
+// p[b + 32 L .. b + 32 L + 31] of a chunk of 2048 in registers (+0.0 past count, which changes no sum), and in turn s
+// lane s adds its 32 to the running sum lane s - 1 handed it, so that an add waits on the add before it only; the
+// next chunk's reads fly meanwhile. With cp, cp[i / CP_BLOCK] = the sum before value i for every multiple i of
+// CP_BLOCK below count. Every lane returns the total. (p: 16-byte aligned, count >= 1, room for whole chunks:
+// sample_probs_floats(count) floats.)
+__device__ double sum_wave(const float *p, int count, double *cp) {
+  const int lane = threadIdx.x & 63;
+  float4 nx[SEG / 4];
+  auto fetch = [&](int b) {  // (past count: what the buffer holds there, masked to +0.0 below)
+    const int i0 = b + lane * SEG;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) a[u] = v2[i / 2 + u];
+    for (int u = 0; u < SEG / 4; ++u) nx[u] = reinterpret_cast<const float4 *>(p + i0)[u];
+  };
+  double run = 0.0;  // the sum before the chunk
+  fetch(0);
+  for (int b = 0; b < count; b += CHUNK) {
+    double v[SEG];
+    const int left = count - b - lane * SEG;  // this lane's values below count
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      acc += a[u].x;
-      acc += a[u].y;
+    for (int u = 0; u < SEG / 4; ++u) {
+      v[4 * u] = 4 * u < left ? (double)nx[u].x : 0.0;
+      v[4 * u + 1] = 4 * u + 1 < left ? (double)nx[u].y : 0.0;
+      v[4 * u + 2] = 4 * u + 2 < left ? (double)nx[u].z : 0.0;
+      v[4 * u + 3] = 4 * u + 3 < left ? (double)nx[u].w : 0.0;
     }
+    if (b + CHUNK < count) fetch(b + CHUNK);
+    // acc: lane 0's start now, each other lane's from its turn on (the sum before its values); the turns unrolled
+    // by rows of 16, so that each hand-on's DPP form is fixed
+    double acc = run;
+    double sum = run;
+    for (int s0 = 0; s0 < 64; s0 += 16) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        sum = acc;
+#pragma unroll
+        for (int u = 0; u < SEG; ++u) sum = sum + v[u];
+        const double moved = k == 15 ? from_lane_below<true>(sum) : from_lane_below<false>(sum);
+        acc = lane == s0 + k + 1 ? moved : acc;
+      }
+    }
+    if (cp && lane % (CP_BLOCK / SEG) == 0 && b + SEG * lane < count) cp[(b + SEG * lane) / CP_BLOCK] = acc;
+    run = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(sum), 63),
+                           __builtin_amdgcn_readlane(__double2loint(sum), 63));
   }
-  if (cp && i < len && i % CP_BLOCK == 0) cp[cp0 + i / CP_BLOCK] = acc;
-  for (; i < len; ++i) acc += v[i];
-  return acc;
+  return run;
 }
 
 // the first j < len whose running sum acc + v[0] + ... + v[j] (float64, in order) passes target (REACH: reaches it), or
@@ -146,7 +187,13 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
 
   // the largest logit (order-free: wmax keeps a NaN and puts +0 above -0)
   float b = logits[0];
-  for (int i = tid; i < n; i += ST) b = wmax(b, logits[i]);
+  for (int i0 = tid; i0 < n; i0 += ST * VU) {  // VU loads in flight a thread (clamped: a repeat changes no max)
+    float v[VU];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) v[u] = logits[min(i0 + ST * u, n - 1)];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) b = wmax(b, v[u]);
+  }
   for (int o = 32; o >= 1; o >>= 1) b = wmax(b, __shfl_xor(b, o, 64));
   if (lane == 0) wf[wave] = b;
   __syncthreads();
@@ -173,24 +220,36 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
   const int wrun = ((n + ST / 64 - 1) / (ST / 64) + 63) & ~63, wlo = min(n, wave * wrun), whi = min(n, wlo + wrun);
   const uint64_t below = (1ull << lane) - 1;
   int c = 0;
-  for (int i = wlo + lane; i < whi; i += 64) c += logits[i] >= floor_;
+  for (int i0 = wlo + lane; i0 < whi; i0 += 64 * VU) {
+    float v[VU];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) v[u] = logits[min(i0 + 64 * u, n - 1)];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) c += i0 + 64 * u < whi && v[u] >= floor_;
+  }
   for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
   int k = block_scan(lane == 0 ? c : 0, wi, &shared_count);
   k = __shfl(k, 0, 64);
   const int count = shared_count, simd = count & ~3;
   const float inverse = 1.0f / temperature;
-  for (int i0 = wlo; i0 < whi; i0 += 64) {
-    const int i = i0 + lane;
-    const float v = i < whi ? logits[i] : 0.0f;
-    const bool keep = i < whi && v >= floor_;
-    const uint64_t mask = __ballot(keep);
-    if (keep) {
-      const int at = k + __popcll(mask & below);
-      const float d = v - best;
-      probs[at] = at < simd ? vexp(d * inverse) : fexp(d / temperature);
-      index[at] = i;
+  for (int j0 = wlo; j0 < whi; j0 += 64 * VU) {
+    float vs[VU];  // every load of the pass requested before its stores (clamped, unconditional)
+#pragma unroll
+    for (int u = 0; u < VU; ++u) vs[u] = logits[min(j0 + 64 * u + lane, n - 1)];
+#pragma unroll
+    for (int u = 0; u < VU; ++u) {
+      const int i = j0 + 64 * u + lane;
+      const float v = vs[u];
+      const bool keep = i < whi && v >= floor_;
+      const uint64_t mask = __ballot(keep);
+      if (keep) {
+        const int at = k + __popcll(mask & below);
+        const float d = v - best;
+        probs[at] = at < simd ? vexp(d * inverse) : fexp(d / temperature);
+        index[at] = i;
+      }
+      k += __popcll(mask);
     }
-    k += __popcll(mask);
   }
   __syncthreads();
 
@@ -199,15 +258,10 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
   for (int j = tid; j < count; j += ST) t = __builtin_fmaxf(t, probs[j]);
   for (int o = 32; o >= 1; o >>= 1) t = __builtin_fmaxf(t, __shfl_xor(t, o, 64));
   if (lane == 0) wf[wave] = t;
+  // total: float64, in order, by wave 0 from registers
   double total = 0.0;
-  double *const wide = reinterpret_cast<double *>(area);  // a chunk of the p widened to float64 (exactly)
-  for (int base = 0; base < count; base += WIDE) {
-    const int len = min(WIDE, count - base);
-    __syncthreads();
-    for (int j = tid; j < len; j += ST) wide[j] = (double)probs[base + j];
-    __syncthreads();
-    if (tid == 0) total = sum_f64(wide, len, total, checkpoints, base / CP_BLOCK);
-  }
+  if (wave == 0) total = sum_wave(probs, count, checkpoints);
+  __syncthreads();  // (the waves' maxima in wf too)
   if (tid == 0) {
     float x = wf[0];
     for (int w = 1; w < ST / 64; ++w) x = __builtin_fmaxf(x, wf[w]);
@@ -224,8 +278,14 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
     if (tid == 0) {
       const double target = random * total;
       const int blocks = (count + CP_BLOCK - 1) / CP_BLOCK;
-      int b = 0;
-      while (b < blocks && (b + 1 < blocks ? checkpoints[b + 1] : total) <= target) ++b;
+      // the first block b whose end (the sum before block b + 1, or the total) passes target, blocks if none: the ends
+      // never decrease, so by halving
+      int b = 0, hi = blocks;
+      while (b < hi) {
+        const int mid = (b + hi) / 2;
+        if ((mid + 1 < blocks ? checkpoints[mid + 1] : total) <= target) b = mid + 1;
+        else hi = mid;
+      }
       int token = -1;
       if (b < blocks) {
         double reached = 0.0;
