@@ -1409,6 +1409,32 @@ int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t coun
   return HE_OK;
 }
 
+int32_t hk_ordered_sum(const void *p, int32_t n, double *total, double *checkpoints, void *stream) {
+  if (!p || !total || n < 1 || n > SAMPLE_MOST) return fail(HE_E_ARG, "hk_ordered_sum: bad arguments");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int32_t ncp = (n + SAMPLE_CHECKPOINT - 1) / SAMPLE_CHECKPOINT;
+  float *padded = nullptr;
+  double *out = nullptr;
+  int32_t rc = dev_alloc(&padded, sizeof(float) * sample_probs_floats(n));  // whole chunks, as the draw's buffers
+  if (!rc) rc = dev_alloc(&out, sizeof(double) * (1 + (size_t)ncp));
+  hipError_t err = hipSuccess;
+  if (!rc) {
+    err = hipMemcpyAsync(padded, p, sizeof(float) * (size_t)n, hipMemcpyDeviceToDevice, s);
+    if (err == hipSuccess)  // +0.0 to the chunk's end, as the draw leaves its buffer
+      err = hipMemsetAsync(padded + n, 0, sizeof(float) * (sample_probs_floats(n) - (size_t)n), s);
+    if (err == hipSuccess) err = launch_ordered_sum(padded, n, out, out + 1, s);
+    if (err == hipSuccess) err = hipMemcpyAsync(total, out, sizeof(double), hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess && checkpoints)
+      err = hipMemcpyAsync(checkpoints, out + 1, sizeof(double) * (size_t)ncp, hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+  }
+  if (padded) (void)hipFree(padded);
+  if (out) (void)hipFree(out);
+  if (rc) return rc;
+  if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_ordered_sum: ") + hipGetErrorString(err));
+  return HE_OK;
+}
+
 int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, double random, int32_t *token,
                   void *stream) {
   if (!logits || !token || n < 1 || !(temperature > 0.0f)) return fail(HE_E_ARG, "hk_sample: bad arguments");

@@ -208,6 +208,10 @@ constexpr size_t sample_probs_floats(int32_t n) { return ((size_t)n + SAMPLE_CHU
 static_assert(SAMPLE_MOST % SAMPLE_CHUNK == 0, "the largest vocabulary is whole chunks");
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
                          int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
+// the draw's float64 total of p[0..n) in index order (kernels/kernel.ts:845-850), and the running sum before every
+// SAMPLE_CHECKPOINT values (checkpoints: ceil(n / SAMPLE_CHECKPOINT) doubles); p: sample_probs_floats(n) floats
+constexpr int32_t SAMPLE_CHECKPOINT = 256;
+hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *checkpoints, hipStream_t s);
 // ---- replayed decode steps (a captured graph of one step, replayed a round at a time) ----
 // the step's state in device memory: the position, the step of the round, the halting step + 1 (0: none yet), the
 // penalty window's count and its oldest entry once full

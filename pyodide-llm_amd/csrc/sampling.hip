@@ -10,8 +10,8 @@
 //   running sum up to the first >= topp * total;
 //   the first token whose running float64 sum passes random * mass, else the last one taken.
 // One block of 1024 threads: the order-free parts (the largest, the filters, the exponentials, the sort) in parallel;
-// the float64 total in the reference's order by one wave from registers (sum_wave), the draw's running sums by one
-// thread from the total's checkpoints.
+// the float64 total with the bits of the reference's order, taken in parallel (sum_block), the draw's running sums by
+// one thread from the total's checkpoints.
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -64,70 +64,299 @@ __device__ __forceinline__ int block_scan(int c, int *wave_sums, int *total) {
   return wave_sums[wave] + x - c;
 }
 
-// The float64 running sums of the draw are sequential (the reference's order: one add after another in index order).
-// The total runs from registers: a dependent float64 add takes about 6 cycles from registers and about twice that
-// when its values come from LDS reads, whose issue then sets the pace.
-constexpr int CP_BLOCK = 256;                     // values between two checkpoints of the running sum
+// The float64 running sums of the draw are sequential in the reference's order (one add after another in index order):
+// the total takes their bits in parallel (sum_block), the draw's search runs them from a checkpoint.
+constexpr int CP_BLOCK = SAMPLE_CHECKPOINT;       // values between two checkpoints of the running sum
 constexpr int CP_MOST = SAMPLE_MOST / CP_BLOCK;   // checkpoints of the largest vocabulary
-constexpr int SEG = 32;                           // values a lane adds in its turn
+constexpr int SEG = 32;                           // values a lane holds of a chunk
 constexpr int CHUNK = 64 * SEG;                   // values a wave holds at a time
 static_assert(CHUNK == SAMPLE_CHUNK, "the probabilities' buffers hold whole chunks");
 static_assert(CP_BLOCK % SEG == 0, "a checkpoint falls on a lane's first value");
 
-// the 64-bit value of lane - 1 (lane 0: any), by DPP: a row shift by one, or (EDGE, for a row's first lane) lane 15
-// of the row before
-template <bool EDGE>
-__device__ __forceinline__ double from_lane_below(double x) {
-  constexpr int ctrl = EDGE ? 0x142 : 0x111;  // row_bcast:15, row_shr:1
-  const int lo = __double2loint(x), hi = __double2hiint(x);
-  return __hiloint2double(__builtin_amdgcn_update_dpp(hi, hi, ctrl, 0xF, 0xF, false),
-                          __builtin_amdgcn_update_dpp(lo, lo, ctrl, 0xF, 0xF, false));
+// A chunk's float64 sum in parallel, with the bits of the sequential adds, while the running sum stays in one binade.
+// With run in [2^e, 2^(e+1)) every sum that stays below 2^(e+1) is a multiple of u = 2^(e-52), and fl(s + x) = s + r u
+// where r is x / u rounded to the nearest integer: that does not depend on s, except on an exact tie (x / u = q + 1/2),
+// which rounds to the even multiple, so that r = q + ((s / u + q) odd) and the sum after it is even. So each lane
+// takes its 32 r as a function of the parity of s / u before them (none of them a tie: a fixed sum and a flip of the
+// parity; else a sum plus 0 or 1 by the incoming parity at the first tie, and a fixed parity after), the lanes'
+// incoming parities follow from lane masks (the last lane with a tie and the flips since), and the r are exact
+// integers in float64 below 2^53. Lanes below from take no part (their values are done). Returns the first lane
+// (from..63) whose values take the sum to 2^(e+1) or past it, 64 if none; *start is the sum before this lane's values
+// (right for the lanes from..the returned one), *end the chunk's end where 64 is returned.
+// a lane's 32 values as r at grid 2^(e-52) (see above): the sum of r with the first tie's 1 left out, whether a tie was
+// seen, the parity flips after the last tie (or of all of them where none was), and the first tie's c
+struct LaneR {
+  double s0;
+  int seen, x, cfirst;
+};
+
+__device__ __forceinline__ LaneR lane_r(const float (&v)[SEG], int e) {
+  // per value (all exact): y = x / u, q = floor(y); g = 2 (y - q) in [0, 2), ge = floor(g) (y - q >= 1/2), whole =
+  // g has no fraction; tie = ge and whole, up = ge and not whole; odd = q's last bit. The flags are made 0 / 1 by
+  // arithmetic and kept as integers, and the q summed on their own, so that nothing waits on the ties' order.
+  // The lane's state in one integer: bit 0 the flips since the last tie, bit 1 a tie seen, bit 2 the first tie's c,
+  // from bit 3 up the 1s added.
+  int st = 0;
+  double sq = 0.0;  // the lane's sum of q
+#pragma unroll
+  for (int u = 0; u < SEG; ++u) {
+    float vu = v[u];
+    asm volatile("" : "+v"(vu));  // (each value's work starts here: none of it is hoisted above the last's)
+    const double y = __builtin_ldexp((double)vu, 52 - e);  // x / u, exact
+    const double q = __builtin_floor(y);
+    const double g = (y - q) * 2.0, gi = __builtin_floor(g);
+    const double h = q * 0.5;
+    const int odd = (int)((h - __builtin_floor(h)) * 2.0);
+    const int ge = (int)gi, frac = (int)__builtin_ceil(g - gi);
+    const int tie = ge & (frac ^ 1), up = ge & frac;
+    sq = sq + q;
+    const int x = st & 1, seen = (st >> 1) & 1;
+    const int a = x ^ odd;  // a tie's extra 1 given the parity since the last tie
+    const int add = (tie & seen & a) | ((tie ^ 1) & up);
+    const int nx = (tie ^ 1) & (x ^ odd ^ up);
+    st = ((st & ~3) | nx | ((seen | tie) << 1) | ((tie & (seen ^ 1) & a) << 2)) + (add << 3);
+    // the lane's state made here, value by value (an empty asm that takes and gives it): left to itself the compiler
+    // holds every value's q and flags to the end and spills
+    asm volatile("" : "+v"(sq), "+v"(st));
+  }
+  return {sq + (double)(st >> 3), (st >> 1) & 1, st & 1, (st >> 2) & 1};
 }
 
-// p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), in order, by one wave: lane L holds
-// p[b + 32 L .. b + 32 L + 31] of a chunk of 2048 in registers (+0.0 past count, which changes no sum), and in turn s
-// lane s adds its 32 to the running sum lane s - 1 handed it, so that an add waits on the add before it only; the
-// next chunk's reads fly meanwhile. With cp, cp[i / CP_BLOCK] = the sum before value i for every multiple i of
-// CP_BLOCK below count. Every lane returns the total. (p: 16-byte aligned, count >= 1, room for whole chunks:
-// sample_probs_floats(count) floats.)
-__device__ double sum_wave(const float *p, int count, double *cp) {
+// the lane's sum of r where lane from's incoming parity is pin0 (lanes below from: 0): the lanes' incoming parities
+// from lane masks, the last lane below with a tie and the flips since
+__device__ __forceinline__ double lane_t(const LaneR &r, int from, int pin0) {
   const int lane = threadIdx.x & 63;
-  float4 nx[SEG / 4];
-  auto fetch = [&](int b) {  // (past count: what the buffer holds there, masked to +0.0 below)
-    const int i0 = b + lane * SEG;
+  const bool mine = lane >= from;
+  const uint64_t below = (1ull << lane) - 1;
+  const uint64_t mt = __ballot(mine && r.seen), mk = __ballot(mine && r.seen && r.x),
+                 mx = __ballot(mine && !r.seen && r.x);
+  int pin;
+  if (mt & below) {
+    const int last = 63 - __builtin_clzll(mt & below);
+    const uint64_t since = below & ~((2ull << last) - 1);
+    pin = (int)((mk >> last) & 1) ^ (__builtin_popcountll(mx & since) & 1);
+  } else {
+    pin = pin0 ^ (__builtin_popcountll(mx & below) & 1);
+  }
+  return mine ? r.s0 + (r.seen ? (double)(pin ^ r.cfirst) : 0.0) : 0.0;
+}
+
+// the sum of t over the lanes up to this one (exact: integers below 2^53 up to the first lane that leaves the binade)
+__device__ __forceinline__ double lanes_upto(double t) {
+  const int lane = threadIdx.x & 63;
+  double inc = t;
 #pragma unroll
-    for (int u = 0; u < SEG / 4; ++u) nx[u] = reinterpret_cast<const float4 *>(p + i0)[u];
-  };
-  double run = 0.0;  // the sum before the chunk
-  fetch(0);
-  for (int b = 0; b < count; b += CHUNK) {
-    double v[SEG];
-    const int left = count - b - lane * SEG;  // this lane's values below count
+  for (int o = 1; o < 64; o <<= 1) {
+    const double y = __shfl_up(inc, o, 64);
+    inc = lane >= o ? inc + y : inc;
+  }
+  return inc;
+}
+
+__device__ __forceinline__ int binade(double s) { return ((__double2hiint(s) >> 20) & 0x7ff) - 1023; }  // s > 0, normal
+
+// Lanes from..63 of a chunk in parallel at run's binade e (lanes below from take no part: their values are done).
+// Returns the first lane whose values take the sum to 2^(e+1) or past it, 64 if none; *start is the sum before this
+// lane's values (right for the lanes from..the returned one), *end the chunk's end where 64 is returned.
+__device__ __forceinline__ int chunk_lanes(const float (&v)[SEG], double run, int from, double *start, double *end) {
+  const int lane = threadIdx.x & 63;
+  const int e = binade(run);
+  const double t = lane_t(lane_r(v, e), from, __double2loint(run) & 1);  // lane from: the parity of run / u
+  const double inc = lanes_upto(t);
+  const double base = __builtin_ldexp(run, 52 - e);  // run / u
+  const uint64_t over = __ballot(!(base + inc < 9007199254740992.0));  // lanes whose sum reaches 2^(e+1)
+  const double excl = __shfl_up(inc, 1, 64);  // the lanes below (inc - t would not be exact in a lane past 2^53)
+  *start = run + __builtin_ldexp(lane > 0 ? excl : 0.0, e - 52);
+  if (over) return __builtin_ctzll(over);
+  *end = run + __builtin_ldexp(__shfl(inc, 63, 64), e - 52);
+  return 64;
+}
+
+// One chunk (values b.., lane L's 32 at b + 32 L) exactly from run, by one wave: the lanes in parallel while the sum
+// stays in one binade; a lane that takes it out of its binade, and the first lane while the sum is 0, adds its values
+// one after another; then the lanes after it in parallel again. After two such lanes (a sum that still crosses
+// binades often: a parallel pass costs about as much as twenty lanes' adds in turn) the rest of the chunk goes lane
+// by lane, each adding its values to the sum the lane below hands it. Returns the chunk's end (every lane); with cp,
+// the checkpoints of the chunk's values.
+__device__ __forceinline__ double chunk_exact(const float (&v)[SEG], double run, int b, int count, double *cp) {
+  const int lane = threadIdx.x & 63;
+  double pre = 0.0;  // this lane's sum before its values
+  int from = 0;
+  for (int crossed = 0; from < 64 && crossed < 2; ++crossed) {
+    int cross = from;
+    double start = run, end = 0.0;
+    if (run > 0.0) cross = chunk_lanes(v, run, from, &start, &end);
+    if (lane >= from && lane <= cross) pre = start;
+    if (cross == 64) {
+      run = __hiloint2double(__builtin_amdgcn_readfirstlane(__double2hiint(end)),
+                             __builtin_amdgcn_readfirstlane(__double2loint(end)));  // (the same in every lane)
+      from = 64;
+      break;
+    }
+    // lane cross's values in order from its start (every lane adds its own; lane cross's sum is kept)
+    double acc = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(start), cross),
+                                  __builtin_amdgcn_readlane(__double2loint(start), cross));
+#pragma unroll
+    for (int u = 0; u < SEG; ++u) {
+      float t = v[u];
+      asm volatile("" : "+v"(t));  // (widened here, one at a time: all 32 held widened would not fit)
+      acc = acc + (double)t;
+    }
+    run = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(acc), cross),
+                           __builtin_amdgcn_readlane(__double2loint(acc), cross));
+    from = cross + 1;
+  }
+  // lane by lane: in turn s lane s adds its values to the sum in acc (every lane adds its own; lane s + 1 takes lane
+  // s's sum, by a readlane: the turns are few enough here that the hand-on's latency does not matter)
+  for (int s = from; s < 64; ++s) {
+    if (lane == s) pre = run;
+    double acc = run;
+#pragma unroll
+    for (int u = 0; u < SEG; ++u) {
+      float t = v[u];
+      asm volatile("" : "+v"(t));
+      acc = acc + (double)t;
+    }
+    run = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(acc), s),
+                           __builtin_amdgcn_readlane(__double2loint(acc), s));
+  }
+  if (cp && lane % (CP_BLOCK / SEG) == 0 && b + SEG * lane < count) cp[(b + SEG * lane) / CP_BLOCK] = pre;
+  return run;
+}
+
+// what the block's waves leave for the in-order pass: each chunk's guessed binade (NO_GUESS: none) and, at it, the
+// chunk's sum of r and its lanes' (0, 8, .., 56) sums of r before them, for either parity of the sum before the chunk
+constexpr int MOST_CHUNKS = SAMPLE_MOST / CHUNK;
+constexpr int NO_GUESS = -100000;
+struct ChunkGuess {
+  double t[2];
+  double pre[2][CHUNK / CP_BLOCK];
+};
+struct SumShared {
+  double approx[MOST_CHUNKS];  // each chunk's sum in any order
+  int guess[MOST_CHUNKS];
+  ChunkGuess g[MOST_CHUNKS];
+};
+
+// p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), with the bits of the adds in index order, by the
+// block (all of it calls): chunks of 2048, lane L of a wave holding p[b + 32 L .. b + 32 L + 31] (+0.0 past count,
+// which changes no sum). (1) Every chunk's sum in any order, and from them the binade the running sum probably has
+// at each chunk's start. (2) Each wave takes every waves-th chunk at its guessed binade (lane_r, then lane_t and the
+// lanes' sums for both parities of the sum before it). (3) Wave 0 goes through the chunks in order: where the sum
+// before a chunk has the guessed binade and the chunk's sum of r keeps it below the next power of two, the chunk's end
+// and checkpoints follow from (2) exactly; any other chunk is taken by chunk_exact. With cp, cp[i / CP_BLOCK] = the
+// sum before value i for every multiple i of CP_BLOCK below count. Wave 0 returns the total. (p: 16-byte aligned,
+// count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
+__device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+  const int chunks = (count + CHUNK - 1) / CHUNK;
+  auto load = [&](int c, float(&v)[SEG]) {
 #pragma unroll
     for (int u = 0; u < SEG / 4; ++u) {
-      v[4 * u] = 4 * u < left ? (double)nx[u].x : 0.0;
-      v[4 * u + 1] = 4 * u + 1 < left ? (double)nx[u].y : 0.0;
-      v[4 * u + 2] = 4 * u + 2 < left ? (double)nx[u].z : 0.0;
-      v[4 * u + 3] = 4 * u + 3 < left ? (double)nx[u].w : 0.0;
+      const float4 r = reinterpret_cast<const float4 *>(p + c * CHUNK + lane * SEG)[u];
+      v[4 * u] = r.x;
+      v[4 * u + 1] = r.y;
+      v[4 * u + 2] = r.z;
+      v[4 * u + 3] = r.w;
     }
-    if (b + CHUNK < count) fetch(b + CHUNK);
-    // acc: lane 0's start now, each other lane's from its turn on (the sum before its values); the turns unrolled
-    // by rows of 16, so that each hand-on's DPP form is fixed
-    double acc = run;
-    double sum = run;
-    for (int s0 = 0; s0 < 64; s0 += 16) {
+  };
+  for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
+    const int d = min(c + waves, chunks - 1);  // (past the last chunk: the last again, its sum written twice)
+    float v[SEG], w[SEG];
+    load(c, v);
+    load(d, w);
+    float a = 0.0f, z = 0.0f;  // (float32: these sums only guess the binades)
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        sum = acc;
+    for (int u = 0; u < SEG; ++u) {
+      a += v[u];
+      z += w[u];
+    }
+    double s = a, t = z;
+    for (int o = 32; o >= 1; o >>= 1) {
+      s += __shfl_xor(s, o, 64);
+      t += __shfl_xor(t, o, 64);
+    }
+    if (lane == 0) {
+      sh.approx[c] = s;
+      sh.approx[d] = t;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // the approximate sums before chunks 2L and 2L + 1
+    const int c0 = 2 * lane, c1 = c0 + 1;
+    const double a0 = c0 < chunks ? sh.approx[c0] : 0.0, a1 = c1 < chunks ? sh.approx[c1] : 0.0;
+    const double before = lanes_upto(a0 + a1) - (a0 + a1), mid = before + a0;
+    if (c0 < chunks) sh.guess[c0] = before > 0.0 ? binade(before) : NO_GUESS;
+    if (c1 < chunks) sh.guess[c1] = mid > 0.0 ? binade(mid) : NO_GUESS;
+  }
+  __syncthreads();
+  for (int c = wave; c < chunks; c += waves) {
+    const int e = sh.guess[c];
+    if (e == NO_GUESS) continue;  // (uniform)
+    float v[SEG];
+    load(c, v);
+    const LaneR r = lane_r(v, e);
 #pragma unroll
-        for (int u = 0; u < SEG; ++u) sum = sum + v[u];
-        const double moved = k == 15 ? from_lane_below<true>(sum) : from_lane_below<false>(sum);
-        acc = lane == s0 + k + 1 ? moved : acc;
+    for (int P = 0; P < 2; ++P) {
+      const double inc = lanes_upto(lane_t(r, 0, P));
+      const double excl = __shfl_up(inc, 1, 64);
+      if (lane % (CP_BLOCK / SEG) == 0) sh.g[c].pre[P][lane / (CP_BLOCK / SEG)] = lane > 0 ? excl : 0.0;
+      if (lane == 63) sh.g[c].t[P] = inc;
+    }
+  }
+  __syncthreads();
+  // in order (wave 0), the chunks' guesses in lanes (lane L: chunks L and L + 64), read by readlane; the checkpoints
+  // of the chunks taken from their guesses are written afterwards, all at once
+  double run = 0.0;
+  if (wave == 0) {
+    static_assert(MOST_CHUNKS <= 128, "two chunks a lane");
+    // (two of each, named, not arrays: an index that is not a constant would put an array in scratch memory)
+    const int c0 = lane, c1 = lane + 64;
+    const int eg0 = c0 < chunks ? sh.guess[c0] : NO_GUESS, eg1 = c1 < chunks ? sh.guess[c1] : NO_GUESS;
+    const double t00 = c0 < chunks ? sh.g[c0].t[0] : 0.0, t01 = c0 < chunks ? sh.g[c0].t[1] : 0.0;
+    const double t10 = c1 < chunks ? sh.g[c1].t[0] : 0.0, t11 = c1 < chunks ? sh.g[c1].t[1] : 0.0;
+    double before0 = -1.0, before1 = -1.0;  // the sum before a chunk taken from its guess (-1: not so taken)
+    auto from_lane = [](double x, int l) {
+      return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(x), l),
+                              __builtin_amdgcn_readlane(__double2loint(x), l));
+    };
+    for (int c = 0; c < chunks; ++c) {
+      const int h = c >> 6, l = c & 63;
+      const int e = __builtin_amdgcn_readlane(h ? eg1 : eg0, l);
+      bool took = false;
+      if (run > 0.0 && e == binade(run)) {
+        const int P = __double2loint(run) & 1;  // the parity of run / u
+        const double T = from_lane(h ? (P ? t11 : t10) : (P ? t01 : t00), l);
+        if (__builtin_ldexp(run, 52 - e) + T < 9007199254740992.0) {
+          if (lane == l) {
+            if (h) before1 = run;
+            else before0 = run;
+          }
+          run = run + __builtin_ldexp(T, e - 52);
+          took = true;
+        }
+      }
+      if (!took) {
+        float v[SEG];
+        load(c, v);
+        run = chunk_exact(v, run, c * CHUNK, count, cp);
       }
     }
-    if (cp && lane % (CP_BLOCK / SEG) == 0 && b + SEG * lane < count) cp[(b + SEG * lane) / CP_BLOCK] = acc;
-    run = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(sum), 63),
-                           __builtin_amdgcn_readlane(__double2loint(sum), 63));
+    if (cp) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = h ? c1 : c0, e = h ? eg1 : eg0;
+        const double bf = h ? before1 : before0;
+        if (bf >= 0.0) {
+          const int P = __double2loint(bf) & 1;
+#pragma unroll
+          for (int k = 0; k < CHUNK / CP_BLOCK; ++k)
+            if (c * CHUNK + k * CP_BLOCK < count)
+              cp[c * (CHUNK / CP_BLOCK) + k] = bf + __builtin_ldexp(sh.g[c].pre[P][k], e - 52);
+        }
+      }
+    }
   }
   return run;
 }
@@ -230,8 +459,9 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
   for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
   int k = block_scan(lane == 0 ? c : 0, wi, &shared_count);
   k = __shfl(k, 0, 64);
-  const int count = shared_count, simd = count & ~3;
+  const int count = __builtin_amdgcn_readfirstlane(shared_count), simd = count & ~3;
   const float inverse = 1.0f / temperature;
+  float top = 0.0f;  // the largest p (order-free)
   for (int j0 = wlo; j0 < whi; j0 += 64 * VU) {
     float vs[VU];  // every load of the pass requested before its stores (clamped, unconditional)
 #pragma unroll
@@ -245,22 +475,24 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
       if (keep) {
         const int at = k + __popcll(mask & below);
         const float d = v - best;
-        probs[at] = at < simd ? vexp(d * inverse) : fexp(d / temperature);
+        const float pv = at < simd ? vexp(d * inverse) : fexp(d / temperature);
+        probs[at] = pv;
         index[at] = i;
+        top = __builtin_fmaxf(top, pv);
       }
       k += __popcll(mask);
     }
   }
+  for (int j = count + tid; j < (int)sample_probs_floats(count); j += ST) probs[j] = 0.0f;  // the total's whole chunks
   __syncthreads();
 
   // top (order-free) and total (float64, in order: one thread from LDS)
-  float t = 0.0f;
-  for (int j = tid; j < count; j += ST) t = __builtin_fmaxf(t, probs[j]);
-  for (int o = 32; o >= 1; o >>= 1) t = __builtin_fmaxf(t, __shfl_xor(t, o, 64));
-  if (lane == 0) wf[wave] = t;
+  for (int o = 32; o >= 1; o >>= 1) top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
+  if (lane == 0) wf[wave] = top;
   // total: float64, in order, by wave 0 from registers
   double total = 0.0;
-  if (wave == 0) total = sum_wave(probs, count, checkpoints);
+  static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
+  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area));
   __syncthreads();  // (the waves' maxima in wf too)
   if (tid == 0) {
     float x = wf[0];
@@ -377,6 +609,13 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
   }
 }
 
+// the draw's float64 total alone (the same block's work): *total, and checkpoints[i / CP_BLOCK] = the sum before value i
+__global__ __launch_bounds__(ST) void ordered_sum_kernel(const float *p, int32_t n, double *total, double *checkpoints) {
+  __shared__ SumShared sh;
+  const double t = sum_block(p, n, checkpoints, sh);
+  if (threadIdx.x == 0) *total = t;
+}
+
 __global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t n, float temperature, float topp,
                                                     double random, float *probs, int32_t *index, int32_t *out_token,
                                                     float *out_best) {
@@ -481,6 +720,12 @@ hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, 
   if (count < 1) return hipSuccess;
   if (count > 64) return hipErrorInvalidValue;
   hipLaunchKernelGGL(penalize_kernel, dim3(1), dim3(64), 0, s, logits, tokens, count, penalty);
+  return hipGetLastError();
+}
+
+hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *checkpoints, hipStream_t s) {
+  if (n < 1 || n > SAMPLE_MOST) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ordered_sum_kernel, dim3(1), dim3(ST), 0, s, p, n, total, checkpoints);
   return hipGetLastError();
 }
 

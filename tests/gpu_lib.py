@@ -109,6 +109,17 @@ def penalize(logits, tokens, penalty):
     return x.numpy()
 
 
+def ordered_sum(p):
+    """hk_ordered_sum: the float64 total of p in index order and the running sum before every 256 values"""
+    x = upload(np.ascontiguousarray(p, dtype=np.float32))
+    total = ctypes.c_double(0.0)
+    cps = np.zeros((x.shape[0] + 255) // 256, dtype=np.float64)
+    check(package().library().hk_ordered_sum(x.ptr, x.shape[0], ctypes.byref(total), ctypes.c_void_p(cps.ctypes.data),
+                                             None))
+    del x
+    return total.value, cps
+
+
 def sample(logits, temperature, topp, random):
     """hk_sample: the token drawn for one random number (-1 not finite, -2 a nucleus larger than the device sorts)"""
     x = upload(np.ascontiguousarray(logits, dtype=np.float32))

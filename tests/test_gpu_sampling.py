@@ -53,6 +53,47 @@ def test_sample_matches_the_oracle(n, scale, temperature, topp):
                 assert got == ol.sample(logits, temperature, topp, u), (trial, u)
 
 
+def in_order(p):
+    """the float64 running sums of p in index order, each add rounded (NumPy's cumsum adds one after another)"""
+    return np.cumsum(np.asarray(p, np.float32).astype(np.float64))
+
+
+def probabilities(kind, n, rng):
+    """float32 values of the draw's kind (in [0, 1]) with many rounding cases of the float64 sum: exact ties (powers of
+    two, short mantissas), values far below the running sum's last bit, a tiny first value, leading zeros"""
+    u = rng.random(n)
+    if kind == "spread":
+        x = np.exp(-u * 10)
+    elif kind == "tails":
+        x = np.exp(-u * 80)
+    elif kind == "powers":
+        x = np.where(rng.random(n) < 0.25, 0.0, np.ldexp(1.0, -rng.integers(0, 40, n)))
+    elif kind == "short":
+        x = np.ldexp(rng.integers(0, 16, n).astype(np.float64), -rng.integers(0, 30, n))
+    elif kind == "tiny_first":
+        x = np.exp(-u * 5)
+        x[0] = 1e-40
+    elif kind == "leading_zeros":
+        x = np.where(np.arange(n) < min(5000, n // 2), 0.0, np.exp(-u * 3))
+    else:
+        x = np.ldexp(1.0 + rng.integers(0, 1 << 23, n) / float(1 << 23), -rng.integers(0, 60, n))
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["spread", "tails", "powers", "short", "tiny_first", "leading_zeros", "mantissas"])
+@pytest.mark.parametrize("n", [1, 31, 2049, 40961, 128256, 262144])
+def test_ordered_sum_bits(kind, n):
+    """the draw's float64 total (taken in parallel a binade at a time, kernels/kernel.ts:845-850 adds in order) and its
+    checkpoints equal the running sums of the adds in index order, to the bit"""
+    rng = np.random.default_rng(n * 7 + len(kind))
+    p = probabilities(kind, n, rng)
+    total, cps = gl.ordered_sum(p)
+    want = in_order(p)
+    assert np.float64(total).view(np.uint64) == want[-1].view(np.uint64)
+    before = np.concatenate([[0.0], want])[np.arange(0, n, 256)]
+    assert np.array_equal(cps.view(np.uint64), before.view(np.uint64))
+
+
 @pytest.mark.parametrize("bad", [np.nan, np.inf])
 def test_logits_that_are_not_finite_give_minus_one(bad):
     logits = np.random.default_rng(1).standard_normal(5000).astype(np.float32)
