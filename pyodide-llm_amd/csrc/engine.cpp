@@ -175,6 +175,7 @@ struct he_engine {
   float *sample_probs = nullptr;
   int32_t *sample_index = nullptr, *window = nullptr, *sample_token = nullptr;
   float *sample_best = nullptr;
+  DrawParts *sample_parts = nullptr;
   int32_t *host_window = nullptr;
   // the other forms: the layer's input a parallel residual's FFN normalizes (GPT-NeoX); the outlier channels' float32
   // columns of the classifier [n][vocab] and the values taken out of the classifier's input
@@ -227,7 +228,7 @@ void destroy(he_engine *e) {
                   e->xq, e->xs, e->scores, e->tilemax, e->logits, e->tokens, e->amax_v, e->amax_i,
                   e->best_v, e->best_i, e->state, e->step_ids, e->step_values, e->sample_probs, e->sample_index,
                   e->window, e->sample_token, e->sample_best, e->before, e->columns, e->picked, e->sink,
-                  e->run_params, e->kept_logits};
+                  e->run_params, e->kept_logits, e->sample_parts};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   void *pinned[] = {e->host_ids, e->host_state, e->host_values, e->host_window, e->host_params};
@@ -384,6 +385,7 @@ int32_t allocate_state(he_engine *e, const float *rope_cos, const float *rope_si
   ALLOC(e->window, sizeof(int32_t) * REPETITION_WINDOW);
   ALLOC(e->sample_token, sizeof(int32_t) * 4);
   ALLOC(e->sample_best, sizeof(float) * 4);
+  ALLOC(e->sample_parts, sizeof(DrawParts));
   ALLOC(e->sink, sizeof(uint32_t) * 64);
   ALLOC(e->run_params, sizeof(RunParams));
   ALLOC(e->kept_logits, sizeof(float) * c.vocab_size);
@@ -948,7 +950,7 @@ void build_graph(he_engine *e, int kind) {
       const bool drawn = (kind & STEP_SAMPLED) != 0;
       if (le == hipSuccess)
         le = drawn ? launch_sample_steps(e->logits, n, e->run_params, e->state, e->sample_probs, e->sample_index,
-                                         e->sample_token, e->sample_best, e->stream)
+                                         e->sample_parts, e->sample_token, e->sample_best, e->stream)
                    : launch_argmax(e->best_i, e->best_v, e->logits, n, e->amax_v, e->amax_i, e->stream);
       if (le == hipSuccess)
         le = launch_step_end(e->logits, n, e->kept_logits, e->tokens, e->state, drawn ? e->sample_token : e->best_i,
@@ -1001,7 +1003,7 @@ int32_t sampled_steps(he_engine *e, int32_t token, int32_t pos, const int32_t *h
       HIP_TRY(hipMemcpyAsync(e->host_values, e->best_v, sizeof(float), hipMemcpyDeviceToHost, e->stream));
     } else {
       HIP_TRY(launch_sample(e->logits, e->c.vocab_size, temperature, topp, randoms[i], e->sample_probs,
-                            e->sample_index, e->sample_token, e->sample_best, e->stream));
+                            e->sample_index, e->sample_parts, e->sample_token, e->sample_best, e->stream));
       HIP_TRY(hipMemcpyAsync(e->host_ids, e->sample_token, sizeof(int32_t), hipMemcpyDeviceToHost, e->stream));
       HIP_TRY(hipMemcpyAsync(e->host_values, e->sample_best, sizeof(float), hipMemcpyDeviceToHost, e->stream));
     }
@@ -1441,18 +1443,20 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   float *probs = nullptr, *best = nullptr;
   int32_t *index = nullptr, *out = nullptr;
+  DrawParts *parts = nullptr;
   int32_t rc = dev_alloc(&probs, sizeof(float) * sample_probs_floats(n));
   if (!rc) rc = dev_alloc(&index, sizeof(int32_t) * n);
   if (!rc) rc = dev_alloc(&out, sizeof(int32_t) * 4);
   if (!rc) rc = dev_alloc(&best, sizeof(float) * 4);
+  if (!rc) rc = dev_alloc(&parts, sizeof(DrawParts));
   hipError_t err = hipSuccess;
   if (!rc) {
-    err = launch_sample(reinterpret_cast<const float *>(logits), n, temperature, topp, random, probs, index, out, best,
-                        s);
+    err = launch_sample(reinterpret_cast<const float *>(logits), n, temperature, topp, random, probs, index, parts, out,
+                        best, s);
     if (err == hipSuccess) err = hipMemcpyAsync(token, out, sizeof(int32_t), hipMemcpyDeviceToHost, s);
     if (err == hipSuccess) err = hipStreamSynchronize(s);
   }
-  void *ptrs[] = {probs, index, out, best};
+  void *ptrs[] = {probs, index, out, best, parts};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (rc) return rc;
@@ -1463,12 +1467,14 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
 }  // extern "C"
 
 // hk_sample_static's scratch: probabilities [HK_SAMPLE_STATIC_MOST] float32, token indices [HK_SAMPLE_STATIC_MOST]
-// int32, then the drawn token and the largest logit, 256 bytes apart (2 MiB and 512 bytes). Every GPU holds its own
+// int32, then the drawn token and the largest logit, 256 bytes apart, then the draw's parts (DrawParts: 2 KiB), in
+// all 2 MiB and 2.5 KiB. Every GPU holds its own
 // copy at its own address, found once a device with hipGetSymbolAddress: in host code the array's name is a stand-in,
 // not a device address, and is never passed to a kernel or a copy.
 namespace ple {
 constexpr size_t SAMPLE_INDEX_AT = 4 * (size_t)HK_SAMPLE_STATIC_MOST, SAMPLE_TOKEN_AT = 8 * (size_t)HK_SAMPLE_STATIC_MOST;
-constexpr size_t SAMPLE_BEST_AT = SAMPLE_TOKEN_AT + 256, SAMPLE_SCRATCH_BYTES = SAMPLE_BEST_AT + 256;
+constexpr size_t SAMPLE_BEST_AT = SAMPLE_TOKEN_AT + 256, SAMPLE_PARTS_AT = SAMPLE_BEST_AT + 256;
+constexpr size_t SAMPLE_SCRATCH_BYTES = SAMPLE_PARTS_AT + sizeof(DrawParts);
 __device__ __align__(256) uint8_t scratch[SAMPLE_SCRATCH_BYTES];
 static_assert(sample_probs_floats(HK_SAMPLE_STATIC_MOST) == (size_t)HK_SAMPLE_STATIC_MOST,
               "the probabilities' region holds the sampler's whole chunks");
@@ -1543,7 +1549,8 @@ int32_t hk_sample_static(const void *logits, int32_t n, float temperature, float
   if (rc) return rc;
   int32_t *out = reinterpret_cast<int32_t *>(base + SAMPLE_TOKEN_AT);
   HIP_TRY(launch_sample(reinterpret_cast<const float *>(logits), n, temperature, topp, random,
-                        reinterpret_cast<float *>(base), reinterpret_cast<int32_t *>(base + SAMPLE_INDEX_AT), out,
+                        reinterpret_cast<float *>(base), reinterpret_cast<int32_t *>(base + SAMPLE_INDEX_AT),
+                        reinterpret_cast<DrawParts *>(base + SAMPLE_PARTS_AT), out,
                         reinterpret_cast<float *>(base + SAMPLE_BEST_AT), s));
   HIP_TRY(hipMemcpyAsync(token, out, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));

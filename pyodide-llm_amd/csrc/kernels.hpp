@@ -206,8 +206,16 @@ constexpr int32_t SAMPLE_MOST = 262144;  // logits a draw takes at most
 constexpr int32_t SAMPLE_CHUNK = 2048;
 constexpr size_t sample_probs_floats(int32_t n) { return ((size_t)n + SAMPLE_CHUNK - 1) / SAMPLE_CHUNK * SAMPLE_CHUNK; }
 static_assert(SAMPLE_MOST % SAMPLE_CHUNK == 0, "the largest vocabulary is whole chunks");
+// what the draw's blocks over the vocabulary (SAMPLE_CHUNK logits each) leave for the draw: each block's largest
+// logit, its count of kept logits, its largest p and its sum of p
+struct DrawParts {
+  float bmax[SAMPLE_MOST / SAMPLE_CHUNK];
+  int32_t bcount[SAMPLE_MOST / SAMPLE_CHUNK];
+  float btop[SAMPLE_MOST / SAMPLE_CHUNK];
+  float csum[SAMPLE_MOST / SAMPLE_CHUNK];
+};
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
-                         int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
+                         int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best, hipStream_t s);
 // the draw's float64 total of p[0..n) in index order (kernels/kernel.ts:845-850), and the running sum before every
 // SAMPLE_CHECKPOINT values (checkpoints: ceil(n / SAMPLE_CHECKPOINT) doubles); p: sample_probs_floats(n) floats
 constexpr int32_t SAMPLE_CHECKPOINT = 256;
@@ -228,7 +236,8 @@ struct RunParams {
 };
 // a step's draw (as launch_sample) with the call's temperature and top-p and the round's random number of the step
 hipError_t launch_sample_steps(const float *logits, int32_t n, const RunParams *params, const int32_t *state,
-                               float *probs, int32_t *index, int32_t *out_token, float *out_best, hipStream_t s);
+                               float *probs, int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best,
+                               hipStream_t s);
 // the call's penalty over the window's state[STATE_WINDOW] tokens
 hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
                                  hipStream_t s);

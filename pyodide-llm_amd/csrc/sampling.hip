@@ -41,6 +41,7 @@ __global__ __launch_bounds__(64) void penalize_kernel(float *logits, const int32
 }
 
 // the exclusive prefix sum of every thread's c over the block (threads in order), and the total
+template <int NT = ST>
 __device__ __forceinline__ int block_scan(int c, int *wave_sums, int *total) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int x = c;
@@ -53,7 +54,7 @@ __device__ __forceinline__ int block_scan(int c, int *wave_sums, int *total) {
   __syncthreads();
   if (tid == 0) {
     int run = 0;
-    for (int w = 0; w < ST / 64; ++w) {
+    for (int w = 0; w < NT / 64; ++w) {
       const int s = wave_sums[w];
       wave_sums[w] = run;
       run += s;
@@ -241,13 +242,14 @@ struct SumShared {
 // p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), with the bits of the adds in index order, by the
 // block (all of it calls): chunks of 2048, lane L of a wave holding p[b + 32 L .. b + 32 L + 31] (+0.0 past count,
 // which changes no sum). (1) Every chunk's sum in any order, and from them the binade the running sum probably has
-// at each chunk's start. (2) Each wave takes every waves-th chunk at its guessed binade (lane_r, then lane_t and the
+// at each chunk's start (chunk_sums: those sums given). (2) Each wave takes every waves-th chunk at its guessed binade (lane_r, then lane_t and the
 // lanes' sums for both parities of the sum before it). (3) Wave 0 goes through the chunks in order: where the sum
 // before a chunk has the guessed binade and the chunk's sum of r keeps it below the next power of two, the chunk's end
 // and checkpoints follow from (2) exactly; any other chunk is taken by chunk_exact. With cp, cp[i / CP_BLOCK] = the
 // sum before value i for every multiple i of CP_BLOCK below count. Wave 0 returns the total. (p: 16-byte aligned,
 // count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
-__device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh) {
+__device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh,
+                                            const float *chunk_sums = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const int chunks = (count + CHUNK - 1) / CHUNK;
   auto load = [&](int c, float(&v)[SEG]) {
@@ -260,6 +262,9 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       v[4 * u + 3] = r.w;
     }
   };
+  if (chunk_sums) {
+    for (int c = threadIdx.x; c < chunks; c += blockDim.x) sh.approx[c] = chunk_sums[c];
+  } else {
   for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
     const int d = min(c + waves, chunks - 1);  // (past the last chunk: the last again, its sum written twice)
     float v[SEG], w[SEG];
@@ -280,6 +285,7 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       sh.approx[c] = s;
       sh.approx[d] = t;
     }
+  }
   }
   __syncthreads();
   if (wave == 0) {
@@ -399,40 +405,180 @@ __device__ __forceinline__ int first_past(const float *v, int len, double acc, d
 // (p, token) pairs: a before b where p is larger, or equal and the token smaller
 __device__ __forceinline__ bool before(float pa, int ia, float pb, int ib) { return pa > pb || (pa == pb && ia < ib); }
 
-__device__ __forceinline__ void sample_block(const float *logits, int32_t n, float temperature, float topp,
-                                             double random, float *probs, int32_t *index, int32_t *out_token,
-                                             float *out_best) {
-  __shared__ float4 area[SORT_MOST / 2];  // the sort's probabilities then tokens; the running sums' staging
-  float *const sp = reinterpret_cast<float *>(area);
-  int *const si = reinterpret_cast<int *>(area) + SORT_MOST;
-  __shared__ float wf[ST / 64];
-  __shared__ int wi[ST / 64];
-  __shared__ float shared_best, shared_top;
-  __shared__ int shared_count, shared_likely, shared_token;
-  __shared__ double shared_total, shared_cutoff;
-  __shared__ double checkpoints[CP_MOST];  // the running sum of the kept p before every CP_BLOCK of them
-  static_assert(STAGE <= 2 * SORT_MOST, "the staging area is the sort's");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// ---- the draw over the vocabulary in blocks of CHUNK values (many CUs), then one block for the ordered sums ----
+// A draw's settings: the call's arguments, or in a replayed step the call's settings and the round's random number of
+// the step from device memory.
+struct Settings {
+  float temperature, topp;
+  double random;
+};
+__device__ __forceinline__ Settings settings(float temperature, float topp, double random, const RunParams *params,
+                                             const int32_t *state) {
+  if (params) return {params->temperature, params->topp, params->randoms[state[STATE_STEP]]};
+  return {temperature, topp, random};
+}
 
-  // the largest logit (order-free: wmax keeps a NaN and puts +0 above -0)
-  float b = logits[0];
-  for (int i0 = tid; i0 < n; i0 += ST * VU) {  // VU loads in flight a thread (clamped: a repeat changes no max)
-    float v[VU];
+constexpr int VB = 256;            // threads of a vocabulary block: CHUNK / VB consecutive logits a thread
+constexpr int VPT = CHUNK / VB;
+constexpr int VBLOCKS_MOST = SAMPLE_MOST / CHUNK;
+
+// the largest logit (order-free: wmax keeps a NaN and puts +0 above -0) from the blocks' largest ones (all of them
+// read by every caller: at most VBLOCKS_MOST)
+__device__ __forceinline__ float best_of(const DrawParts *parts, int blocks, float *wf) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float b = parts->bmax[0];
+  for (int i = tid; i < blocks; i += blockDim.x) b = wmax(b, parts->bmax[i]);
+  for (int o = 32; o >= 1; o >>= 1) b = wmax(b, __shfl_xor(b, o, 64));
+  if (lane == 0) wf[wave] = b;
+  __syncthreads();
+  float x = wf[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) x = wmax(x, wf[w]);
+  __syncthreads();
+  return x;
+}
+
+// the floor of the kept logits (kernels/kernel.ts:815-817): with a nucleus, best - temperature * 16.118095
+__device__ __forceinline__ float floor_of(float best, const Settings &st) {
+  const bool nucleus = st.topp > 0 && st.topp < 1;
+  return nucleus ? best - st.temperature * 16.118095f : -3.4028234663852886e38f;
+}
+
+// (1) each block's largest logit
+__global__ __launch_bounds__(VB) void vocab_max_kernel(const float *logits, int32_t n, DrawParts *parts) {
+  __shared__ float wf[VB / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i0 = blockIdx.x * CHUNK + tid * VPT;
+  float v[VPT];
 #pragma unroll
-    for (int u = 0; u < VU; ++u) v[u] = logits[min(i0 + ST * u, n - 1)];
+  for (int u = 0; u < VPT; ++u) v[u] = logits[min(i0 + u, n - 1)];  // (clamped: a repeat changes no max)
+  float b = v[0];
 #pragma unroll
-    for (int u = 0; u < VU; ++u) b = wmax(b, v[u]);
-  }
+  for (int u = 1; u < VPT; ++u) b = wmax(b, v[u]);
   for (int o = 32; o >= 1; o >>= 1) b = wmax(b, __shfl_xor(b, o, 64));
   if (lane == 0) wf[wave] = b;
   __syncthreads();
   if (tid == 0) {
     float x = wf[0];
-    for (int w = 1; w < ST / 64; ++w) x = wmax(x, wf[w]);
-    shared_best = x;
+    for (int w = 1; w < VB / 64; ++w) x = wmax(x, wf[w]);
+    parts->bmax[blockIdx.x] = x;
+  }
+}
+
+// (2) each block's count of kept logits (v >= floor)
+__global__ __launch_bounds__(VB) void vocab_count_kernel(const float *logits, int32_t n, DrawParts *parts,
+                                                         float temperature, float topp, double random,
+                                                         const RunParams *params, const int32_t *state) {
+  __shared__ float wf[VB / 64];
+  __shared__ int wi[VB / 64];
+  __shared__ int total;
+  const Settings st = settings(temperature, topp, random, params, state);
+  const float best = best_of(parts, gridDim.x, wf);
+  if (!__builtin_isfinite(best)) return;  // (the whole block: the draw gives SAMPLE_NOT_FINITE)
+  const float floor_ = floor_of(best, st);
+  const int tid = threadIdx.x, i0 = blockIdx.x * CHUNK + tid * VPT;
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    const float v = logits[min(i0 + u, n - 1)];
+    c += i0 + u < n && v >= floor_;
+  }
+  block_scan<VB>(c, wi, &total);
+  if (tid == 0) parts->bcount[blockIdx.x] = total;
+}
+
+// (3) each block's kept values in index order at their places (the counts of the blocks before), their p, the
+// block's largest p and its sum of p (where nothing is left out: the block's values are the total's chunk, the sum
+// the one its binade is guessed from)
+__global__ __launch_bounds__(VB) void vocab_kept_kernel(const float *logits, int32_t n, DrawParts *parts, float *probs,
+                                                        int32_t *index, float temperature, float topp, double random,
+                                                        const RunParams *params, const int32_t *state) {
+  __shared__ float wf[VB / 64], ws[VB / 64];
+  __shared__ int wi[VB / 64];
+  __shared__ int before_, count_, local_;
+  const Settings st = settings(temperature, topp, random, params, state);
+  const int blocks = gridDim.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float best = best_of(parts, blocks, wf);
+  if (!__builtin_isfinite(best)) return;
+  const float floor_ = floor_of(best, st);
+  if (tid < 64) {  // the kept values of the blocks before this one, and of all
+    int a = 0, t = 0;
+    for (int i = tid; i < blocks; i += 64) {
+      const int c = parts->bcount[i];
+      a += i < (int)blockIdx.x ? c : 0;
+      t += c;
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+      a += __shfl_xor(a, o, 64);
+      t += __shfl_xor(t, o, 64);
+    }
+    if (tid == 0) {
+      before_ = a;
+      count_ = t;
+    }
+  }
+  const int i0 = blockIdx.x * CHUNK + tid * VPT;
+  float v[VPT];
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    v[u] = logits[min(i0 + u, n - 1)];
+    c += i0 + u < n && v[u] >= floor_;
+  }
+  int at = block_scan<VB>(c, wi, &local_);  // (its barriers also publish before_ and count_)
+  at += before_;
+  const int count = count_, simd = count & ~3;
+  const float inverse = 1.0f / st.temperature;
+  float top = 0.0f, sum = 0.0f;
+#pragma unroll
+  for (int u = 0; u < VPT; ++u) {
+    if (i0 + u < n && v[u] >= floor_) {
+      const float d = v[u] - best;
+      const float pv = at < simd ? vexp(d * inverse) : fexp(d / st.temperature);
+      probs[at] = pv;
+      index[at] = i0 + u;
+      top = __builtin_fmaxf(top, pv);
+      sum += pv;
+      ++at;
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
+    sum += __shfl_xor(sum, o, 64);
+  }
+  if (lane == 0) {
+    wf[wave] = top;
+    ws[wave] = sum;
   }
   __syncthreads();
-  const float best = shared_best;
+  if (tid == 0) {
+    float x = wf[0], y = ws[0];
+    for (int w = 1; w < VB / 64; ++w) {
+      x = __builtin_fmaxf(x, wf[w]);
+      y += ws[w];
+    }
+    parts->btop[blockIdx.x] = x;
+    parts->csum[blockIdx.x] = y;
+  }
+}
+
+// (4) the draw, one block: the largest logit, the count and the largest p from the blocks' parts; the total's chunks
+// padded with +0.0; the total, the nucleus and the draw
+__device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const DrawParts *parts, float *probs,
+                                          int32_t *index, int32_t *out_token, float *out_best) {
+  __shared__ float4 area[SORT_MOST / 2];  // the sort's probabilities then tokens; the total's guesses
+  float *const sp = reinterpret_cast<float *>(area);
+  int *const si = reinterpret_cast<int *>(area) + SORT_MOST;
+  __shared__ float wf[ST / 64];
+  __shared__ int wi[ST / 64];
+  __shared__ float shared_top;
+  __shared__ int shared_likely;
+  __shared__ double shared_total, shared_cutoff;
+  __shared__ double checkpoints[CP_MOST];  // the running sum of the kept p before every CP_BLOCK of them
+  static_assert(STAGE <= 2 * SORT_MOST, "the staging area is the sort's");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float temperature = st.temperature, topp = st.topp;
+  const double random = st.random;
+  const int blocks = (n + CHUNK - 1) / CHUNK;
+  const float best = best_of(parts, blocks, wf);
   if (!__builtin_isfinite(best)) {
     if (tid == 0) {
       *out_token = SAMPLE_NOT_FINITE;
@@ -441,58 +587,28 @@ __device__ __forceinline__ void sample_block(const float *logits, int32_t n, flo
     return;  // the whole block
   }
   const bool nucleus = topp > 0 && topp < 1;
-  const float floor_ = nucleus ? best - temperature * 16.118095f : -3.4028234663852886e38f;
-
-  // kept: v - best for v >= floor in index order, then p. Each wave takes a contiguous run of the vocabulary, 64
-  // values a step side by side: the count of its run, a block scan over the waves, then the kept values' places in
-  // order (the lanes below in the step, the steps before)
-  const int wrun = ((n + ST / 64 - 1) / (ST / 64) + 63) & ~63, wlo = min(n, wave * wrun), whi = min(n, wlo + wrun);
   const uint64_t below = (1ull << lane) - 1;
   int c = 0;
-  for (int i0 = wlo + lane; i0 < whi; i0 += 64 * VU) {
-    float v[VU];
-#pragma unroll
-    for (int u = 0; u < VU; ++u) v[u] = logits[min(i0 + 64 * u, n - 1)];
-#pragma unroll
-    for (int u = 0; u < VU; ++u) c += i0 + 64 * u < whi && v[u] >= floor_;
+  float top = 0.0f;
+  for (int i = lane; i < blocks; i += 64) {  // (every wave all of them)
+    c += parts->bcount[i];
+    top = __builtin_fmaxf(top, parts->btop[i]);
   }
-  for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, 64);
-  int k = block_scan(lane == 0 ? c : 0, wi, &shared_count);
-  k = __shfl(k, 0, 64);
-  const int count = __builtin_amdgcn_readfirstlane(shared_count), simd = count & ~3;
-  const float inverse = 1.0f / temperature;
-  float top = 0.0f;  // the largest p (order-free)
-  for (int j0 = wlo; j0 < whi; j0 += 64 * VU) {
-    float vs[VU];  // every load of the pass requested before its stores (clamped, unconditional)
-#pragma unroll
-    for (int u = 0; u < VU; ++u) vs[u] = logits[min(j0 + 64 * u + lane, n - 1)];
-#pragma unroll
-    for (int u = 0; u < VU; ++u) {
-      const int i = j0 + 64 * u + lane;
-      const float v = vs[u];
-      const bool keep = i < whi && v >= floor_;
-      const uint64_t mask = __ballot(keep);
-      if (keep) {
-        const int at = k + __popcll(mask & below);
-        const float d = v - best;
-        const float pv = at < simd ? vexp(d * inverse) : fexp(d / temperature);
-        probs[at] = pv;
-        index[at] = i;
-        top = __builtin_fmaxf(top, pv);
-      }
-      k += __popcll(mask);
-    }
+  for (int o = 32; o >= 1; o >>= 1) {
+    c += __shfl_xor(c, o, 64);
+    top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
   }
+  const int count = __builtin_amdgcn_readfirstlane(c);
   for (int j = count + tid; j < (int)sample_probs_floats(count); j += ST) probs[j] = 0.0f;  // the total's whole chunks
+  if (lane == 0) wf[wave] = top;
   __syncthreads();
 
-  // top (order-free) and total (float64, in order: one thread from LDS)
-  for (int o = 32; o >= 1; o >>= 1) top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
-  if (lane == 0) wf[wave] = top;
   // total: float64, in order, by wave 0 from registers
   double total = 0.0;
   static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
-  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area));
+  // (without a nucleus every value is kept: block b's values are the total's chunk b, and its sum of p guesses the
+  // binade there)
+  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts->csum);
   __syncthreads();  // (the waves' maxima in wf too)
   if (tid == 0) {
     float x = wf[0];
@@ -616,20 +732,25 @@ __global__ __launch_bounds__(ST) void ordered_sum_kernel(const float *p, int32_t
   if (threadIdx.x == 0) *total = t;
 }
 
-__global__ __launch_bounds__(ST) void sample_kernel(const float *logits, int32_t n, float temperature, float topp,
-                                                    double random, float *probs, int32_t *index, int32_t *out_token,
-                                                    float *out_best) {
-  sample_block(logits, n, temperature, topp, random, probs, index, out_token, out_best);
+__global__ __launch_bounds__(ST) void draw_kernel(int32_t n, const DrawParts *parts, float *probs, int32_t *index,
+                                                  int32_t *out_token, float *out_best, float temperature, float topp,
+                                                  double random, const RunParams *params, const int32_t *state) {
+  draw_block(n, settings(temperature, topp, random, params, state), parts, probs, index, out_token, out_best);
 }
 
-// ---- the sampled steps of a replayed graph: settings, random numbers and the penalty's window in device memory ----
-
-// a step's draw: the temperature and top-p of the call, the round's random number of this step (state[STATE_STEP])
-__global__ __launch_bounds__(ST) void sample_steps_kernel(const float *logits, int32_t n, const RunParams *params,
-                                                          const int32_t *state, float *probs, int32_t *index,
-                                                          int32_t *out_token, float *out_best) {
-  sample_block(logits, n, params->temperature, params->topp, params->randoms[state[STATE_STEP]], probs, index,
-               out_token, out_best);
+// the four launches of a draw (the settings as values, or with params the call's and the step's from device memory)
+hipError_t launch_draw(const float *logits, int32_t n, float temperature, float topp, double random,
+                       const RunParams *params, const int32_t *state, float *probs, int32_t *index, DrawParts *parts,
+                       int32_t *out_token, float *out_best, hipStream_t s) {
+  const int blocks = (n + CHUNK - 1) / CHUNK;
+  hipLaunchKernelGGL(vocab_max_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts);
+  hipLaunchKernelGGL(vocab_count_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, temperature, topp, random,
+                     params, state);
+  hipLaunchKernelGGL(vocab_kept_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, probs, index, temperature, topp,
+                     random, params, state);
+  hipLaunchKernelGGL(draw_kernel, dim3(1), dim3(ST), 0, s, n, parts, probs, index, out_token, out_best, temperature,
+                     topp, random, params, state);
+  return hipGetLastError();
 }
 
 // the penalty of the call over the window's state[STATE_WINDOW] tokens (in any order: each distinct one once)
@@ -693,11 +814,10 @@ __global__ void advance_steps_kernel(int32_t *tokens, int32_t *state, const int3
 }  // namespace
 
 hipError_t launch_sample_steps(const float *logits, int32_t n, const RunParams *params, const int32_t *state,
-                               float *probs, int32_t *index, int32_t *out_token, float *out_best, hipStream_t s) {
+                               float *probs, int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best,
+                               hipStream_t s) {
   if (n < 1 || n > SAMPLE_MOST) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sample_steps_kernel, dim3(1), dim3(ST), 0, s, logits, n, params, state, probs, index, out_token,
-                     out_best);
-  return hipGetLastError();
+  return launch_draw(logits, n, 0.0f, 0.0f, 0.0, params, state, probs, index, parts, out_token, out_best, s);
 }
 
 hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
@@ -730,11 +850,10 @@ hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *
 }
 
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
-                         int32_t *index, int32_t *out_token, float *out_best, hipStream_t s) {
+                         int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best, hipStream_t s) {
   if (n < 1 || n > SAMPLE_MOST || !(temperature > 0)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(ST), 0, s, logits, n, temperature, topp, random, probs, index,
-                     out_token, out_best);
-  return hipGetLastError();
+  return launch_draw(logits, n, temperature, topp, random, nullptr, nullptr, probs, index, parts, out_token, out_best,
+                     s);
 }
 
 }  // namespace ple
