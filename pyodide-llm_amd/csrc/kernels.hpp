@@ -206,13 +206,22 @@ constexpr int32_t SAMPLE_MOST = 262144;  // logits a draw takes at most
 constexpr int32_t SAMPLE_CHUNK = 2048;
 constexpr size_t sample_probs_floats(int32_t n) { return ((size_t)n + SAMPLE_CHUNK - 1) / SAMPLE_CHUNK * SAMPLE_CHUNK; }
 static_assert(SAMPLE_MOST % SAMPLE_CHUNK == 0, "the largest vocabulary is whole chunks");
+// a chunk of the draw's float64 total taken at a guessed binade of the sum before it (sampling.hip, sum_block): the
+// chunk's sum of r and its lanes' (0, 8, .., 56) sums of r before them, for either parity of the sum before the chunk
+struct ChunkGuess {
+  double t[2];
+  double pre[2][SAMPLE_CHUNK / 32 / 8];
+};
 // what the draw's blocks over the vocabulary (SAMPLE_CHUNK logits each) leave for the draw: each block's largest
-// logit, its count of kept logits, its largest p and its sum of p
+// logit, its count of kept logits, its largest p and its sum of p; and without a nucleus, each chunk of the total at
+// its guessed binade (guess: the binade, or none)
 struct DrawParts {
   float bmax[SAMPLE_MOST / SAMPLE_CHUNK];
   int32_t bcount[SAMPLE_MOST / SAMPLE_CHUNK];
   float btop[SAMPLE_MOST / SAMPLE_CHUNK];
   float csum[SAMPLE_MOST / SAMPLE_CHUNK];
+  int32_t guess[SAMPLE_MOST / SAMPLE_CHUNK];
+  ChunkGuess g[SAMPLE_MOST / SAMPLE_CHUNK];
 };
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
                          int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best, hipStream_t s);

@@ -225,14 +225,25 @@ __device__ __forceinline__ double chunk_exact(const float (&v)[SEG], double run,
   return run;
 }
 
+// one chunk taken at binade e, for either parity of the sum before it: its sum of r and its lanes' sums of r before
+// them (every lane of the wave calls; lanes 0, 8, .., 56 and 63 write)
+__device__ __forceinline__ void chunk_guess(const float (&v)[SEG], int e, ChunkGuess &g) {
+  const int lane = threadIdx.x & 63;
+  const LaneR r = lane_r(v, e);
+#pragma unroll
+  for (int P = 0; P < 2; ++P) {
+    const double inc = lanes_upto(lane_t(r, 0, P));
+    const double excl = __shfl_up(inc, 1, 64);
+    if (lane % (CP_BLOCK / SEG) == 0) g.pre[P][lane / (CP_BLOCK / SEG)] = lane > 0 ? excl : 0.0;
+    if (lane == 63) g.t[P] = inc;
+  }
+}
+
 // what the block's waves leave for the in-order pass: each chunk's guessed binade (NO_GUESS: none) and, at it, the
 // chunk's sum of r and its lanes' (0, 8, .., 56) sums of r before them, for either parity of the sum before the chunk
 constexpr int MOST_CHUNKS = SAMPLE_MOST / CHUNK;
 constexpr int NO_GUESS = -100000;
-struct ChunkGuess {
-  double t[2];
-  double pre[2][CHUNK / CP_BLOCK];
-};
+static_assert(sizeof(ChunkGuess) == sizeof(double) * 2 * (1 + CHUNK / CP_BLOCK), "a chunk's guess");
 struct SumShared {
   double approx[MOST_CHUNKS];  // each chunk's sum in any order
   int guess[MOST_CHUNKS];
@@ -242,14 +253,15 @@ struct SumShared {
 // p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), with the bits of the adds in index order, by the
 // block (all of it calls): chunks of 2048, lane L of a wave holding p[b + 32 L .. b + 32 L + 31] (+0.0 past count,
 // which changes no sum). (1) Every chunk's sum in any order, and from them the binade the running sum probably has
-// at each chunk's start (chunk_sums: those sums given). (2) Each wave takes every waves-th chunk at its guessed binade (lane_r, then lane_t and the
+// at each chunk's start. (2) Each wave takes every waves-th chunk at its guessed binade (lane_r, then lane_t and the
 // lanes' sums for both parities of the sum before it). (3) Wave 0 goes through the chunks in order: where the sum
 // before a chunk has the guessed binade and the chunk's sum of r keeps it below the next power of two, the chunk's end
 // and checkpoints follow from (2) exactly; any other chunk is taken by chunk_exact. With cp, cp[i / CP_BLOCK] = the
-// sum before value i for every multiple i of CP_BLOCK below count. Wave 0 returns the total. (p: 16-byte aligned,
+// sum before value i for every multiple i of CP_BLOCK below count. With given, steps (1) and (2) are its guesses
+// (vocab_guess_kernel's). Wave 0 returns the total. (p: 16-byte aligned,
 // count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
 __device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh,
-                                            const float *chunk_sums = nullptr) {
+                                            const DrawParts *given = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const int chunks = (count + CHUNK - 1) / CHUNK;
   auto load = [&](int c, float(&v)[SEG]) {
@@ -262,53 +274,49 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       v[4 * u + 3] = r.w;
     }
   };
-  if (chunk_sums) {
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x) sh.approx[c] = chunk_sums[c];
+  if (given) {  // steps (1) and (2) done by other blocks
+    for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+      sh.guess[c] = given->guess[c];
+      sh.g[c] = given->g[c];
+    }
   } else {
-  for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
-    const int d = min(c + waves, chunks - 1);  // (past the last chunk: the last again, its sum written twice)
-    float v[SEG], w[SEG];
-    load(c, v);
-    load(d, w);
-    float a = 0.0f, z = 0.0f;  // (float32: these sums only guess the binades)
+    for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
+      const int d = min(c + waves, chunks - 1);  // (past the last chunk: the last again, its sum written twice)
+      float v[SEG], w[SEG];
+      load(c, v);
+      load(d, w);
+      float a = 0.0f, z = 0.0f;  // (float32: these sums only guess the binades)
 #pragma unroll
-    for (int u = 0; u < SEG; ++u) {
-      a += v[u];
-      z += w[u];
+      for (int u = 0; u < SEG; ++u) {
+        a += v[u];
+        z += w[u];
+      }
+      double s = a, t = z;
+      for (int o = 32; o >= 1; o >>= 1) {
+        s += __shfl_xor(s, o, 64);
+        t += __shfl_xor(t, o, 64);
+      }
+      if (lane == 0) {
+        sh.approx[c] = s;
+        sh.approx[d] = t;
+      }
     }
-    double s = a, t = z;
-    for (int o = 32; o >= 1; o >>= 1) {
-      s += __shfl_xor(s, o, 64);
-      t += __shfl_xor(t, o, 64);
+    __syncthreads();
+    if (wave == 0) {
+      // the approximate sums before chunks 2L and 2L + 1
+      const int c0 = 2 * lane, c1 = c0 + 1;
+      const double a0 = c0 < chunks ? sh.approx[c0] : 0.0, a1 = c1 < chunks ? sh.approx[c1] : 0.0;
+      const double before = lanes_upto(a0 + a1) - (a0 + a1), mid = before + a0;
+      if (c0 < chunks) sh.guess[c0] = before > 0.0 ? binade(before) : NO_GUESS;
+      if (c1 < chunks) sh.guess[c1] = mid > 0.0 ? binade(mid) : NO_GUESS;
     }
-    if (lane == 0) {
-      sh.approx[c] = s;
-      sh.approx[d] = t;
-    }
-  }
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // the approximate sums before chunks 2L and 2L + 1
-    const int c0 = 2 * lane, c1 = c0 + 1;
-    const double a0 = c0 < chunks ? sh.approx[c0] : 0.0, a1 = c1 < chunks ? sh.approx[c1] : 0.0;
-    const double before = lanes_upto(a0 + a1) - (a0 + a1), mid = before + a0;
-    if (c0 < chunks) sh.guess[c0] = before > 0.0 ? binade(before) : NO_GUESS;
-    if (c1 < chunks) sh.guess[c1] = mid > 0.0 ? binade(mid) : NO_GUESS;
-  }
-  __syncthreads();
-  for (int c = wave; c < chunks; c += waves) {
-    const int e = sh.guess[c];
-    if (e == NO_GUESS) continue;  // (uniform)
-    float v[SEG];
-    load(c, v);
-    const LaneR r = lane_r(v, e);
-#pragma unroll
-    for (int P = 0; P < 2; ++P) {
-      const double inc = lanes_upto(lane_t(r, 0, P));
-      const double excl = __shfl_up(inc, 1, 64);
-      if (lane % (CP_BLOCK / SEG) == 0) sh.g[c].pre[P][lane / (CP_BLOCK / SEG)] = lane > 0 ? excl : 0.0;
-      if (lane == 63) sh.g[c].t[P] = inc;
+    __syncthreads();
+    for (int c = wave; c < chunks; c += waves) {
+      const int e = sh.guess[c];
+      if (e == NO_GUESS) continue;  // (uniform)
+      float v[SEG];
+      load(c, v);
+      chunk_guess(v, e, sh.g[c]);
     }
   }
   __syncthreads();
@@ -526,6 +534,8 @@ __global__ __launch_bounds__(VB) void vocab_kept_kernel(const float *logits, int
   int at = block_scan<VB>(c, wi, &local_);  // (its barriers also publish before_ and count_)
   at += before_;
   const int count = count_, simd = count & ~3;
+  if (blockIdx.x == 0)  // +0.0 from count to the end of its chunk: the total reads whole chunks
+    for (int j = count + tid; j < (int)sample_probs_floats(count); j += VB) probs[j] = 0.0f;
   const float inverse = 1.0f / st.temperature;
   float top = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -560,7 +570,37 @@ __global__ __launch_bounds__(VB) void vocab_kept_kernel(const float *logits, int
   }
 }
 
-// (4) the draw, one block: the largest logit, the count and the largest p from the blocks' parts; the total's chunks
+// (4) without a nucleus, each chunk of the total at its guessed binade, a wave a chunk: every value is kept, so block
+// b's values are the total's chunk b (unless some logits are -inf: then the guesses are only worse), the binade of the
+// sum before it is guessed from the blocks' sums of p, and chunk_guess takes the chunk at that binade; with a nucleus
+// the draw takes the chunks itself
+__global__ __launch_bounds__(64) void vocab_guess_kernel(int32_t n, DrawParts *parts, const float *probs,
+                                                         float temperature, float topp, double random,
+                                                         const RunParams *params, const int32_t *state) {
+  __shared__ float wf[1];
+  const Settings st = settings(temperature, topp, random, params, state);
+  if (st.topp > 0 && st.topp < 1) return;
+  if (!__builtin_isfinite(best_of(parts, gridDim.x, wf))) return;  // (the draw gives SAMPLE_NOT_FINITE)
+  const int b = blockIdx.x, lane = threadIdx.x;
+  double a = 0.0;  // the sum of p before the chunk, in any order
+  for (int i = lane; i < b; i += 64) a += parts->csum[i];
+  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
+  const int e = a > 0.0 ? binade(a) : NO_GUESS;
+  if (lane == 0) parts->guess[b] = e;
+  if (e == NO_GUESS) return;
+  float v[SEG];
+#pragma unroll
+  for (int u = 0; u < SEG / 4; ++u) {
+    const float4 r = reinterpret_cast<const float4 *>(probs + b * CHUNK + lane * SEG)[u];
+    v[4 * u] = r.x;
+    v[4 * u + 1] = r.y;
+    v[4 * u + 2] = r.z;
+    v[4 * u + 3] = r.w;
+  }
+  chunk_guess(v, e, parts->g[b]);
+}
+
+// (5) the draw, one block: the largest logit, the count and the largest p from the blocks' parts; the total's chunks
 // padded with +0.0; the total, the nucleus and the draw
 __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const DrawParts *parts, float *probs,
                                           int32_t *index, int32_t *out_token, float *out_best) {
@@ -598,17 +638,15 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
     c += __shfl_xor(c, o, 64);
     top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
   }
-  const int count = __builtin_amdgcn_readfirstlane(c);
-  for (int j = count + tid; j < (int)sample_probs_floats(count); j += ST) probs[j] = 0.0f;  // the total's whole chunks
+  const int count = __builtin_amdgcn_readfirstlane(c);  // (probs is +0.0 from count to its chunk's end)
   if (lane == 0) wf[wave] = top;
   __syncthreads();
 
   // total: float64, in order, by wave 0 from registers
   double total = 0.0;
   static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
-  // (without a nucleus every value is kept: block b's values are the total's chunk b, and its sum of p guesses the
-  // binade there)
-  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts->csum);
+  // (without a nucleus the chunks' guesses come from vocab_guess_kernel)
+  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts);
   __syncthreads();  // (the waves' maxima in wf too)
   if (tid == 0) {
     float x = wf[0];
@@ -738,7 +776,7 @@ __global__ __launch_bounds__(ST) void draw_kernel(int32_t n, const DrawParts *pa
   draw_block(n, settings(temperature, topp, random, params, state), parts, probs, index, out_token, out_best);
 }
 
-// the four launches of a draw (the settings as values, or with params the call's and the step's from device memory)
+// the five launches of a draw (the settings as values, or with params the call's and the step's from device memory)
 hipError_t launch_draw(const float *logits, int32_t n, float temperature, float topp, double random,
                        const RunParams *params, const int32_t *state, float *probs, int32_t *index, DrawParts *parts,
                        int32_t *out_token, float *out_best, hipStream_t s) {
@@ -748,6 +786,8 @@ hipError_t launch_draw(const float *logits, int32_t n, float temperature, float 
                      params, state);
   hipLaunchKernelGGL(vocab_kept_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, probs, index, temperature, topp,
                      random, params, state);
+  hipLaunchKernelGGL(vocab_guess_kernel, dim3(blocks), dim3(64), 0, s, n, parts, probs, temperature, topp, random,
+                     params, state);
   hipLaunchKernelGGL(draw_kernel, dim3(1), dim3(ST), 0, s, n, parts, probs, index, out_token, out_best, temperature,
                      topp, random, params, state);
   return hipGetLastError();
