@@ -233,8 +233,10 @@ int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t coun
 
 /* The float64 total of sample()'s kept probabilities (kernels/kernel.ts:845-850: total += p in index order) on device
  * p (n floats, 1 <= n <= 262144) into *total (host), and with checkpoints (host, ceil(n / 256) doubles, or null) the
- * running sum before every 256 values, as the draw's search takes them. Blocks until done. */
-int32_t hk_ordered_sum(const void *p, int32_t n, double *total, double *checkpoints, void *stream);
+ * running sum before every 256 values, as the draw's search takes them; nucleus nonzero: by the one block that the
+ * draw with a nucleus uses, else as the draw without one takes it (its chunks guessed over the CUs first). The same
+ * bits either way. Blocks until done. */
+int32_t hk_ordered_sum(const void *p, int32_t n, int32_t nucleus, double *total, double *checkpoints, void *stream);
 
 /* kernels/kernel.ts:803-868 sample on device logits (n floats): the token drawn for random in [0, 1) into *token
  * (host): -1 where the largest logit is not finite, -2 where the nucleus holds more than 8192 tokens. temperature

@@ -946,11 +946,13 @@ void build_graph(he_engine *e, int kind) {
     if (rc == HE_OK) {
       const int32_t n = e->c.vocab_size;
       hipError_t le = hipSuccess;
-      if (kind & STEP_PENALIZED) le = launch_penalize_steps(e->logits, e->window, e->state, e->run_params, e->stream);
-      const bool drawn = (kind & STEP_SAMPLED) != 0;
+      const bool drawn = (kind & STEP_SAMPLED) != 0, penalized = (kind & STEP_PENALIZED) != 0;
+      // (a drawn step takes the penalty in the draw's first launch)
+      if (penalized && !drawn) le = launch_penalize_steps(e->logits, e->window, e->state, e->run_params, e->stream);
       if (le == hipSuccess)
-        le = drawn ? launch_sample_steps(e->logits, n, e->run_params, e->state, e->sample_probs, e->sample_index,
-                                         e->sample_parts, e->sample_token, e->sample_best, e->stream)
+        le = drawn ? launch_sample_steps(e->logits, n, e->run_params, e->state, penalized ? e->window : nullptr,
+                                         e->sample_probs, e->sample_index, e->sample_parts, e->sample_token,
+                                         e->sample_best, e->stream)
                    : launch_argmax(e->best_i, e->best_v, e->logits, n, e->amax_v, e->amax_i, e->stream);
       if (le == hipSuccess)
         le = launch_step_end(e->logits, n, e->kept_logits, e->tokens, e->state, drawn ? e->sample_token : e->best_i,
@@ -1411,20 +1413,22 @@ int32_t hk_penalize(void *logits, int32_t n, const int32_t *tokens, int32_t coun
   return HE_OK;
 }
 
-int32_t hk_ordered_sum(const void *p, int32_t n, double *total, double *checkpoints, void *stream) {
+int32_t hk_ordered_sum(const void *p, int32_t n, int32_t nucleus, double *total, double *checkpoints, void *stream) {
   if (!p || !total || n < 1 || n > SAMPLE_MOST) return fail(HE_E_ARG, "hk_ordered_sum: bad arguments");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int32_t ncp = (n + SAMPLE_CHECKPOINT - 1) / SAMPLE_CHECKPOINT;
   float *padded = nullptr;
   double *out = nullptr;
+  DrawParts *parts = nullptr;
   int32_t rc = dev_alloc(&padded, sizeof(float) * sample_probs_floats(n));  // whole chunks, as the draw's buffers
   if (!rc) rc = dev_alloc(&out, sizeof(double) * (1 + (size_t)ncp));
+  if (!rc && !nucleus) rc = dev_alloc(&parts, sizeof(DrawParts));
   hipError_t err = hipSuccess;
   if (!rc) {
     err = hipMemcpyAsync(padded, p, sizeof(float) * (size_t)n, hipMemcpyDeviceToDevice, s);
     if (err == hipSuccess)  // +0.0 to the chunk's end, as the draw leaves its buffer
       err = hipMemsetAsync(padded + n, 0, sizeof(float) * (sample_probs_floats(n) - (size_t)n), s);
-    if (err == hipSuccess) err = launch_ordered_sum(padded, n, out, out + 1, s);
+    if (err == hipSuccess) err = launch_ordered_sum(padded, n, out, out + 1, parts, s);
     if (err == hipSuccess) err = hipMemcpyAsync(total, out, sizeof(double), hipMemcpyDeviceToHost, s);
     if (err == hipSuccess && checkpoints)
       err = hipMemcpyAsync(checkpoints, out + 1, sizeof(double) * (size_t)ncp, hipMemcpyDeviceToHost, s);
@@ -1432,6 +1436,7 @@ int32_t hk_ordered_sum(const void *p, int32_t n, double *total, double *checkpoi
   }
   if (padded) (void)hipFree(padded);
   if (out) (void)hipFree(out);
+  if (parts) (void)hipFree(parts);
   if (rc) return rc;
   if (err != hipSuccess) return fail(HE_E_HIP, std::string("hk_ordered_sum: ") + hipGetErrorString(err));
   return HE_OK;
@@ -1467,8 +1472,8 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
 }  // extern "C"
 
 // hk_sample_static's scratch: probabilities [HK_SAMPLE_STATIC_MOST] float32, token indices [HK_SAMPLE_STATIC_MOST]
-// int32, then the drawn token and the largest logit, 256 bytes apart, then the draw's parts (DrawParts: 2 KiB), in
-// all 2 MiB and 2.5 KiB. Every GPU holds its own
+// int32, then the drawn token and the largest logit, 256 bytes apart, then the draw's parts (DrawParts: 277 KiB), in
+// all 2 MiB and 278 KiB. Every GPU holds its own
 // copy at its own address, found once a device with hipGetSymbolAddress: in host code the array's name is a stand-in,
 // not a device address, and is never passed to a kernel or a copy.
 namespace ple {
@@ -1476,6 +1481,7 @@ constexpr size_t SAMPLE_INDEX_AT = 4 * (size_t)HK_SAMPLE_STATIC_MOST, SAMPLE_TOK
 constexpr size_t SAMPLE_BEST_AT = SAMPLE_TOKEN_AT + 256, SAMPLE_PARTS_AT = SAMPLE_BEST_AT + 256;
 constexpr size_t SAMPLE_SCRATCH_BYTES = SAMPLE_PARTS_AT + sizeof(DrawParts);
 __device__ __align__(256) uint8_t scratch[SAMPLE_SCRATCH_BYTES];
+static_assert(SAMPLE_SCRATCH_BYTES <= (2u << 20) + 278u * 1024, "the static scratch's stated size");
 static_assert(sample_probs_floats(HK_SAMPLE_STATIC_MOST) == (size_t)HK_SAMPLE_STATIC_MOST,
               "the probabilities' region holds the sampler's whole chunks");
 }  // namespace ple

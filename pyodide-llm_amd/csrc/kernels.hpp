@@ -206,15 +206,24 @@ constexpr int32_t SAMPLE_MOST = 262144;  // logits a draw takes at most
 constexpr int32_t SAMPLE_CHUNK = 2048;
 constexpr size_t sample_probs_floats(int32_t n) { return ((size_t)n + SAMPLE_CHUNK - 1) / SAMPLE_CHUNK * SAMPLE_CHUNK; }
 static_assert(SAMPLE_MOST % SAMPLE_CHUNK == 0, "the largest vocabulary is whole chunks");
+constexpr int32_t SAMPLE_CHECKPOINT = 256;  // values between two checkpoints of the draw's running sum
 // a chunk of the draw's float64 total taken at a guessed binade of the sum before it (sampling.hip, sum_block): the
 // chunk's sum of r and its lanes' (0, 8, .., 56) sums of r before them, for either parity of the sum before the chunk
 struct ChunkGuess {
   double t[2];
   double pre[2][SAMPLE_CHUNK / 32 / 8];
 };
+// a lane's 32 values of a chunk taken at one binade, whatever the sum before them (sampling.hip, lane_r): the lane's
+// sum of r with its first tie's 1 left out, and its flags (bit 0 the parity flips after the last tie, bit 1 a tie
+// seen, bit 2 the first tie's c)
+struct LanePack {
+  double s0;
+  int32_t flags, unused;
+};
 // what the draw's blocks over the vocabulary (SAMPLE_CHUNK logits each) leave for the draw: each block's largest
 // logit, its count of kept logits, its largest p and its sum of p; and without a nucleus, each chunk of the total at
-// its guessed binade (guess: the binade, or none)
+// its guessed binade (guess: the binade, or none), its lanes at that binade and the next, whether its sum probably
+// crosses into the next (cross), and the first chunk's end and checkpoints
 struct DrawParts {
   float bmax[SAMPLE_MOST / SAMPLE_CHUNK];
   int32_t bcount[SAMPLE_MOST / SAMPLE_CHUNK];
@@ -222,13 +231,18 @@ struct DrawParts {
   float csum[SAMPLE_MOST / SAMPLE_CHUNK];
   int32_t guess[SAMPLE_MOST / SAMPLE_CHUNK];
   ChunkGuess g[SAMPLE_MOST / SAMPLE_CHUNK];
+  LanePack lanes[SAMPLE_MOST / SAMPLE_CHUNK][2][64];
+  int32_t cross[SAMPLE_MOST / SAMPLE_CHUNK];
+  double first_end;
+  double first_cp[SAMPLE_CHUNK / SAMPLE_CHECKPOINT];
 };
 hipError_t launch_sample(const float *logits, int32_t n, float temperature, float topp, double random, float *probs,
                          int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best, hipStream_t s);
 // the draw's float64 total of p[0..n) in index order (kernels/kernel.ts:845-850), and the running sum before every
-// SAMPLE_CHECKPOINT values (checkpoints: ceil(n / SAMPLE_CHECKPOINT) doubles); p: sample_probs_floats(n) floats
-constexpr int32_t SAMPLE_CHECKPOINT = 256;
-hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *checkpoints, hipStream_t s);
+// SAMPLE_CHECKPOINT values (checkpoints: ceil(n / SAMPLE_CHECKPOINT) doubles); p: sample_probs_floats(n) floats. With
+// parts, as the draw without a nucleus takes it (the chunks guessed over the CUs first); else as with one
+hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *checkpoints, DrawParts *parts,
+                              hipStream_t s);
 // ---- replayed decode steps (a captured graph of one step, replayed a round at a time) ----
 // the step's state in device memory: the position, the step of the round, the halting step + 1 (0: none yet), the
 // penalty window's count and its oldest entry once full
@@ -243,10 +257,12 @@ struct RunParams {
   int32_t n_stops;
   int32_t stops[RUN_STOPS_MOST];
 };
-// a step's draw (as launch_sample) with the call's temperature and top-p and the round's random number of the step
-hipError_t launch_sample_steps(const float *logits, int32_t n, const RunParams *params, const int32_t *state,
-                               float *probs, int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best,
-                               hipStream_t s);
+// a step's draw (as launch_sample) with the call's temperature and top-p and the round's random number of the step;
+// with window, the call's penalty over the window's state[STATE_WINDOW] tokens first (launch_penalize_steps's, in the
+// draw's first launch: the logits penalized in place)
+hipError_t launch_sample_steps(float *logits, int32_t n, const RunParams *params, const int32_t *state,
+                               const int32_t *window, float *probs, int32_t *index, DrawParts *parts,
+                               int32_t *out_token, float *out_best, hipStream_t s);
 // the call's penalty over the window's state[STATE_WINDOW] tokens
 hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
                                  hipStream_t s);

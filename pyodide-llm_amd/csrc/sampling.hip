@@ -123,35 +123,63 @@ __device__ __forceinline__ LaneR lane_r(const float (&v)[SEG], int e) {
   return {sq + (double)(st >> 3), (st >> 1) & 1, st & 1, (st >> 2) & 1};
 }
 
-// the lane's sum of r where lane from's incoming parity is pin0 (lanes below from: 0): the lanes' incoming parities
-// from lane masks, the last lane below with a tie and the flips since
-__device__ __forceinline__ double lane_t(const LaneR &r, int from, int pin0) {
+__device__ __forceinline__ LanePack pack(const LaneR &r) { return {r.s0, r.x | (r.seen << 1) | (r.cfirst << 2), 0}; }
+__device__ __forceinline__ LaneR unpack(const LanePack &p) {
+  return {p.s0, (p.flags >> 1) & 1, p.flags & 1, (p.flags >> 2) & 1};
+}
+
+// the parity (of the sum / u) that this lane receives, where lane `from` (the lowest with mine) receives pin0 and
+// each lane with mine hands on either a fixed parity (seen: x) or the one it received flipped by x: from lane masks,
+// the last lane below with a fixed parity and the flips since
+__device__ __forceinline__ int parity_in(bool mine, int seen, int x, int pin0) {
   const int lane = threadIdx.x & 63;
-  const bool mine = lane >= from;
   const uint64_t below = (1ull << lane) - 1;
-  const uint64_t mt = __ballot(mine && r.seen), mk = __ballot(mine && r.seen && r.x),
-                 mx = __ballot(mine && !r.seen && r.x);
-  int pin;
+  const uint64_t mt = __ballot(mine && seen), mk = __ballot(mine && seen && x), mx = __ballot(mine && !seen && x);
   if (mt & below) {
     const int last = 63 - __builtin_clzll(mt & below);
     const uint64_t since = below & ~((2ull << last) - 1);
-    pin = (int)((mk >> last) & 1) ^ (__builtin_popcountll(mx & since) & 1);
-  } else {
-    pin = pin0 ^ (__builtin_popcountll(mx & below) & 1);
+    return (int)((mk >> last) & 1) ^ (__builtin_popcountll(mx & since) & 1);
   }
+  return pin0 ^ (__builtin_popcountll(mx & below) & 1);
+}
+
+// the lane's sum of r where lane from's incoming parity is pin0 (lanes below from: 0)
+__device__ __forceinline__ double lane_t(const LaneR &r, int from, int pin0) {
+  const bool mine = (int)(threadIdx.x & 63) >= from;
+  const int pin = parity_in(mine, r.seen, r.x, pin0);
   return mine ? r.s0 + (r.seen ? (double)(pin ^ r.cfirst) : 0.0) : 0.0;
 }
 
-// the sum of t over the lanes up to this one (exact: integers below 2^53 up to the first lane that leaves the binade)
+// a double moved across the lanes by a DPP control (lanes with no source, or in rows the mask leaves out, get 0)
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ double dpp_move(double x) {
+  return __hiloint2double(__builtin_amdgcn_update_dpp(0, __double2hiint(x), CTRL, ROWS, 0xf, true),
+                          __builtin_amdgcn_update_dpp(0, __double2loint(x), CTRL, ROWS, 0xf, true));
+}
+
+// the sum of t over the lanes up to this one: row shifts by 1, 2, 4 and 8, then lane 15 of each row into the next and
+// lane 31 into the upper half. Exact on integers whose sum up to this lane is below 2^53, whatever the order of the
+// adds (every partial sum is below it too); past the first lane whose sum leaves the binade nothing is used.
 __device__ __forceinline__ double lanes_upto(double t) {
-  const int lane = threadIdx.x & 63;
-  double inc = t;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const double y = __shfl_up(inc, o, 64);
-    inc = lane >= o ? inc + y : inc;
-  }
-  return inc;
+  t = t + dpp_move<0x111>(t);
+  t = t + dpp_move<0x112>(t);
+  t = t + dpp_move<0x114>(t);
+  t = t + dpp_move<0x118>(t);
+  t = t + dpp_move<0x142, 0xa>(t);
+  t = t + dpp_move<0x143, 0xc>(t);
+  return t;
+}
+// the value of the lane below (lane 0: 0)
+__device__ __forceinline__ double lane_below(double x) { return dpp_move<0x138>(x); }
+
+// a double that is the same in every lane, or lane l's, as a uniform value
+__device__ __forceinline__ double uniform(double x) {
+  return __hiloint2double(__builtin_amdgcn_readfirstlane(__double2hiint(x)),
+                          __builtin_amdgcn_readfirstlane(__double2loint(x)));
+}
+__device__ __forceinline__ double from_lane(double x, int l) {
+  return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(x), l),
+                          __builtin_amdgcn_readlane(__double2loint(x), l));
 }
 
 __device__ __forceinline__ int binade(double s) { return ((__double2hiint(s) >> 20) & 0x7ff) - 1023; }  // s > 0, normal
@@ -159,18 +187,22 @@ __device__ __forceinline__ int binade(double s) { return ((__double2hiint(s) >> 
 // Lanes from..63 of a chunk in parallel at run's binade e (lanes below from take no part: their values are done).
 // Returns the first lane whose values take the sum to 2^(e+1) or past it, 64 if none; *start is the sum before this
 // lane's values (right for the lanes from..the returned one), *end the chunk's end where 64 is returned.
-__device__ __forceinline__ int chunk_lanes(const float (&v)[SEG], double run, int from, double *start, double *end) {
+// (r: the lanes' values taken at run's binade, lane_r)
+__device__ __forceinline__ int chunk_lanes_r(const LaneR &r, double run, int from, double *start, double *end) {
   const int lane = threadIdx.x & 63;
   const int e = binade(run);
-  const double t = lane_t(lane_r(v, e), from, __double2loint(run) & 1);  // lane from: the parity of run / u
+  const double t = lane_t(r, from, __double2loint(run) & 1);  // lane from: the parity of run / u
   const double inc = lanes_upto(t);
   const double base = __builtin_ldexp(run, 52 - e);  // run / u
   const uint64_t over = __ballot(!(base + inc < 9007199254740992.0));  // lanes whose sum reaches 2^(e+1)
-  const double excl = __shfl_up(inc, 1, 64);  // the lanes below (inc - t would not be exact in a lane past 2^53)
-  *start = run + __builtin_ldexp(lane > 0 ? excl : 0.0, e - 52);
+  const double excl = lane_below(inc);  // the lanes below (inc - t would not be exact in a lane past 2^53)
+  *start = run + __builtin_ldexp(excl, e - 52);
   if (over) return __builtin_ctzll(over);
-  *end = run + __builtin_ldexp(__shfl(inc, 63, 64), e - 52);
+  *end = run + __builtin_ldexp(from_lane(inc, 63), e - 52);
   return 64;
+}
+__device__ __forceinline__ int chunk_lanes(const float (&v)[SEG], double run, int from, double *start, double *end) {
+  return chunk_lanes_r(lane_r(v, binade(run)), run, from, start, end);
 }
 
 // One chunk (values b.., lane L's 32 at b + 32 L) exactly from run, by one wave: the lanes in parallel while the sum
@@ -189,22 +221,19 @@ __device__ __forceinline__ double chunk_exact(const float (&v)[SEG], double run,
     if (run > 0.0) cross = chunk_lanes(v, run, from, &start, &end);
     if (lane >= from && lane <= cross) pre = start;
     if (cross == 64) {
-      run = __hiloint2double(__builtin_amdgcn_readfirstlane(__double2hiint(end)),
-                             __builtin_amdgcn_readfirstlane(__double2loint(end)));  // (the same in every lane)
+      run = uniform(end);
       from = 64;
       break;
     }
     // lane cross's values in order from its start (every lane adds its own; lane cross's sum is kept)
-    double acc = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(start), cross),
-                                  __builtin_amdgcn_readlane(__double2loint(start), cross));
+    double acc = from_lane(start, cross);
 #pragma unroll
     for (int u = 0; u < SEG; ++u) {
       float t = v[u];
       asm volatile("" : "+v"(t));  // (widened here, one at a time: all 32 held widened would not fit)
       acc = acc + (double)t;
     }
-    run = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(acc), cross),
-                           __builtin_amdgcn_readlane(__double2loint(acc), cross));
+    run = from_lane(acc, cross);
     from = cross + 1;
   }
   // lane by lane: in turn s lane s adds its values to the sum in acc (every lane adds its own; lane s + 1 takes lane
@@ -218,26 +247,74 @@ __device__ __forceinline__ double chunk_exact(const float (&v)[SEG], double run,
       asm volatile("" : "+v"(t));
       acc = acc + (double)t;
     }
-    run = __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(acc), s),
-                           __builtin_amdgcn_readlane(__double2loint(acc), s));
+    run = from_lane(acc, s);
   }
   if (cp && lane % (CP_BLOCK / SEG) == 0 && b + SEG * lane < count) cp[(b + SEG * lane) / CP_BLOCK] = pre;
   return run;
 }
 
+// One chunk (values b.., lane L's 32 at b + 32 L) exactly from run > 0 at lane from (the lanes below it done, their
+// sums before them in pre), from its lanes already taken at binades E .. E + W - 1 (at(k): binade E + k): each run of
+// lanes that keeps the sum in one binade in parallel, as chunk_exact, and each lane that takes it out of its binade by
+// its adds in order, however many there are; while the sum is below 2^E, a lane at a time in order. Returns false,
+// having written nothing, where the sum reaches a binade above those; else true, *end the chunk's end and, with cp,
+// the checkpoints of the chunk's values.
+template <int W, typename At>
+__device__ __forceinline__ bool chunk_walk(const float (&v)[SEG], double run, int from, double pre, int E, At at, int b,
+                                           int count, double *cp, double *end) {
+  const int lane = threadIdx.x & 63;
+  while (from < 64) {
+    const int k = binade(run) - E;
+    if (k >= W) return false;  // (uniform)
+    if (k < 0) {  // lane from's values in order (every lane adds its own; lane from's sum is kept)
+      if (lane == from) pre = run;
+      double acc = run;
+#pragma unroll
+      for (int u = 0; u < SEG; ++u) {
+        float t = v[u];
+        asm volatile("" : "+v"(t));
+        acc = acc + (double)t;
+      }
+      run = from_lane(acc, from);
+      ++from;
+      continue;
+    }
+    double start = run, stop = 0.0;
+    const int cross = chunk_lanes_r(at(k), run, from, &start, &stop);
+    if (lane >= from && lane <= cross) pre = start;
+    if (cross == 64) {
+      run = uniform(stop);
+      break;
+    }
+    // lane cross's values in order from its start (every lane adds its own; lane cross's sum is kept)
+    double acc = from_lane(start, cross);
+#pragma unroll
+    for (int u = 0; u < SEG; ++u) {
+      float t = v[u];
+      asm volatile("" : "+v"(t));
+      acc = acc + (double)t;
+    }
+    run = from_lane(acc, cross);
+    from = cross + 1;
+  }
+  if (cp && lane % (CP_BLOCK / SEG) == 0 && b + SEG * lane < count) cp[(b + SEG * lane) / CP_BLOCK] = pre;
+  *end = run;
+  return true;
+}
+
 // one chunk taken at binade e, for either parity of the sum before it: its sum of r and its lanes' sums of r before
 // them (every lane of the wave calls; lanes 0, 8, .., 56 and 63 write)
-__device__ __forceinline__ void chunk_guess(const float (&v)[SEG], int e, ChunkGuess &g) {
+__device__ __forceinline__ void chunk_guess_r(const LaneR &r, ChunkGuess &g) {
   const int lane = threadIdx.x & 63;
-  const LaneR r = lane_r(v, e);
 #pragma unroll
   for (int P = 0; P < 2; ++P) {
     const double inc = lanes_upto(lane_t(r, 0, P));
-    const double excl = __shfl_up(inc, 1, 64);
-    if (lane % (CP_BLOCK / SEG) == 0) g.pre[P][lane / (CP_BLOCK / SEG)] = lane > 0 ? excl : 0.0;
+    const double excl = lane_below(inc);
+    if (lane % (CP_BLOCK / SEG) == 0) g.pre[P][lane / (CP_BLOCK / SEG)] = excl;
     if (lane == 63) g.t[P] = inc;
   }
 }
+__device__ __forceinline__ void chunk_guess(const float (&v)[SEG], int e, ChunkGuess &g) { chunk_guess_r(lane_r(v, e), g); }
 
 // what the block's waves leave for the in-order pass: each chunk's guessed binade (NO_GUESS: none) and, at it, the
 // chunk's sum of r and its lanes' (0, 8, .., 56) sums of r before them, for either parity of the sum before the chunk
@@ -249,6 +326,22 @@ struct SumShared {
   int guess[MOST_CHUNKS];
   ChunkGuess g[MOST_CHUNKS];
 };
+// a chunk whose sum probably crosses a binade, held in LDS for the in-order pass: its values (float4 u of lane L at
+// v[64 u + L]) and its lanes at two binades
+constexpr int NSLOT = 8;
+struct Slot {
+  float4 v[SEG / 4 * 64];
+  LanePack r[2][64];
+};
+// the j-th set bit of the 128-bit mask (lo, hi), 128 if none
+__device__ __forceinline__ int nth_bit(uint64_t lo, uint64_t hi, int j) {
+  const int below = __builtin_popcountll(lo);
+  uint64_t m = j < below ? lo : hi;
+  int k = j < below ? j : j - below;
+  if (k >= __builtin_popcountll(m)) return 128;
+  for (; k > 0; --k) m &= m - 1;
+  return (j < below ? 0 : 64) + __builtin_ctzll(m);
+}
 
 // p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), with the bits of the adds in index order, by the
 // block (all of it calls): chunks of 2048, lane L of a wave holding p[b + 32 L .. b + 32 L + 31] (+0.0 past count,
@@ -261,7 +354,7 @@ struct SumShared {
 // (vocab_guess_kernel's). Wave 0 returns the total. (p: 16-byte aligned,
 // count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
 __device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh,
-                                            const DrawParts *given = nullptr) {
+                                            const DrawParts *given = nullptr, Slot *slots = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const int chunks = (count + CHUNK - 1) / CHUNK;
   auto load = [&](int c, float(&v)[SEG]) {
@@ -274,10 +367,25 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       v[4 * u + 3] = r.w;
     }
   };
+  // with given: the chunks that probably cross a binade (the first NSLOT of them in slots, one a wave from wave 1)
+  uint64_t cross_lo = 0, cross_hi = 0;
   if (given) {  // steps (1) and (2) done by other blocks
     for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
       sh.guess[c] = given->guess[c];
       sh.g[c] = given->g[c];
+    }
+    if (slots && wave <= NSLOT) {
+      cross_lo = __ballot(lane > 0 && lane < chunks && given->cross[lane]);
+      cross_hi = __ballot(lane + 64 < chunks && given->cross[lane + 64]);
+      const int c = wave > 0 ? nth_bit(cross_lo, cross_hi, wave - 1) : 128;
+      if (c < chunks) {
+        Slot &sl = slots[wave - 1];
+#pragma unroll
+        for (int u = 0; u < SEG / 4; ++u)
+          sl.v[64 * u + lane] = reinterpret_cast<const float4 *>(p + c * CHUNK + lane * SEG)[u];
+        sl.r[0][lane] = given->lanes[c][0][lane];
+        sl.r[1][lane] = given->lanes[c][1][lane];
+      }
     }
   } else {
     for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
@@ -331,31 +439,77 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
     const double t00 = c0 < chunks ? sh.g[c0].t[0] : 0.0, t01 = c0 < chunks ? sh.g[c0].t[1] : 0.0;
     const double t10 = c1 < chunks ? sh.g[c1].t[0] : 0.0, t11 = c1 < chunks ? sh.g[c1].t[1] : 0.0;
     double before0 = -1.0, before1 = -1.0;  // the sum before a chunk taken from its guess (-1: not so taken)
-    auto from_lane = [](double x, int l) {
-      return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(x), l),
-                              __builtin_amdgcn_readlane(__double2loint(x), l));
-    };
-    for (int c = 0; c < chunks; ++c) {
+    int c = 0;
+    if (given) {  // the first chunk, from 0, done by vocab_guess_kernel
+      run = given->first_end;
+      if (cp && lane < CHUNK / CP_BLOCK && lane * CP_BLOCK < count) cp[lane] = given->first_cp[lane];
+      c = 1;
+    }
+    while (c < chunks) {
+      if (run > 0.0) {
+        // the chunks from c to the end of its group of 64 (a lane each) that keep the sum in run's binade E, at once:
+        // a chunk's parity out (of the sum / u) is (P + T[P]) mod 2 of its parity in P, so either fixed or P flipped
+        // or not; the parities in follow from lane masks (parity_in), then the chunks' T by a scan. The run stops at
+        // the first chunk whose guess is not E or whose T takes the sum to 2^(E+1).
+        const int h = c >> 6, l = c & 63;
+        const int E = binade(run);
+        const double Ta = h ? t10 : t00, Tb = h ? t11 : t01;
+        const bool fit = lane >= l && 64 * h + lane < chunks && (h ? eg1 : eg0) == E;
+        const double ha = Ta * 0.5, hb = Tb * 0.5;
+        const int f0 = ha != __builtin_floor(ha), f1 = hb == __builtin_floor(hb);  // the parity out for 0 and for 1
+        const int pin = parity_in(fit, f0 == f1, f0, __double2loint(run) & 1);
+        const double inc = lanes_upto(fit ? (pin ? Tb : Ta) : 0.0);
+        const uint64_t stop_at =
+            __ballot(lane >= l && !(fit && __builtin_ldexp(run, 52 - E) + inc < 9007199254740992.0));
+        const int stop = stop_at ? __builtin_ctzll(stop_at) : 64;
+        if (lane >= l && lane < stop) {
+          const double bf = run + __builtin_ldexp(lane_below(inc), E - 52);
+          if (h) before1 = bf;
+          else before0 = bf;
+        }
+        if (stop > l) run = run + __builtin_ldexp(from_lane(inc, stop - 1), E - 52);
+        c = 64 * h + stop;
+        if (stop == 64 || c >= chunks) continue;
+      }
+      // chunk c alone (its sum leaves the binade, its guess is another binade, or the sum before it is 0)
       const int h = c >> 6, l = c & 63;
       const int e = __builtin_amdgcn_readlane(h ? eg1 : eg0, l);
-      bool took = false;
-      if (run > 0.0 && e == binade(run)) {
-        const int P = __double2loint(run) & 1;  // the parity of run / u
-        const double T = from_lane(h ? (P ? t11 : t10) : (P ? t01 : t00), l);
-        if (__builtin_ldexp(run, 52 - e) + T < 9007199254740992.0) {
-          if (lane == l) {
-            if (h) before1 = run;
-            else before0 = run;
-          }
-          run = run + __builtin_ldexp(T, e - 52);
-          took = true;
-        }
-      }
-      if (!took) {
+      {
+        // the chunk from its slot where it has one (the values read back at the same lane), else from memory
+        const int slot = h ? __builtin_popcountll(cross_lo) + __builtin_popcountll(cross_hi & ((1ull << l) - 1))
+                           : __builtin_popcountll(cross_lo & ((1ull << l) - 1));
+        const bool held = slots && given && ((h ? cross_hi : cross_lo) >> l & 1) && slot < NSLOT;
         float v[SEG];
-        load(c, v);
-        run = chunk_exact(v, run, c * CHUNK, count, cp);
+        LanePack q0, q1;
+        if (held) {
+          const Slot &sl = slots[slot];
+#pragma unroll
+          for (int u = 0; u < SEG / 4; ++u) {
+            const float4 r = sl.v[64 * u + lane];
+            v[4 * u] = r.x;
+            v[4 * u + 1] = r.y;
+            v[4 * u + 2] = r.z;
+            v[4 * u + 3] = r.w;
+          }
+          q0 = sl.r[0][lane];
+          q1 = sl.r[1][lane];
+        } else {
+          load(c, v);
+          if (given) {
+            q0 = given->lanes[c][0][lane];
+            q1 = given->lanes[c][1][lane];
+          }
+        }
+        bool walked = false;
+        if (given && e != NO_GUESS && run > 0.0) {  // from the chunk's lanes at binades e and e + 1
+          const LaneR r0 = unpack(q0), r1 = unpack(q1);
+          double end = 0.0;
+          walked = chunk_walk<2>(v, run, 0, 0.0, e, [&](int k) { return k ? r1 : r0; }, c * CHUNK, count, cp, &end);
+          if (walked) run = end;
+        }
+        if (!walked) run = chunk_exact(v, run, c * CHUNK, count, cp);
       }
+      ++c;
     }
     if (cp) {
 #pragma unroll
@@ -451,13 +605,43 @@ __device__ __forceinline__ float floor_of(float best, const Settings &st) {
   return nucleus ? best - st.temperature * 16.118095f : -3.4028234663852886e38f;
 }
 
-// (1) each block's largest logit
-__global__ __launch_bounds__(VB) void vocab_max_kernel(const float *logits, int32_t n, DrawParts *parts) {
+// (1) each block's largest logit. With window (a replayed step's draw), the call's penalty first, over the window's
+// state[STATE_WINDOW] tokens that fall in the block, each distinct one once (penalize_steps_kernel's), the penalized
+// logits written back (the draw's later launches and the step's end read them)
+__global__ __launch_bounds__(VB) void vocab_max_kernel(const float *logits, int32_t n, DrawParts *parts,
+                                                       float *write_back, const int32_t *window, const int32_t *state,
+                                                       const RunParams *params) {
   __shared__ float wf[VB / 64];
+  __shared__ uint32_t hit[CHUNK / 32];
+  __shared__ int32_t win[RUN_WINDOW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i0 = blockIdx.x * CHUNK + tid * VPT;
   float v[VPT];
 #pragma unroll
   for (int u = 0; u < VPT; ++u) v[u] = logits[min(i0 + u, n - 1)];  // (clamped: a repeat changes no max)
+  if (window) {
+    static_assert(VPT <= 32 && 32 % VPT == 0, "a thread's logits in one word of the block's marks");
+    const int count = state[STATE_WINDOW], b0 = blockIdx.x * CHUNK;
+    if (tid < CHUNK / 32) hit[tid] = 0;
+    if (tid < count) win[tid] = window[tid];
+    __syncthreads();
+    if (tid < count) {
+      const int32_t t = win[tid];
+      bool first = true;
+      for (int j = 0; j < tid; ++j) first = first && win[j] != t;
+      if (first && t >= b0 && t < b0 + CHUNK) atomicOr(&hit[(t - b0) >> 5], 1u << ((t - b0) & 31));
+    }
+    __syncthreads();
+    const uint32_t marks = hit[(tid * VPT) >> 5] >> ((tid * VPT) & 31);
+    if (marks & ((1u << VPT) - 1)) {
+      const float penalty = params->penalty;
+#pragma unroll
+      for (int u = 0; u < VPT; ++u)
+        if ((marks >> u) & 1) {  // (a window token: below n)
+          v[u] = v[u] > 0 ? v[u] / penalty : v[u] * penalty;
+          write_back[i0 + u] = v[u];
+        }
+    }
+  }
   float b = v[0];
 #pragma unroll
   for (int u = 1; u < VPT; ++u) b = wmax(b, v[u]);
@@ -570,24 +754,24 @@ __global__ __launch_bounds__(VB) void vocab_kept_kernel(const float *logits, int
   }
 }
 
-// (4) without a nucleus, each chunk of the total at its guessed binade, a wave a chunk: every value is kept, so block
+// (4) without a nucleus, each chunk of the total at its guessed binade, a block a chunk: every value is kept, so block
 // b's values are the total's chunk b (unless some logits are -inf: then the guesses are only worse), the binade of the
-// sum before it is guessed from the blocks' sums of p, and chunk_guess takes the chunk at that binade; with a nucleus
-// the draw takes the chunks itself
-__global__ __launch_bounds__(64) void vocab_guess_kernel(int32_t n, DrawParts *parts, const float *probs,
-                                                         float temperature, float topp, double random,
-                                                         const RunParams *params, const int32_t *state) {
-  __shared__ float wf[1];
+// sum before it is guessed from the blocks' sums of p, and chunk_guess takes the chunk at that binade (wave 0); the
+// chunk's lanes are kept at that binade (wave 0) and the next (wave 1), for a chunk whose sum crosses into it. Block 0
+// takes the first chunk exactly, since the sum before it is 0: its first lane with a value that is not 0 in order,
+// the lanes after it at GW binades from there at once (a wave a binade), then the walk through them. With a nucleus
+// the draw takes the chunks itself.
+constexpr int GW = 8;  // waves of a guess block
+__global__ __launch_bounds__(64 * GW) void vocab_guess_kernel(int32_t n, DrawParts *parts, const float *probs,
+                                                              float temperature, float topp, double random,
+                                                              const RunParams *params, const int32_t *state) {
+  __shared__ float wf[GW];
+  __shared__ LanePack first[GW][64];
   const Settings st = settings(temperature, topp, random, params, state);
   if (st.topp > 0 && st.topp < 1) return;
   if (!__builtin_isfinite(best_of(parts, gridDim.x, wf))) return;  // (the draw gives SAMPLE_NOT_FINITE)
-  const int b = blockIdx.x, lane = threadIdx.x;
-  double a = 0.0;  // the sum of p before the chunk, in any order
-  for (int i = lane; i < b; i += 64) a += parts->csum[i];
-  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
-  const int e = a > 0.0 ? binade(a) : NO_GUESS;
-  if (lane == 0) parts->guess[b] = e;
-  if (e == NO_GUESS) return;
+  const int b = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (b > 0 && wave >= 2) return;
   float v[SEG];
 #pragma unroll
   for (int u = 0; u < SEG / 4; ++u) {
@@ -597,7 +781,55 @@ __global__ __launch_bounds__(64) void vocab_guess_kernel(int32_t n, DrawParts *p
     v[4 * u + 2] = r.z;
     v[4 * u + 3] = r.w;
   }
-  chunk_guess(v, e, parts->g[b]);
+  if (b == 0) {
+    // lanes below f hold only zeros (their sums before them are 0, as is lane f's); lane f adds its values in order
+    bool some = false;
+#pragma unroll
+    for (int u = 0; u < SEG; ++u) some |= v[u] != 0.0f;
+    const uint64_t m = __ballot(some);  // (the same in every wave)
+    const int f = m ? __builtin_ctzll(m) : 63;
+    double acc = 0.0;
+#pragma unroll
+    for (int u = 0; u < SEG; ++u) {
+      float t = v[u];
+      asm volatile("" : "+v"(t));
+      acc = acc + (double)t;
+    }
+    const double s = from_lane(acc, f);
+    // the binades taken: up to one past the chunk's end (by its sum in any order), from at most GW - 2 below it, or
+    // from lane f's sum; lanes whose sum before them is below those go one at a time
+    double t = 0.0;
+#pragma unroll
+    for (int u = 0; u < SEG; ++u) t += v[u];
+    for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
+    const int E = s > 0.0 ? max(binade(s), binade(t) - (GW - 2)) : 0;
+    if (s > 0.0) first[wave][lane] = pack(lane_r(v, E + wave));
+    __syncthreads();
+    if (wave != 0) return;
+    if (lane == 0) parts->guess[0] = NO_GUESS;
+    double end = s;
+    if (s > 0.0 && f < 63) {
+      if (!chunk_walk<GW>(v, s, f + 1, 0.0, E, [&](int k) { return unpack(first[k][lane]); }, 0, CHUNK,
+                          parts->first_cp, &end))
+        end = chunk_exact(v, 0.0, 0, CHUNK, parts->first_cp);
+    } else if (lane % (CP_BLOCK / SEG) == 0) {
+      parts->first_cp[lane / (CP_BLOCK / SEG)] = 0.0;  // (every lane up to f: the sum before it is 0)
+    }
+    if (lane == 0) parts->first_end = end;
+    return;
+  }
+  double a = 0.0;  // the sum of p before the chunk, in any order
+  for (int i = lane; i < b; i += 64) a += parts->csum[i];
+  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
+  const int e = a > 0.0 ? binade(a) : NO_GUESS;
+  if (wave == 0 && lane == 0) {
+    parts->guess[b] = e;
+    parts->cross[b] = e != NO_GUESS && binade(a + (double)parts->csum[b]) > e;
+  }
+  if (e == NO_GUESS) return;
+  const LaneR r = lane_r(v, e + wave);
+  parts->lanes[b][wave][lane] = pack(r);
+  if (wave == 0) chunk_guess_r(r, parts->g[b]);
 }
 
 // (5) the draw, one block: the largest logit, the count and the largest p from the blocks' parts; the total's chunks
@@ -613,6 +845,7 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   __shared__ int shared_likely;
   __shared__ double shared_total, shared_cutoff;
   __shared__ double checkpoints[CP_MOST];  // the running sum of the kept p before every CP_BLOCK of them
+  __shared__ Slot slots[NSLOT];
   static_assert(STAGE <= 2 * SORT_MOST, "the staging area is the sort's");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float temperature = st.temperature, topp = st.topp;
@@ -646,7 +879,8 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   double total = 0.0;
   static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
   // (without a nucleus the chunks' guesses come from vocab_guess_kernel)
-  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts);
+  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts,
+                    nucleus ? nullptr : slots);
   __syncthreads();  // (the waves' maxima in wf too)
   if (tid == 0) {
     float x = wf[0];
@@ -763,11 +997,31 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   }
 }
 
-// the draw's float64 total alone (the same block's work): *total, and checkpoints[i / CP_BLOCK] = the sum before value i
-__global__ __launch_bounds__(ST) void ordered_sum_kernel(const float *p, int32_t n, double *total, double *checkpoints) {
+// the draw's float64 total alone (the same block's work, with given the chunks' guesses of vocab_guess_kernel): *total,
+// and checkpoints[i / CP_BLOCK] = the sum before value i
+__global__ __launch_bounds__(ST) void ordered_sum_kernel(const float *p, int32_t n, double *total, double *checkpoints,
+                                                         const DrawParts *given) {
   __shared__ SumShared sh;
-  const double t = sum_block(p, n, checkpoints, sh);
+  __shared__ Slot slots[NSLOT];
+  const double t = sum_block(p, n, checkpoints, sh, given, given ? slots : nullptr);
   if (threadIdx.x == 0) *total = t;
+}
+
+// for the total alone taken as the draw without a nucleus takes it: each chunk's sum of p in any order (the guesses'
+// prefix), and a finite largest logit for vocab_guess_kernel
+__global__ __launch_bounds__(64) void chunk_sums_kernel(const float *p, DrawParts *parts) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  float a = 0.0f;
+#pragma unroll
+  for (int u = 0; u < SEG / 4; ++u) {
+    const float4 r = reinterpret_cast<const float4 *>(p + b * CHUNK + lane * SEG)[u];
+    a += (r.x + r.y) + (r.z + r.w);
+  }
+  for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
+  if (lane == 0) {
+    parts->csum[b] = a;
+    parts->bmax[b] = 0.0f;
+  }
 }
 
 __global__ __launch_bounds__(ST) void draw_kernel(int32_t n, const DrawParts *parts, float *probs, int32_t *index,
@@ -776,17 +1030,20 @@ __global__ __launch_bounds__(ST) void draw_kernel(int32_t n, const DrawParts *pa
   draw_block(n, settings(temperature, topp, random, params, state), parts, probs, index, out_token, out_best);
 }
 
-// the five launches of a draw (the settings as values, or with params the call's and the step's from device memory)
+// the five launches of a draw (the settings as values, or with params the call's and the step's from device memory;
+// with window, the call's penalty over it applied to the logits first, in the first launch)
 hipError_t launch_draw(const float *logits, int32_t n, float temperature, float topp, double random,
                        const RunParams *params, const int32_t *state, float *probs, int32_t *index, DrawParts *parts,
-                       int32_t *out_token, float *out_best, hipStream_t s) {
+                       int32_t *out_token, float *out_best, hipStream_t s, float *write_back = nullptr,
+                       const int32_t *window = nullptr) {
   const int blocks = (n + CHUNK - 1) / CHUNK;
-  hipLaunchKernelGGL(vocab_max_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts);
+  hipLaunchKernelGGL(vocab_max_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, write_back, window, state,
+                     params);
   hipLaunchKernelGGL(vocab_count_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, temperature, topp, random,
                      params, state);
   hipLaunchKernelGGL(vocab_kept_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, probs, index, temperature, topp,
                      random, params, state);
-  hipLaunchKernelGGL(vocab_guess_kernel, dim3(blocks), dim3(64), 0, s, n, parts, probs, temperature, topp, random,
+  hipLaunchKernelGGL(vocab_guess_kernel, dim3(blocks), dim3(64 * GW), 0, s, n, parts, probs, temperature, topp, random,
                      params, state);
   hipLaunchKernelGGL(draw_kernel, dim3(1), dim3(ST), 0, s, n, parts, probs, index, out_token, out_best, temperature,
                      topp, random, params, state);
@@ -853,11 +1110,12 @@ __global__ void advance_steps_kernel(int32_t *tokens, int32_t *state, const int3
 
 }  // namespace
 
-hipError_t launch_sample_steps(const float *logits, int32_t n, const RunParams *params, const int32_t *state,
-                               float *probs, int32_t *index, DrawParts *parts, int32_t *out_token, float *out_best,
-                               hipStream_t s) {
+hipError_t launch_sample_steps(float *logits, int32_t n, const RunParams *params, const int32_t *state,
+                               const int32_t *window, float *probs, int32_t *index, DrawParts *parts,
+                               int32_t *out_token, float *out_best, hipStream_t s) {
   if (n < 1 || n > SAMPLE_MOST) return hipErrorInvalidValue;
-  return launch_draw(logits, n, 0.0f, 0.0f, 0.0, params, state, probs, index, parts, out_token, out_best, s);
+  return launch_draw(logits, n, 0.0f, 0.0f, 0.0, params, state, probs, index, parts, out_token, out_best, s,
+                     window ? logits : nullptr, window);
 }
 
 hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
@@ -883,9 +1141,16 @@ hipError_t launch_penalize(float *logits, const int32_t *tokens, int32_t count, 
   return hipGetLastError();
 }
 
-hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *checkpoints, hipStream_t s) {
+hipError_t launch_ordered_sum(const float *p, int32_t n, double *total, double *checkpoints, DrawParts *parts,
+                              hipStream_t s) {
   if (n < 1 || n > SAMPLE_MOST) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(ordered_sum_kernel, dim3(1), dim3(ST), 0, s, p, n, total, checkpoints);
+  if (parts) {
+    const int blocks = (n + CHUNK - 1) / CHUNK;
+    hipLaunchKernelGGL(chunk_sums_kernel, dim3(blocks), dim3(64), 0, s, p, parts);
+    hipLaunchKernelGGL(vocab_guess_kernel, dim3(blocks), dim3(64 * GW), 0, s, n, parts, p, 1.0f, 1.0f, 0.0, nullptr,
+                       nullptr);
+  }
+  hipLaunchKernelGGL(ordered_sum_kernel, dim3(1), dim3(ST), 0, s, p, n, total, checkpoints, parts);
   return hipGetLastError();
 }
 

@@ -101,7 +101,7 @@ def library():
             "hk_matmul": (I32, [P, P, P, P, P, I32, I32, I32, I32, I32, P]),
             "hk_group_sums": (I32, [P, P, P, I32, I32, I32, I32, I32, I32, P]),
             "hk_penalize": (I32, [P, I32, P, I32, F, P]),
-            "hk_ordered_sum": (I32, [P, I32, P, P, P]),
+            "hk_ordered_sum": (I32, [P, I32, I32, P, P, P]),
             "hk_sample": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
             "hk_sample_static": (I32, [P, I32, F, F, ctypes.c_double, P, P]),
             "hk_read_ceiling": (I32, [P, ctypes.c_int64, I32, P, P, P]),

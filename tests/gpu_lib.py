@@ -109,13 +109,14 @@ def penalize(logits, tokens, penalty):
     return x.numpy()
 
 
-def ordered_sum(p):
-    """hk_ordered_sum: the float64 total of p in index order and the running sum before every 256 values"""
+def ordered_sum(p, nucleus):
+    """hk_ordered_sum: the float64 total of p in index order and the running sum before every 256 values (nucleus: as
+    the draw with a nucleus takes them, in one block; else as the draw without one)"""
     x = upload(np.ascontiguousarray(p, dtype=np.float32))
     total = ctypes.c_double(0.0)
     cps = np.zeros((x.shape[0] + 255) // 256, dtype=np.float64)
-    check(package().library().hk_ordered_sum(x.ptr, x.shape[0], ctypes.byref(total), ctypes.c_void_p(cps.ctypes.data),
-                                             None))
+    check(package().library().hk_ordered_sum(x.ptr, x.shape[0], int(nucleus), ctypes.byref(total),
+                                             ctypes.c_void_p(cps.ctypes.data), None))
     del x
     return total.value, cps
 

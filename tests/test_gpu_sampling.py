@@ -80,14 +80,17 @@ def probabilities(kind, n, rng):
     return x.astype(np.float32)
 
 
+@pytest.mark.parametrize("nucleus", [1, 0])
 @pytest.mark.parametrize("kind", ["spread", "tails", "powers", "short", "tiny_first", "leading_zeros", "mantissas"])
 @pytest.mark.parametrize("n", [1, 31, 2049, 40961, 128256, 262144])
-def test_ordered_sum_bits(kind, n):
+def test_ordered_sum_bits(kind, n, nucleus):
     """the draw's float64 total (taken in parallel a binade at a time, kernels/kernel.ts:845-850 adds in order) and its
-    checkpoints equal the running sums of the adds in index order, to the bit"""
+    checkpoints equal the running sums of the adds in index order, to the bit, both as the draw with a nucleus takes
+    them (one block) and as the draw without one does (the chunks guessed over the CUs, the first chunk and the
+    chunks whose sum crosses a binade walked from their lanes at two binades)"""
     rng = np.random.default_rng(n * 7 + len(kind))
     p = probabilities(kind, n, rng)
-    total, cps = gl.ordered_sum(p)
+    total, cps = gl.ordered_sum(p, nucleus)
     want = in_order(p)
     assert np.float64(total).view(np.uint64) == want[-1].view(np.uint64)
     before = np.concatenate([[0.0], want])[np.arange(0, n, 256)]
