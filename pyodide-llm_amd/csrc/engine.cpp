@@ -163,9 +163,9 @@ struct he_engine {
   float *step_values = nullptr;                       // their logits
   int32_t *host_ids = nullptr, *host_state = nullptr;  // pinned
   float *host_values = nullptr;                       // pinned
-  // the captured step graphs by kind (STEP_GREEDY, STEP_PENALIZED, STEP_SAMPLED, STEP_SAMPLED | STEP_PENALIZED)
-  hipGraphExec_t graph[4] = {};
-  bool graph_tried[4] = {};
+  // the captured step graphs by kind (STEP_GREEDY or STEP_SAMPLED, with STEP_WHOLE and STEP_PENALIZED)
+  hipGraphExec_t graph[8] = {};
+  bool graph_tried[8] = {};
   // a call's settings (device, and its pinned host copy); the logits of the step that ended the last call, where the
   // round's later replays overwrote its own
   RunParams *run_params = nullptr, *host_params = nullptr;
@@ -218,7 +218,7 @@ constexpr int32_t STOP_ROUND = 16;         // the same where a stop token may en
 constexpr int32_t REPETITION_WINDOW = RUN_WINDOW;  // the penalty's latest tokens (public/llama2_numpy.py:545)
 static_assert(STEPS_A_ROUND <= RUN_RANDOMS, "a random number for every step of a round");
 // the kinds of replayed step graph
-enum { STEP_GREEDY = 0, STEP_PENALIZED = 1, STEP_SAMPLED = 2 };
+enum { STEP_GREEDY = 0, STEP_PENALIZED = 1, STEP_SAMPLED = 2, STEP_WHOLE = 4 };  // (WHOLE: sampled, no nucleus)
 
 void destroy(he_engine *e) {
   if (!e) return;
@@ -951,8 +951,8 @@ void build_graph(he_engine *e, int kind) {
       if (penalized && !drawn) le = launch_penalize_steps(e->logits, e->window, e->state, e->run_params, e->stream);
       if (le == hipSuccess)
         le = drawn ? launch_sample_steps(e->logits, n, e->run_params, e->state, penalized ? e->window : nullptr,
-                                         e->sample_probs, e->sample_index, e->sample_parts, e->sample_token,
-                                         e->sample_best, e->stream)
+                                         (kind & STEP_WHOLE) != 0, e->sample_probs, e->sample_index,
+                                         e->sample_parts, e->sample_token, e->sample_best, e->stream)
                    : launch_argmax(e->best_i, e->best_v, e->logits, n, e->amax_v, e->amax_i, e->stream);
       if (le == hipSuccess)
         le = launch_step_end(e->logits, n, e->kept_logits, e->tokens, e->state, drawn ? e->sample_token : e->best_i,
@@ -1050,7 +1050,9 @@ int32_t he_generate_many(he_engine *e, int32_t token, int32_t pos, const int32_t
   if (n_stops > RUN_STOPS_MOST)
     return sampled_steps(e, token, pos, history, n_history, count, temperature, topp, penalty, randoms, is_stop, ids,
                          n_ids);
-  const int kind = (temperature > 0.0f ? STEP_SAMPLED : STEP_GREEDY) | (penalty != 1.0f ? STEP_PENALIZED : 0);
+  const bool nucleus = topp > 0.0f && topp < 1.0f;  // (as the draw decides it on the device)
+  const int kind = (temperature > 0.0f ? (nucleus ? STEP_SAMPLED : STEP_SAMPLED | STEP_WHOLE) : STEP_GREEDY) |
+                   (penalty != 1.0f ? STEP_PENALIZED : 0);
   // the penalty's window: the latest of history, then the tokens this call chooses
   std::vector<int32_t> window(history + std::max(0, n_history - REPETITION_WINDOW), history + n_history);
   int32_t done = 0;

@@ -259,9 +259,10 @@ struct RunParams {
 };
 // a step's draw (as launch_sample) with the call's temperature and top-p and the round's random number of the step;
 // with window, the call's penalty over the window's state[STATE_WINDOW] tokens first (launch_penalize_steps's, in the
-// draw's first launch: the logits penalized in place)
+// draw's first launch: the logits penalized in place); whole: the call's top-p is known to take no nucleus (one launch
+// fewer)
 hipError_t launch_sample_steps(float *logits, int32_t n, const RunParams *params, const int32_t *state,
-                               const int32_t *window, float *probs, int32_t *index, DrawParts *parts,
+                               const int32_t *window, bool whole, float *probs, int32_t *index, DrawParts *parts,
                                int32_t *out_token, float *out_best, hipStream_t s);
 // the call's penalty over the window's state[STATE_WINDOW] tokens
 hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,

@@ -607,13 +607,17 @@ __device__ __forceinline__ float floor_of(float best, const Settings &st) {
 
 // (1) each block's largest logit. With window (a replayed step's draw), the call's penalty first, over the window's
 // state[STATE_WINDOW] tokens that fall in the block, each distinct one once (penalize_steps_kernel's), the penalized
-// logits written back (the draw's later launches and the step's end read them)
+// logits written back (the draw's later launches and the step's end read them). With counts (a draw that is known to
+// have no nucleus, whose floor keeps every logit above -FLT_MAX whatever the largest), each block's count of kept
+// logits too, in place of vocab_count_kernel's launch.
 __global__ __launch_bounds__(VB) void vocab_max_kernel(const float *logits, int32_t n, DrawParts *parts,
                                                        float *write_back, const int32_t *window, const int32_t *state,
-                                                       const RunParams *params) {
+                                                       const RunParams *params, int32_t counts) {
   __shared__ float wf[VB / 64];
   __shared__ uint32_t hit[CHUNK / 32];
   __shared__ int32_t win[RUN_WINDOW];
+  __shared__ int wi[VB / 64];
+  __shared__ int total;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, i0 = blockIdx.x * CHUNK + tid * VPT;
   float v[VPT];
 #pragma unroll
@@ -641,6 +645,14 @@ __global__ __launch_bounds__(VB) void vocab_max_kernel(const float *logits, int3
           write_back[i0 + u] = v[u];
         }
     }
+  }
+  if (counts) {
+    const float floor_ = floor_of(0.0f, Settings{1.0f, 1.0f, 0.0});  // (no nucleus: the same for any largest logit)
+    int c = 0;
+#pragma unroll
+    for (int u = 0; u < VPT; ++u) c += i0 + u < n && v[u] >= floor_;
+    block_scan<VB>(c, wi, &total);
+    if (tid == 0) parts->bcount[blockIdx.x] = total;
   }
   float b = v[0];
 #pragma unroll
@@ -1035,12 +1047,13 @@ __global__ __launch_bounds__(ST) void draw_kernel(int32_t n, const DrawParts *pa
 hipError_t launch_draw(const float *logits, int32_t n, float temperature, float topp, double random,
                        const RunParams *params, const int32_t *state, float *probs, int32_t *index, DrawParts *parts,
                        int32_t *out_token, float *out_best, hipStream_t s, float *write_back = nullptr,
-                       const int32_t *window = nullptr) {
+                       const int32_t *window = nullptr, bool whole = false) {
   const int blocks = (n + CHUNK - 1) / CHUNK;
   hipLaunchKernelGGL(vocab_max_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, write_back, window, state,
-                     params);
-  hipLaunchKernelGGL(vocab_count_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, temperature, topp, random,
-                     params, state);
+                     params, (int32_t)whole);
+  if (!whole)
+    hipLaunchKernelGGL(vocab_count_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, temperature, topp, random,
+                       params, state);
   hipLaunchKernelGGL(vocab_kept_kernel, dim3(blocks), dim3(VB), 0, s, logits, n, parts, probs, index, temperature, topp,
                      random, params, state);
   hipLaunchKernelGGL(vocab_guess_kernel, dim3(blocks), dim3(64 * GW), 0, s, n, parts, probs, temperature, topp, random,
@@ -1111,11 +1124,11 @@ __global__ void advance_steps_kernel(int32_t *tokens, int32_t *state, const int3
 }  // namespace
 
 hipError_t launch_sample_steps(float *logits, int32_t n, const RunParams *params, const int32_t *state,
-                               const int32_t *window, float *probs, int32_t *index, DrawParts *parts,
+                               const int32_t *window, bool whole, float *probs, int32_t *index, DrawParts *parts,
                                int32_t *out_token, float *out_best, hipStream_t s) {
   if (n < 1 || n > SAMPLE_MOST) return hipErrorInvalidValue;
   return launch_draw(logits, n, 0.0f, 0.0f, 0.0, params, state, probs, index, parts, out_token, out_best, s,
-                     window ? logits : nullptr, window);
+                     window ? logits : nullptr, window, whole);
 }
 
 hipError_t launch_penalize_steps(float *logits, const int32_t *window, const int32_t *state, const RunParams *params,
