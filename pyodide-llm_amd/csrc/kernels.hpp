@@ -222,8 +222,8 @@ struct LanePack {
 };
 // what the draw's blocks over the vocabulary (SAMPLE_CHUNK logits each) leave for the draw: each block's largest
 // logit, its count of kept logits, its largest p and its sum of p; and without a nucleus, each chunk of the total at
-// its guessed binade (guess: the binade, or none), its lanes at that binade and the next, whether its sum probably
-// crosses into the next (cross), and the first chunk's end and checkpoints
+// its guessed binade (guess: the binade, or none), its lanes at that binade and the next, and the first chunk's end and
+// checkpoints
 struct DrawParts {
   float bmax[SAMPLE_MOST / SAMPLE_CHUNK];
   int32_t bcount[SAMPLE_MOST / SAMPLE_CHUNK];
@@ -232,7 +232,6 @@ struct DrawParts {
   int32_t guess[SAMPLE_MOST / SAMPLE_CHUNK];
   ChunkGuess g[SAMPLE_MOST / SAMPLE_CHUNK];
   LanePack lanes[SAMPLE_MOST / SAMPLE_CHUNK][2][64];
-  int32_t cross[SAMPLE_MOST / SAMPLE_CHUNK];
   double first_end;
   double first_cp[SAMPLE_CHUNK / SAMPLE_CHECKPOINT];
 };

@@ -253,6 +253,20 @@ __device__ __forceinline__ double chunk_exact(const float (&v)[SEG], double run,
   return run;
 }
 
+// lane from's values added in order to run (every lane adds its own; lane from's sum is kept): the sum after them, and
+// lane from's pre (its sum before them) set to run
+__device__ __forceinline__ double lane_in_order(const float (&v)[SEG], double run, int from, double &pre) {
+  if ((int)(threadIdx.x & 63) == from) pre = run;
+  double acc = run;
+#pragma unroll
+  for (int u = 0; u < SEG; ++u) {
+    float t = v[u];
+    asm volatile("" : "+v"(t));
+    acc = acc + (double)t;
+  }
+  return from_lane(acc, from);
+}
+
 // One chunk (values b.., lane L's 32 at b + 32 L) exactly from run > 0 at lane from (the lanes below it done, their
 // sums before them in pre), from its lanes already taken at binades E .. E + W - 1 (at(k): binade E + k): each run of
 // lanes that keeps the sum in one binade in parallel, as chunk_exact, and each lane that takes it out of its binade by
@@ -266,16 +280,8 @@ __device__ __forceinline__ bool chunk_walk(const float (&v)[SEG], double run, in
   while (from < 64) {
     const int k = binade(run) - E;
     if (k >= W) return false;  // (uniform)
-    if (k < 0) {  // lane from's values in order (every lane adds its own; lane from's sum is kept)
-      if (lane == from) pre = run;
-      double acc = run;
-#pragma unroll
-      for (int u = 0; u < SEG; ++u) {
-        float t = v[u];
-        asm volatile("" : "+v"(t));
-        acc = acc + (double)t;
-      }
-      run = from_lane(acc, from);
+    if (k < 0) {
+      run = lane_in_order(v, run, from, pre);
       ++from;
       continue;
     }
@@ -304,17 +310,22 @@ __device__ __forceinline__ bool chunk_walk(const float (&v)[SEG], double run, in
 
 // one chunk taken at binade e, for either parity of the sum before it: its sum of r and its lanes' sums of r before
 // them (every lane of the wave calls; lanes 0, 8, .., 56 and 63 write)
-__device__ __forceinline__ void chunk_guess_r(const LaneR &r, ChunkGuess &g) {
+__device__ __forceinline__ void chunk_guess_s(double inc0, double inc1, ChunkGuess &g) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int P = 0; P < 2; ++P) {
-    const double inc = lanes_upto(lane_t(r, 0, P));
+    const double inc = P ? inc1 : inc0;
     const double excl = lane_below(inc);
     if (lane % (CP_BLOCK / SEG) == 0) g.pre[P][lane / (CP_BLOCK / SEG)] = excl;
     if (lane == 63) g.t[P] = inc;
   }
 }
-__device__ __forceinline__ void chunk_guess(const float (&v)[SEG], int e, ChunkGuess &g) { chunk_guess_r(lane_r(v, e), g); }
+// the lanes' sums of r in order from lane 0, for parity P there
+__device__ __forceinline__ double scan_from0(const LaneR &r, int P) { return lanes_upto(lane_t(r, 0, P)); }
+__device__ __forceinline__ void chunk_guess(const float (&v)[SEG], int e, ChunkGuess &g) {
+  const LaneR r = lane_r(v, e);
+  chunk_guess_s(scan_from0(r, 0), scan_from0(r, 1), g);
+}
 
 // what the block's waves leave for the in-order pass: each chunk's guessed binade (NO_GUESS: none) and, at it, the
 // chunk's sum of r and its lanes' (0, 8, .., 56) sums of r before them, for either parity of the sum before the chunk
@@ -326,23 +337,6 @@ struct SumShared {
   int guess[MOST_CHUNKS];
   ChunkGuess g[MOST_CHUNKS];
 };
-// a chunk whose sum probably crosses a binade, held in LDS for the in-order pass: its values (float4 u of lane L at
-// v[64 u + L]) and its lanes at two binades
-constexpr int NSLOT = 8;
-struct Slot {
-  float4 v[SEG / 4 * 64];
-  LanePack r[2][64];
-};
-// the j-th set bit of the 128-bit mask (lo, hi), 128 if none
-__device__ __forceinline__ int nth_bit(uint64_t lo, uint64_t hi, int j) {
-  const int below = __builtin_popcountll(lo);
-  uint64_t m = j < below ? lo : hi;
-  int k = j < below ? j : j - below;
-  if (k >= __builtin_popcountll(m)) return 128;
-  for (; k > 0; --k) m &= m - 1;
-  return (j < below ? 0 : 64) + __builtin_ctzll(m);
-}
-
 // p[0] + p[1] + ... + p[count-1] in float64 (each p widened exactly), with the bits of the adds in index order, by the
 // block (all of it calls): chunks of 2048, lane L of a wave holding p[b + 32 L .. b + 32 L + 31] (+0.0 past count,
 // which changes no sum). (1) Every chunk's sum in any order, and from them the binade the running sum probably has
@@ -354,7 +348,7 @@ __device__ __forceinline__ int nth_bit(uint64_t lo, uint64_t hi, int j) {
 // (vocab_guess_kernel's). Wave 0 returns the total. (p: 16-byte aligned,
 // count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
 __device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh,
-                                            const DrawParts *given = nullptr, Slot *slots = nullptr) {
+                                            const DrawParts *given = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const int chunks = (count + CHUNK - 1) / CHUNK;
   auto load = [&](int c, float(&v)[SEG]) {
@@ -367,25 +361,10 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       v[4 * u + 3] = r.w;
     }
   };
-  // with given: the chunks that probably cross a binade (the first NSLOT of them in slots, one a wave from wave 1)
-  uint64_t cross_lo = 0, cross_hi = 0;
   if (given) {  // steps (1) and (2) done by other blocks
     for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
       sh.guess[c] = given->guess[c];
       sh.g[c] = given->g[c];
-    }
-    if (slots && wave <= NSLOT) {
-      cross_lo = __ballot(lane > 0 && lane < chunks && given->cross[lane]);
-      cross_hi = __ballot(lane + 64 < chunks && given->cross[lane + 64]);
-      const int c = wave > 0 ? nth_bit(cross_lo, cross_hi, wave - 1) : 128;
-      if (c < chunks) {
-        Slot &sl = slots[wave - 1];
-#pragma unroll
-        for (int u = 0; u < SEG / 4; ++u)
-          sl.v[64 * u + lane] = reinterpret_cast<const float4 *>(p + c * CHUNK + lane * SEG)[u];
-        sl.r[0][lane] = given->lanes[c][0][lane];
-        sl.r[1][lane] = given->lanes[c][1][lane];
-      }
     }
   } else {
     for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
@@ -475,34 +454,11 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       const int h = c >> 6, l = c & 63;
       const int e = __builtin_amdgcn_readlane(h ? eg1 : eg0, l);
       {
-        // the chunk from its slot where it has one (the values read back at the same lane), else from memory
-        const int slot = h ? __builtin_popcountll(cross_lo) + __builtin_popcountll(cross_hi & ((1ull << l) - 1))
-                           : __builtin_popcountll(cross_lo & ((1ull << l) - 1));
-        const bool held = slots && given && ((h ? cross_hi : cross_lo) >> l & 1) && slot < NSLOT;
         float v[SEG];
-        LanePack q0, q1;
-        if (held) {
-          const Slot &sl = slots[slot];
-#pragma unroll
-          for (int u = 0; u < SEG / 4; ++u) {
-            const float4 r = sl.v[64 * u + lane];
-            v[4 * u] = r.x;
-            v[4 * u + 1] = r.y;
-            v[4 * u + 2] = r.z;
-            v[4 * u + 3] = r.w;
-          }
-          q0 = sl.r[0][lane];
-          q1 = sl.r[1][lane];
-        } else {
-          load(c, v);
-          if (given) {
-            q0 = given->lanes[c][0][lane];
-            q1 = given->lanes[c][1][lane];
-          }
-        }
+        load(c, v);
         bool walked = false;
         if (given && e != NO_GUESS && run > 0.0) {  // from the chunk's lanes at binades e and e + 1
-          const LaneR r0 = unpack(q0), r1 = unpack(q1);
+          const LaneR r0 = unpack(given->lanes[c][0][lane]), r1 = unpack(given->lanes[c][1][lane]);
           double end = 0.0;
           walked = chunk_walk<2>(v, run, 0, 0.0, e, [&](int k) { return k ? r1 : r0; }, c * CHUNK, count, cp, &end);
           if (walked) run = end;
@@ -770,15 +726,16 @@ __global__ __launch_bounds__(VB) void vocab_kept_kernel(const float *logits, int
 // b's values are the total's chunk b (unless some logits are -inf: then the guesses are only worse), the binade of the
 // sum before it is guessed from the blocks' sums of p, and chunk_guess takes the chunk at that binade (wave 0); the
 // chunk's lanes are kept at that binade (wave 0) and the next (wave 1), for a chunk whose sum crosses into it. Block 0
-// takes the first chunk exactly, since the sum before it is 0: its first lane with a value that is not 0 in order,
-// the lanes after it at GW binades from there at once (a wave a binade), then the walk through them. With a nucleus
-// the draw takes the chunks itself.
+// takes the first chunk exactly, since the sum before it is 0 (below). With a nucleus the draw takes the chunks
+// itself.
 constexpr int GW = 8;  // waves of a guess block
+constexpr int NB = 5;  // binades block 0 takes the first chunk's lanes at (waves 1..NB)
+static_assert(NB < GW, "a wave for each binade and one that adds in order");
 __global__ __launch_bounds__(64 * GW) void vocab_guess_kernel(int32_t n, DrawParts *parts, const float *probs,
                                                               float temperature, float topp, double random,
                                                               const RunParams *params, const int32_t *state) {
   __shared__ float wf[GW];
-  __shared__ LanePack first[GW][64];
+  __shared__ LanePack first[NB][64];
   const Settings st = settings(temperature, topp, random, params, state);
   if (st.topp > 0 && st.topp < 1) return;
   if (!__builtin_isfinite(best_of(parts, gridDim.x, wf))) return;  // (the draw gives SAMPLE_NOT_FINITE)
@@ -794,39 +751,37 @@ __global__ __launch_bounds__(64 * GW) void vocab_guess_kernel(int32_t n, DrawPar
     v[4 * u + 3] = r.w;
   }
   if (b == 0) {
-    // lanes below f hold only zeros (their sums before them are 0, as is lane f's); lane f adds its values in order
-    bool some = false;
+    // the first chunk, from 0: its sum in any order (t) puts its end at about binade Ef. Waves 1..NB take its lanes at
+    // binades Ef - NB + 2 .. Ef + 1 while wave 0 adds lanes in order, from the first that holds a value other than 0
+    // (the lanes below it sum to 0), up to the first whose sum before it reaches the lowest of those binades (where
+    // the binades change every lane or two, in order is the faster); then wave 0 walks the rest through them.
+    float tf = 0.0f;
 #pragma unroll
-    for (int u = 0; u < SEG; ++u) some |= v[u] != 0.0f;
-    const uint64_t m = __ballot(some);  // (the same in every wave)
-    const int f = m ? __builtin_ctzll(m) : 63;
-    double acc = 0.0;
-#pragma unroll
-    for (int u = 0; u < SEG; ++u) {
-      float t = v[u];
-      asm volatile("" : "+v"(t));
-      acc = acc + (double)t;
-    }
-    const double s = from_lane(acc, f);
-    // the binades taken: up to one past the chunk's end (by its sum in any order), from at most GW - 2 below it, or
-    // from lane f's sum; lanes whose sum before them is below those go one at a time
-    double t = 0.0;
-#pragma unroll
-    for (int u = 0; u < SEG; ++u) t += v[u];
+    for (int u = 0; u < SEG; ++u) tf += v[u];
+    double t = tf;
     for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
-    const int E = s > 0.0 ? max(binade(s), binade(t) - (GW - 2)) : 0;
-    if (s > 0.0) first[wave][lane] = pack(lane_r(v, E + wave));
+    const int E = t > 0.0 ? binade(t) - (NB - 2) : 0;
+    if (t > 0.0 && wave >= 1 && wave <= NB) first[wave - 1][lane] = pack(lane_r(v, E + wave - 1));
+    double run = 0.0, pre = 0.0;
+    int from = 64;
+    if (wave == 0) {
+      bool some = false;
+#pragma unroll
+      for (int u = 0; u < SEG; ++u) some |= v[u] != 0.0f;
+      const uint64_t m = __ballot(some);
+      from = m ? __builtin_ctzll(m) : 64;
+      while (from < 64 && (run == 0.0 || binade(run) < E)) {
+        run = lane_in_order(v, run, from, pre);
+        ++from;
+      }
+    }
     __syncthreads();
     if (wave != 0) return;
     if (lane == 0) parts->guess[0] = NO_GUESS;
-    double end = s;
-    if (s > 0.0 && f < 63) {
-      if (!chunk_walk<GW>(v, s, f + 1, 0.0, E, [&](int k) { return unpack(first[k][lane]); }, 0, CHUNK,
-                          parts->first_cp, &end))
-        end = chunk_exact(v, 0.0, 0, CHUNK, parts->first_cp);
-    } else if (lane % (CP_BLOCK / SEG) == 0) {
-      parts->first_cp[lane / (CP_BLOCK / SEG)] = 0.0;  // (every lane up to f: the sum before it is 0)
-    }
+    double end = 0.0;
+    if (!chunk_walk<NB>(v, run, from, pre, E, [&](int k) { return unpack(first[k][lane]); }, 0, CHUNK,
+                        parts->first_cp, &end))
+      end = chunk_exact(v, 0.0, 0, CHUNK, parts->first_cp);
     if (lane == 0) parts->first_end = end;
     return;
   }
@@ -834,14 +789,11 @@ __global__ __launch_bounds__(64 * GW) void vocab_guess_kernel(int32_t n, DrawPar
   for (int i = lane; i < b; i += 64) a += parts->csum[i];
   for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
   const int e = a > 0.0 ? binade(a) : NO_GUESS;
-  if (wave == 0 && lane == 0) {
-    parts->guess[b] = e;
-    parts->cross[b] = e != NO_GUESS && binade(a + (double)parts->csum[b]) > e;
-  }
+  if (wave == 0 && lane == 0) parts->guess[b] = e;
   if (e == NO_GUESS) return;
   const LaneR r = lane_r(v, e + wave);
   parts->lanes[b][wave][lane] = pack(r);
-  if (wave == 0) chunk_guess_r(r, parts->g[b]);
+  if (wave == 0) chunk_guess_s(scan_from0(r, 0), scan_from0(r, 1), parts->g[b]);
 }
 
 // (5) the draw, one block: the largest logit, the count and the largest p from the blocks' parts; the total's chunks
@@ -857,7 +809,6 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   __shared__ int shared_likely;
   __shared__ double shared_total, shared_cutoff;
   __shared__ double checkpoints[CP_MOST];  // the running sum of the kept p before every CP_BLOCK of them
-  __shared__ Slot slots[NSLOT];
   static_assert(STAGE <= 2 * SORT_MOST, "the staging area is the sort's");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float temperature = st.temperature, topp = st.topp;
@@ -891,8 +842,7 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   double total = 0.0;
   static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
   // (without a nucleus the chunks' guesses come from vocab_guess_kernel)
-  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts,
-                    nucleus ? nullptr : slots);
+  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts);
   __syncthreads();  // (the waves' maxima in wf too)
   if (tid == 0) {
     float x = wf[0];
@@ -1014,8 +964,7 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
 __global__ __launch_bounds__(ST) void ordered_sum_kernel(const float *p, int32_t n, double *total, double *checkpoints,
                                                          const DrawParts *given) {
   __shared__ SumShared sh;
-  __shared__ Slot slots[NSLOT];
-  const double t = sum_block(p, n, checkpoints, sh, given, given ? slots : nullptr);
+  const double t = sum_block(p, n, checkpoints, sh, given);
   if (threadIdx.x == 0) *total = t;
 }
 
