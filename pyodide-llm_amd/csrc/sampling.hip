@@ -348,7 +348,7 @@ struct SumShared {
 // (vocab_guess_kernel's). Wave 0 returns the total. (p: 16-byte aligned,
 // count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
 __device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh,
-                                            const DrawParts *given = nullptr) {
+                                            const DrawParts *given = nullptr, bool copied = false) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   const int chunks = (count + CHUNK - 1) / CHUNK;
   auto load = [&](int c, float(&v)[SEG]) {
@@ -361,11 +361,12 @@ __device__ __forceinline__ double sum_block(const float *p, int count, double *c
       v[4 * u + 3] = r.w;
     }
   };
-  if (given) {  // steps (1) and (2) done by other blocks
-    for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
-      sh.guess[c] = given->guess[c];
-      sh.g[c] = given->g[c];
-    }
+  if (given) {  // steps (1) and (2) done by other blocks (copied: their guesses already in sh)
+    if (!copied)
+      for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+        sh.guess[c] = given->guess[c];
+        sh.g[c] = given->g[c];
+      }
   } else {
     for (int c = wave; c < chunks; c += 2 * waves) {  // two chunks at a time, so that their loads fly together
       const int d = min(c + waves, chunks - 1);  // (past the last chunk: the last again, its sum written twice)
@@ -803,9 +804,7 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   __shared__ float4 area[SORT_MOST / 2];  // the sort's probabilities then tokens; the total's guesses
   float *const sp = reinterpret_cast<float *>(area);
   int *const si = reinterpret_cast<int *>(area) + SORT_MOST;
-  __shared__ float wf[ST / 64];
   __shared__ int wi[ST / 64];
-  __shared__ float shared_top;
   __shared__ int shared_likely;
   __shared__ double shared_total, shared_cutoff;
   __shared__ double checkpoints[CP_MOST];  // the running sum of the kept p before every CP_BLOCK of them
@@ -814,7 +813,29 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   const float temperature = st.temperature, topp = st.topp;
   const double random = st.random;
   const int blocks = (n + CHUNK - 1) / CHUNK;
-  const float best = best_of(parts, blocks, wf);
+  const bool nucleus = topp > 0 && topp < 1;
+  SumShared &sh = *reinterpret_cast<SumShared *>(area);
+  static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
+  // every read of the vocabulary launches' parts at once: each wave all of the blocks' largest logits, kept counts
+  // and largest p (so that every wave has their reductions, with no barrier), and without a nucleus the block the
+  // chunks' guesses into LDS (for sum_block, whose barrier they meet)
+  float best = parts->bmax[0], top = 0.0f;
+  int c = 0;
+  for (int i = lane; i < blocks; i += 64) {
+    best = wmax(best, parts->bmax[i]);
+    c += parts->bcount[i];
+    top = __builtin_fmaxf(top, parts->btop[i]);
+  }
+  if (!nucleus)
+    for (int i = tid; i < blocks; i += ST) {
+      sh.guess[i] = parts->guess[i];
+      sh.g[i] = parts->g[i];
+    }
+  for (int o = 32; o >= 1; o >>= 1) {
+    best = wmax(best, __shfl_xor(best, o, 64));
+    c += __shfl_xor(c, o, 64);
+    top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
+  }
   if (!__builtin_isfinite(best)) {
     if (tid == 0) {
       *out_token = SAMPLE_NOT_FINITE;
@@ -822,61 +843,77 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
     }
     return;  // the whole block
   }
-  const bool nucleus = topp > 0 && topp < 1;
   const uint64_t below = (1ull << lane) - 1;
-  int c = 0;
-  float top = 0.0f;
-  for (int i = lane; i < blocks; i += 64) {  // (every wave all of them)
-    c += parts->bcount[i];
-    top = __builtin_fmaxf(top, parts->btop[i]);
-  }
-  for (int o = 32; o >= 1; o >>= 1) {
-    c += __shfl_xor(c, o, 64);
-    top = __builtin_fmaxf(top, __shfl_xor(top, o, 64));
-  }
   const int count = __builtin_amdgcn_readfirstlane(c);  // (probs is +0.0 from count to its chunk's end)
-  if (lane == 0) wf[wave] = top;
-  __syncthreads();
 
-  // total: float64, in order, by wave 0 from registers
-  double total = 0.0;
-  static_assert(sizeof(SumShared) <= sizeof(float4) * (SORT_MOST / 2), "the total's LDS fits the sort's area");
-  // (without a nucleus the chunks' guesses come from vocab_guess_kernel)
-  total = sum_block(probs, count, checkpoints, *reinterpret_cast<SumShared *>(area), nucleus ? nullptr : parts);
-  __syncthreads();  // (the waves' maxima in wf too)
-  if (tid == 0) {
-    float x = wf[0];
-    for (int w = 1; w < ST / 64; ++w) x = __builtin_fmaxf(x, wf[w]);
-    shared_top = x;
-    shared_total = total;
-  }
+  // total: float64, in order, by wave 0 from registers (without a nucleus from vocab_guess_kernel's guesses)
+  double total = sum_block(probs, count, checkpoints, sh, nucleus ? nullptr : parts, true);
+  if (tid == 0) shared_total = total;
   __syncthreads();
   total = shared_total;
 
   if (!nucleus) {
     // the running sum in index order up to the first that passes random * total: the block of CP_BLOCK where it
     // passes, from the checkpoints (the sum never decreases: every p >= 0), then that block's adds again from its
-    // checkpoint (the same adds, the same bits)
-    if (tid == 0) {
+    // checkpoint (the same adds, the same bits), by wave 0: the block's values and token indices read at once (a
+    // float4 and an int4 a lane) into LDS (the guesses' area, done with), then lane 0's adds, 32 at a time from
+    // registers, the first index past target kept by a select
+    static_assert(CP_BLOCK == 64 * 4, "a checkpoint block is a float4 a lane");
+    if (wave == 0) {
       const double target = random * total;
       const int blocks = (count + CP_BLOCK - 1) / CP_BLOCK;
       // the first block b whose end (the sum before block b + 1, or the total) passes target, blocks if none: the ends
-      // never decrease, so by halving
-      int b = 0, hi = blocks;
-      while (b < hi) {
-        const int mid = (b + hi) / 2;
-        if ((mid + 1 < blocks ? checkpoints[mid + 1] : total) <= target) b = mid + 1;
-        else hi = mid;
+      // never decrease, so the lanes look at every 16th end, then at the 16 of the first group that passes
+      static_assert(CP_MOST <= 64 * 16, "two looks over the checkpoints");
+      auto passes = [&](int m) { return (m + 1 < blocks ? checkpoints[m + 1] : total) > target; };
+      const uint64_t g16 = __ballot(16 * lane < blocks && passes(min(16 * lane + 15, blocks - 1)));
+      int b = blocks;
+      if (g16) {
+        const int g = __builtin_ctzll(g16);
+        const uint64_t one = __ballot(lane < 16 && 16 * g + lane < blocks && passes(16 * g + lane));
+        b = 16 * g + __builtin_ctzll(one);  // (the group's last passes: one is not 0)
       }
       int token = -1;
       if (b < blocks) {
-        double reached = 0.0;
-        const int j = first_past(probs + b * CP_BLOCK, min(CP_BLOCK, count - b * CP_BLOCK), checkpoints[b], target,
-                                 &reached);
-        if (j >= 0) token = b * CP_BLOCK + j;
+        const int len = min(CP_BLOCK, count - b * CP_BLOCK);
+        float4 *const vals = area;  // (probs holds whole chunks: the block's 256 are there)
+        int4 *const ids = reinterpret_cast<int4 *>(area + 64);
+        vals[lane] = reinterpret_cast<const float4 *>(probs + b * CP_BLOCK)[lane];
+        const int i0 = b * CP_BLOCK + 4 * lane;  // (index holds n: clamped past the count, those never taken)
+        ids[lane] = make_int4(index[min(i0, count - 1)], index[min(i0 + 1, count - 1)], index[min(i0 + 2, count - 1)],
+                              index[min(i0 + 3, count - 1)]);
+        wave_sync_lds();
+        if (lane == 0) {
+          // 32 adds at a time with one look at the end; the 32 in which the sum passes target again, one at a time
+          const float *const x = reinterpret_cast<const float *>(vals);
+          double acc = checkpoints[b];
+          int j = -1;
+          for (int q = 0; q * 32 < len; ++q) {
+            float4 a[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = vals[q * 8 + u];
+            double t = acc;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t = (((t + (double)a[u].x) + (double)a[u].y) + (double)a[u].z) + (double)a[u].w;
+            if (t > target) {  // (every p >= 0: the sum passes within these 32)
+              for (int i = q * 32; i < min(q * 32 + 32, len); ++i) {
+                acc += (double)x[i];
+                if (acc > target) {
+                  j = i;
+                  break;
+                }
+              }
+              break;
+            }
+            acc = t;
+          }
+          if (j >= 0) token = reinterpret_cast<const int *>(ids)[j];
+        }
       }
-      *out_token = index[token >= 0 ? token : count - 1];
-      *out_best = best;
+      if (lane == 0) {
+        *out_token = token >= 0 ? token : index[count - 1];
+        *out_best = best;
+      }
     }
     return;
   }
@@ -884,8 +921,7 @@ __device__ __forceinline__ void draw_block(int32_t n, const Settings &st, const 
   // the nucleus: the kept p >= cutoff, sorted from the most probable
   if (tid == 0) {
     const double ceiling = (1.0 - (double)topp) / (double)(count > 1 ? count - 1 : 1) * total;
-    const double top = (double)shared_top;
-    shared_cutoff = ceiling < top ? ceiling : top;
+    shared_cutoff = ceiling < (double)top ? ceiling : (double)top;
   }
   __syncthreads();
   const double cutoff = shared_cutoff;
