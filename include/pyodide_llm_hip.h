@@ -246,7 +246,8 @@ int32_t hk_sample(const void *logits, int32_t n, float temperature, float topp, 
 
 /* No counterpart in the reference: hk_sample for callers that cannot allocate device memory (serving loops and
  * harnesses that forbid hipMalloc). The same draw as hk_sample, token for token, with the
- * sampler's scratch (n probabilities and n token indices, the token and the largest logit) in a static device array of
+ * sampler's scratch (n probabilities and n token indices, the token and the largest logit, the vocabulary launches'
+ * parts for the draw) in a static device array of
  * the library, which every GPU it runs on holds until the process ends; n <= HK_SAMPLE_STATIC_MOST, else HE_E_ARG.
  * It allocates nothing. Every call on one GPU uses that GPU's one array: calls that overlap on one GPU (two streams,
  * two threads) race, and the caller must order them. Blocks until done: it copies the token to the host and waits
