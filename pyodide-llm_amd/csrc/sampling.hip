@@ -341,12 +341,14 @@ struct SumShared {
 // block (all of it calls): chunks of 2048, lane L of a wave holding p[b + 32 L .. b + 32 L + 31] (+0.0 past count,
 // which changes no sum). (1) Every chunk's sum in any order, and from them the binade the running sum probably has
 // at each chunk's start. (2) Each wave takes every waves-th chunk at its guessed binade (lane_r, then lane_t and the
-// lanes' sums for both parities of the sum before it). (3) Wave 0 goes through the chunks in order: where the sum
-// before a chunk has the guessed binade and the chunk's sum of r keeps it below the next power of two, the chunk's end
-// and checkpoints follow from (2) exactly; any other chunk is taken by chunk_exact. With cp, cp[i / CP_BLOCK] = the
-// sum before value i for every multiple i of CP_BLOCK below count. With given, steps (1) and (2) are its guesses
-// (vocab_guess_kernel's). Wave 0 returns the total. (p: 16-byte aligned,
-// count >= 1, whole chunks: +0.0 from count up to sample_probs_floats(count).)
+// lanes' sums for both parities of the sum before it). (3) Wave 0 goes through the chunks in order: a run of chunks
+// whose sums before them have the guessed binade and whose sums of r keep it below the next power of two is taken at
+// once, a lane a chunk (their ends and checkpoints follow from (2) exactly); the chunk that ends such a run is walked
+// from its lanes at two binades where given has them (chunk_walk), else taken by chunk_exact. With cp,
+// cp[i / CP_BLOCK] = the sum before value i for every multiple i of CP_BLOCK below count. With given, steps (1) and
+// (2) are its guesses and the first chunk its exact end and checkpoints (vocab_guess_kernel's; copied: the guesses
+// already in sh). Wave 0 returns the total. (p: 16-byte aligned, count >= 1, whole chunks: +0.0 from count up to
+// sample_probs_floats(count).)
 __device__ __forceinline__ double sum_block(const float *p, int count, double *cp, SumShared &sh,
                                             const DrawParts *given = nullptr, bool copied = false) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
