@@ -34,7 +34,7 @@ def test_penalize_matches_the_oracle():
         assert np.array_equal(bits(gl.penalize(logits, tokens, penalty)), bits(ol.penalize(logits, tokens, penalty)))
 
 
-@pytest.mark.parametrize("n, scale", [(200, 3.0), (320, 1.0), (32000, 6.0), (128256, 8.0)])
+@pytest.mark.parametrize("n, scale", [(200, 3.0), (320, 1.0), (32000, 6.0), (128256, 8.0), (262144, 4.0)])
 @pytest.mark.parametrize("temperature, topp", [(0.7, 0.9), (1.0, 1.0), (0.3, 0.5), (1.3, 0.95), (0.8, 0.0)])
 def test_sample_matches_the_oracle(n, scale, temperature, topp):
     rng = np.random.default_rng(n + int(10 * temperature) + int(100 * topp))
